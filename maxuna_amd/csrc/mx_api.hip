@@ -1,0 +1,557 @@
+// C-ABI entry points: host-side validation (every check happens before any
+// launch, as dispatch.rs:812-847 does), then the launchers.  No exception or
+// HIP error escapes as anything but a status code + thread-local text.
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "mx_launch.h"
+
+namespace mx {
+
+static thread_local char g_err[512] = "";
+
+mx_status fail(mx_status code, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+mx_status hip_check(hipError_t e, const char *what) {
+    if (e == hipSuccess) return MX_OK;
+    return fail(MX_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+static bool supported(int dt) { return dt == kQ4_K || dt == kQ6_K || dt == kQ8_0; }
+static bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+static const char *dt_name(int dt) {
+    return dt == kQ4_K ? "Q4_K" : dt == kQ6_K ? "Q6_K" : dt == kQ8_0 ? "Q8_0" : "unsupported";
+}
+
+// Validates a stack and returns its geometry.
+struct StackGeom {
+    const uint8_t *w;
+    int64_t row_bytes, expert_bytes;
+};
+
+static mx_status check_stack(const mx_expert_stack *st, const char *what, StackGeom &g) {
+    if (!st) return fail(MX_ERR_NULL, "%s: stack is NULL", what);
+    if (!st->data) return fail(MX_ERR_NULL, "%s: stack has no device buffer", what);
+    if (!supported(st->dtype))
+        return fail(MX_ERR_DTYPE, "%s: no kernel for ggml type %d", what, (int)st->dtype);
+    if (st->n_expert <= 0 || st->n_out <= 0 || st->k <= 0)
+        return fail(MX_ERR_SHAPE, "%s: empty stack [%lld, %lld, %lld]", what, (long long)st->n_expert,
+                    (long long)st->n_out, (long long)st->k);
+    const int bs = block_size(st->dtype);
+    if (st->k % bs)
+        return fail(MX_ERR_BLOCK, "%s: k (%lld) is not a multiple of %s block size %d", what,
+                    (long long)st->k, dt_name(st->dtype), bs);
+    if (st->n_expert > 32767 || st->n_out > (1 << 30) || st->k > (1 << 24))
+        return fail(MX_ERR_OVERFLOW, "%s: stack dimensions exceed the kernels' index range", what);
+    g.w = static_cast<const uint8_t *>(st->data) + st->base_off;
+    g.row_bytes = st->k / bs * type_size(st->dtype);
+    g.expert_bytes = st->n_out * g.row_bytes;
+    // Q4_K rows are read with 16-byte loads.  Q6_K/Q8_0 blocks are 2-byte aligned
+    // inside a row; they are read with 16-bit loads or with 4-byte-aligned dwords
+    // that each contain at least one byte of the block (never a byte of an
+    // unmapped page), so 2-byte alignment suffices.
+    const size_t need = st->dtype == kQ4_K ? 16 : 2;
+    if (!aligned(g.w, need))
+        return fail(MX_ERR_ALIGN, "%s: first block (data + base_off) must be %zu-byte aligned", what, need);
+    return MX_OK;
+}
+
+static mx_status check_f32(const float *p, const char *what) {
+    if (!p) return fail(MX_ERR_NULL, "%s is NULL", what);
+    if (!aligned(p, 16)) return fail(MX_ERR_ALIGN, "%s must be 16-byte aligned", what);
+    return MX_OK;
+}
+
+// Shapes shared by mv_id / mm_id (dispatch.rs:812-847).
+static mx_status check_id_call(const mx_expert_stack *st, const float *x, int64_t t,
+                               int64_t x_per_row, int64_t k, const uint32_t *ids, int64_t ids_t,
+                               int64_t top_k, float *dst, StackGeom &g) {
+    MX_TRY(check_stack(st, "expert stack", g));
+    if (t < 0 || top_k < 0) return fail(MX_ERR_SHAPE, "negative t (%lld) or top_k (%lld)", (long long)t, (long long)top_k);
+    if (k != st->k)
+        return fail(MX_ERR_SHAPE, "x k (%lld) does not match expert stack k (%lld)", (long long)k, (long long)st->k);
+    if (ids_t != t)
+        return fail(MX_ERR_SHAPE, "ids t (%lld) does not match x t (%lld)", (long long)ids_t, (long long)t);
+    if (top_k == 0 || top_k > 64) return fail(MX_ERR_TOPK, "top_k (%lld) must be in 1..64", (long long)top_k);
+    if (x_per_row != 1 && x_per_row != top_k)
+        return fail(MX_ERR_XPR, "x_per_row (%lld) must be 1 (shared row) or top_k (%lld) (per-slot row)",
+                    (long long)x_per_row, (long long)top_k);
+    if ((k % 4) != 0) return fail(MX_ERR_SHAPE, "k must be a multiple of 4");
+    if (t * top_k > (int64_t)1 << 22 || t * top_k * st->n_out > INT64_C(1) << 40)
+        return fail(MX_ERR_OVERFLOW, "t*top_k=%lld exceeds the kernels' index range", (long long)(t * top_k));
+    if (t == 0) return MX_OK;
+    MX_TRY(check_f32(x, "x"));
+    MX_TRY(check_f32(dst, "dst"));
+    if (!ids) return fail(MX_ERR_NULL, "ids is NULL");
+    return MX_OK;
+}
+
+}  // namespace mx
+
+using namespace mx;
+
+extern "C" {
+
+const char *mx_last_error(void) { return g_err; }
+const char *mx_version(void) { return "maxuna_moe 0.1.0 gfx950"; }
+int32_t mx_block_size(int32_t dtype) { return supported(dtype) ? block_size(dtype) : -1; }
+int32_t mx_type_size(int32_t dtype) { return supported(dtype) ? type_size(dtype) : -1; }
+
+mx_status mx_dequantize(int32_t dtype, const void *blocks, int64_t n, float *out, mx_stream_t stream) {
+    if (!supported(dtype)) return fail(MX_ERR_DTYPE, "dequantize: no kernel for ggml type %d", (int)dtype);
+    if (n < 0) return fail(MX_ERR_SHAPE, "dequantize: negative n");
+    if (n % block_size(dtype))
+        return fail(MX_ERR_BLOCK, "dequantize: n (%lld) is not a multiple of %s block size %d", (long long)n,
+                    dt_name(dtype), block_size(dtype));
+    if (n == 0) return MX_OK;
+    if (!blocks) return fail(MX_ERR_NULL, "dequantize: blocks is NULL");
+    MX_TRY(check_f32(out, "dequantize: out"));
+    if (!aligned(blocks, dtype == kQ4_K ? 16 : 2))
+        return fail(MX_ERR_ALIGN, "dequantize: blocks misaligned");
+    return launch_dequantize(dtype, static_cast<const uint8_t *>(blocks), n, out, (hipStream_t)stream);
+}
+
+mx_status mx_mul_mv_id(const mx_expert_stack *stack, const float *x, int64_t t, int64_t x_per_row,
+                       int64_t k, const uint32_t *ids, int64_t ids_t, int64_t top_k, float *dst,
+                       mx_stream_t stream) {
+    StackGeom g;
+    MX_TRY(check_id_call(stack, x, t, x_per_row, k, ids, ids_t, top_k, dst, g));
+    if (t == 0) return MX_OK;
+    MvArgs a{g.w, g.expert_bytes, g.row_bytes, (int)stack->n_expert, (int)stack->n_out, (int)stack->k,
+             x, (int)x_per_row, ids, (int)t, (int)top_k, dst};
+    return launch_mul_mv_id(stack->dtype, a, (hipStream_t)stream);
+}
+
+mx_status mx_mul_mv(const void *w, int32_t dtype, int64_t n_out, int64_t k, const float *x, int64_t t,
+                    float *dst, mx_stream_t stream) {
+    mx_expert_stack st{w, 0, dtype, 0, 1, n_out, k};
+    StackGeom g;
+    MX_TRY(check_stack(&st, "mul_mv weight", g));
+    if (t < 0) return fail(MX_ERR_SHAPE, "mul_mv: negative t");
+    if (t == 0) return MX_OK;
+    MX_TRY(check_f32(x, "x"));
+    MX_TRY(check_f32(dst, "dst"));
+    if (t > (1 << 22)) return fail(MX_ERR_OVERFLOW, "mul_mv: t too large");
+    MvArgs a{g.w, g.expert_bytes, g.row_bytes, 1, (int)n_out, (int)k, x, 1, nullptr, (int)t, 1, dst};
+    return launch_mul_mv_id(dtype, a, (hipStream_t)stream);
+}
+
+size_t mx_map0_scratch_bytes(int64_t n_expert, int64_t t, int64_t top_k) {
+    if (n_expert <= 0 || t < 0 || top_k <= 0) return 0;
+    return map0_bytes((int)n_expert, (int)t, (int)top_k);
+}
+
+static mx_status check_map_geom(int64_t n_expert, int64_t t, int64_t top_k) {
+    if (n_expert <= 0 || n_expert > 16384) return fail(MX_ERR_SHAPE, "map0: n_expert (%lld) must be in 1..16384", (long long)n_expert);
+    if (t < 0) return fail(MX_ERR_SHAPE, "map0: negative t");
+    if (top_k <= 0 || top_k > 64 || top_k > n_expert) return fail(MX_ERR_TOPK, "map0: top_k (%lld) must be in 1..min(64, n_expert)", (long long)top_k);
+    if (t * top_k > (int64_t)1 << 22) return fail(MX_ERR_OVERFLOW, "map0: t*top_k exceeds 4M pairs");
+    return MX_OK;
+}
+
+mx_status mx_prepare_map0(int64_t n_expert, const uint32_t *ids, int64_t t, int64_t top_k, void *scratch,
+                          size_t scratch_bytes, mx_stream_t stream) {
+    MX_TRY(check_map_geom(n_expert, t, top_k));
+    if (!scratch) return fail(MX_ERR_NULL, "map0: scratch is NULL");
+    if (!aligned(scratch, 4)) return fail(MX_ERR_ALIGN, "map0: scratch must be 4-byte aligned");
+    const size_t need = map0_bytes((int)n_expert, (int)t, (int)top_k);
+    if (scratch_bytes < need)
+        return fail(MX_ERR_SCRATCH, "map0: scratch of %zu bytes, need %zu", scratch_bytes, need);
+    if (t > 0 && !ids) return fail(MX_ERR_NULL, "map0: ids is NULL");
+    return launch_map0(ids, (int)t, (int)top_k, (int)n_expert, static_cast<int32_t *>(scratch),
+                       (hipStream_t)stream);
+}
+
+mx_status mx_mul_mm_id_shared(const mx_expert_stack *stack, const float *x, int64_t t, int64_t x_per_row,
+                              int64_t k, const uint32_t *ids, int64_t ids_t, int64_t top_k,
+                              const mx_map0 *map, float *dst, mx_stream_t stream) {
+    StackGeom g;
+    MX_TRY(check_id_call(stack, x, t, x_per_row, k, ids, ids_t, top_k, dst, g));
+    if (!map || !map->buffer) return fail(MX_ERR_NULL, "mul_mm_id_shared: map0 scratch is NULL");
+    // dispatch.rs:886-896: the producer's geometry must match this projection
+    if (map->n_expert != stack->n_expert || map->t != t || map->top_k != top_k)
+        return fail(MX_ERR_SCRATCH,
+                    "shared map0 scratch geometry (n_expert=%lld, t=%lld, top_k=%lld) does not match this "
+                    "projection (n_expert=%lld, t=%lld, top_k=%lld)",
+                    (long long)map->n_expert, (long long)map->t, (long long)map->top_k,
+                    (long long)stack->n_expert, (long long)t, (long long)top_k);
+    if (map->bytes < map0_bytes((int)map->n_expert, (int)t, (int)top_k))
+        return fail(MX_ERR_SCRATCH, "shared map0 scratch too small");
+    if (t == 0) return MX_OK;
+    MmArgs a{g.w, g.expert_bytes, g.row_bytes, (int)stack->n_expert, (int)stack->n_out, (int)stack->k,
+             x, (int)x_per_row, (int)t, (int)top_k, static_cast<const int32_t *>(map->buffer), dst};
+    return launch_mul_mm_id(stack->dtype, a, (hipStream_t)stream);
+}
+
+size_t mx_mul_mm_id_workspace_bytes(int64_t n_expert, int64_t t, int64_t top_k, int64_t x_per_row, int64_t k) {
+    (void)x_per_row;
+    (void)k;
+    return mx_map0_scratch_bytes(n_expert, t, top_k);
+}
+
+mx_status mx_mul_mm_id(const mx_expert_stack *stack, const float *x, int64_t t, int64_t x_per_row, int64_t k,
+                       const uint32_t *ids, int64_t ids_t, int64_t top_k, void *workspace,
+                       size_t workspace_bytes, float *dst, mx_stream_t stream) {
+    StackGeom g;
+    MX_TRY(check_id_call(stack, x, t, x_per_row, k, ids, ids_t, top_k, dst, g));
+    MX_TRY(check_map_geom(stack->n_expert, t, top_k));
+    if (t == 0) return MX_OK;
+    MX_TRY(mx_prepare_map0(stack->n_expert, ids, t, top_k, workspace, workspace_bytes, stream));
+    mx_map0 m{workspace, workspace_bytes, stack->n_expert, t, top_k};
+    return mx_mul_mm_id_shared(stack, x, t, x_per_row, k, ids, ids_t, top_k, &m, dst, stream);
+}
+
+mx_status mx_silu_mul(const float *gate, const float *up, int64_t n, float *dst, mx_stream_t stream) {
+    if (n < 0) return fail(MX_ERR_SHAPE, "silu_mul: negative n");
+    if (n == 0) return MX_OK;
+    if (!gate || !up || !dst) return fail(MX_ERR_NULL, "silu_mul: NULL operand");
+    return launch_silu_mul(gate, up, n, dst, (hipStream_t)stream);
+}
+
+mx_status mx_combine(const float *down, const float *col_l2, const float *w, int64_t seq, int64_t top_k,
+                     int64_t n_out, float *dst, mx_stream_t stream) {
+    if (seq < 0 || top_k <= 0 || n_out <= 0)
+        return fail(MX_ERR_SHAPE, "combine: bad shape seq=%lld top_k=%lld n_out=%lld", (long long)seq,
+                    (long long)top_k, (long long)n_out);
+    // combine.rs / dispatch.rs:1453-1462: index math must fit i32
+    if (seq * top_k * n_out > INT32_MAX)
+        return fail(MX_ERR_OVERFLOW, "combine index math overflows i32: seq*top_k*n_out = %lld",
+                    (long long)(seq * top_k * n_out));
+    if (seq == 0) return MX_OK;
+    if (!down || !w || !dst) return fail(MX_ERR_NULL, "combine: NULL operand");
+    return launch_combine(down, col_l2, w, (int)seq, (int)top_k, (int)n_out, dst, (hipStream_t)stream);
+}
+
+mx_status mx_rms_norm(const float *x, const float *alpha, int64_t rows, int64_t dim, float eps, float *dst,
+                      mx_stream_t stream) {
+    if (rows < 0 || dim <= 0 || rows > INT32_MAX) return fail(MX_ERR_SHAPE, "rms_norm: bad shape");
+    if (rows == 0) return MX_OK;
+    if (!x || !alpha || !dst) return fail(MX_ERR_NULL, "rms_norm: NULL operand");
+    return launch_rms_norm(x, alpha, (int)rows, (int)dim, eps, dst, (hipStream_t)stream);
+}
+
+mx_status mx_route_logits(const float *x, const float *router_t, int64_t t, int64_t hidden, int64_t n_expert,
+                          float *logits, mx_stream_t stream) {
+    if (t < 0 || hidden <= 0 || n_expert <= 0 || t > INT32_MAX / 2)
+        return fail(MX_ERR_SHAPE, "route_logits: bad shape");
+    if (t == 0) return MX_OK;
+    if (!x || !router_t || !logits) return fail(MX_ERR_NULL, "route_logits: NULL operand");
+    return launch_route_logits(x, router_t, (int)t, (int)hidden, (int)n_expert, logits, (hipStream_t)stream);
+}
+
+static mx_status check_route(int64_t t, int64_t n_expert, int64_t top_k) {
+    if (t < 0) return fail(MX_ERR_SHAPE, "route: negative t");
+    if (n_expert <= 0 || n_expert > 1024) return fail(MX_ERR_SHAPE, "route: n_expert (%lld) must be in 1..1024", (long long)n_expert);
+    if (top_k <= 0 || top_k > 32 || top_k > n_expert)
+        return fail(MX_ERR_TOPK, "route: top_k (%lld) must be in 1..min(32, n_expert)", (long long)top_k);
+    return MX_OK;
+}
+
+mx_status mx_route_from_logits(const float *logits, const float *bias, int64_t t, int64_t n_expert, int64_t top_k,
+                               double scale, int32_t norm, uint32_t *ids, float *w, mx_stream_t stream) {
+    MX_TRY(check_route(t, n_expert, top_k));
+    if (t == 0) return MX_OK;
+    if (!logits || !bias || !ids || !w) return fail(MX_ERR_NULL, "route_from_logits: NULL operand");
+    const int apply = (scale != 0.0 && scale != 1.0) ? 1 : 0;
+    return launch_route_select(logits, bias, (int)t, (int)n_expert, (int)top_k, (float)scale, apply, norm ? 1 : 0,
+                               ids, w, (hipStream_t)stream);
+}
+
+}  // extern "C"
+
+// ---- whole MoE block --------------------------------------------------------------------
+namespace {
+
+constexpr int64_t kDefaultMmMinSeq = 32;  // ops/mod.rs:31 MM_ID_MIN_SEQ
+constexpr int64_t kFusedRouterMaxT = 16;
+
+struct Ws {
+    uint8_t *base;
+    size_t off = 0;
+    explicit Ws(void *b) : base(static_cast<uint8_t *>(b)) {}
+    template <class T> T *take(size_t count) {
+        off = (off + 255) & ~size_t(255);
+        T *p = base ? reinterpret_cast<T *>(base + off) : nullptr;
+        off += count * sizeof(T);
+        return p;
+    }
+};
+
+struct Plan {
+    bool mm, fused_router, has_shared;
+    int64_t min_seq;
+};
+
+Plan plan_for(const mx_moe_layer *L, int64_t t) {
+    Plan p;
+    p.min_seq = L->mm_min_seq > 0 ? L->mm_min_seq : kDefaultMmMinSeq;
+    p.mm = L->mm_min_seq >= 0 && t >= p.min_seq;  // < 0: never (LAGUNA_NO_MM_ID)
+    p.fused_router = !p.mm && t <= kFusedRouterMaxT;
+    p.has_shared = L->shared_gate.data != nullptr;
+    return p;
+}
+
+// Carves the workspace; with base == nullptr it only measures.
+struct Layout {
+    uint8_t *route_ws = nullptr;
+    float *x_normed = nullptr, *logits = nullptr, *w = nullptr, *act = nullptr;
+    uint32_t *ids = nullptr, *zero_ids = nullptr;
+    int32_t *map = nullptr, *map_sh = nullptr;
+    float *gate = nullptr, *up = nullptr, *down = nullptr, *routed = nullptr;
+    float *sh_g = nullptr, *sh_u = nullptr, *sh_out = nullptr;
+    size_t bytes = 0;
+};
+
+Layout carve(const mx_moe_layer *L, int64_t t, const Plan &p, void *base) {
+    Ws ws(base);
+    Layout o;
+    const int64_t H = L->hidden, FF = L->expert_ff, K = L->top_k, E = L->gate.n_expert;
+    if (L->rms_alpha) o.x_normed = ws.take<float>(t * H);
+    o.ids = ws.take<uint32_t>(t * K);
+    o.w = ws.take<float>(t * K);
+    if (p.fused_router) {
+        o.route_ws = ws.take<uint8_t>(route_fused_ws_bytes((int)t, (int)H, (int)E));
+    } else {
+        o.logits = ws.take<float>(t * E);
+    }
+    if (!p.mm) {
+        o.act = ws.take<float>(t * (K + (p.has_shared ? 1 : 0)) * FF);
+    } else {
+        o.map = ws.take<int32_t>(map0_bytes((int)E, (int)t, (int)K) / 4);
+        o.gate = ws.take<float>(t * K * FF);
+        o.up = ws.take<float>(t * K * FF);
+        o.down = ws.take<float>(t * K * H);
+        o.routed = ws.take<float>(t * H);
+        if (p.has_shared) {
+            o.zero_ids = ws.take<uint32_t>(t);
+            o.map_sh = ws.take<int32_t>(map0_bytes(1, (int)t, 1) / 4);
+            o.sh_g = ws.take<float>(t * FF);
+            o.sh_u = ws.take<float>(t * FF);
+            o.sh_out = ws.take<float>(t * H);
+        }
+    }
+    o.bytes = ws.off + 256;
+    return o;
+}
+
+__global__ void k_fill_u32(uint32_t *p, int64_t n, uint32_t v) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
+mx_status check_layer(const mx_moe_layer *L, int64_t t, StackGeom &gg, StackGeom &gu, StackGeom &gd,
+                      StackGeom &sg, StackGeom &su, StackGeom &sd) {
+    if (!L) return fail(MX_ERR_NULL, "moe: layer is NULL");
+    if (t < 0) return fail(MX_ERR_SHAPE, "moe: negative t");
+    MX_TRY(check_stack(&L->gate, "ffn_gate_exps", gg));
+    MX_TRY(check_stack(&L->up, "ffn_up_exps", gu));
+    MX_TRY(check_stack(&L->down, "ffn_down_exps", gd));
+    const int64_t H = L->hidden, FF = L->expert_ff, E = L->gate.n_expert;
+    // moe.rs:206-216: the three stacks must agree on n_expert
+    if (L->up.n_expert != E || L->down.n_expert != E)
+        return fail(MX_ERR_SHAPE, "MoE expert stacks disagree on n_expert: gate=%lld, up=%lld, down=%lld",
+                    (long long)E, (long long)L->up.n_expert, (long long)L->down.n_expert);
+    if (L->gate.n_out != FF || L->up.n_out != FF || L->gate.k != H || L->up.k != H || L->down.n_out != H ||
+        L->down.k != FF)
+        return fail(MX_ERR_SHAPE, "moe: expert stacks do not match hidden=%lld expert_ff=%lld", (long long)H,
+                    (long long)FF);
+    if (L->gate.dtype != L->up.dtype)
+        return fail(MX_ERR_DTYPE, "moe: gate (%s) and up (%s) experts must share a quant type",
+                    dt_name(L->gate.dtype), dt_name(L->up.dtype));
+    MX_TRY(check_route(t, E, L->top_k));
+    if (!L->router_t || !L->exp_probs_b) return fail(MX_ERR_NULL, "moe: router or exp_probs_b is NULL");
+    if (L->shared_gate.data) {
+        MX_TRY(check_stack(&L->shared_gate, "ffn_gate_shexp", sg));
+        MX_TRY(check_stack(&L->shared_up, "ffn_up_shexp", su));
+        MX_TRY(check_stack(&L->shared_down, "ffn_down_shexp", sd));
+        if (L->shared_gate.n_expert != 1 || L->shared_up.n_expert != 1 || L->shared_down.n_expert != 1)
+            return fail(MX_ERR_SHAPE, "moe: shared expert stacks must have n_expert == 1");
+        if (L->shared_gate.n_out != FF || L->shared_up.n_out != FF || L->shared_gate.k != H ||
+            L->shared_up.k != H || L->shared_down.n_out != H || L->shared_down.k != FF)
+            return fail(MX_ERR_SHAPE, "moe: shared expert must be [%lld x %lld] / [%lld x %lld]", (long long)FF,
+                        (long long)H, (long long)H, (long long)FF);
+        if (L->shared_gate.dtype != L->shared_up.dtype)
+            return fail(MX_ERR_DTYPE, "moe: shared gate and up must share a quant type");
+    }
+    if (H % 4 || FF % 4) return fail(MX_ERR_SHAPE, "moe: hidden and expert_ff must be multiples of 4");
+    if (t * L->top_k > (int64_t)1 << 22) return fail(MX_ERR_OVERFLOW, "moe: t*top_k exceeds 4M pairs");
+    return MX_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t mx_moe_workspace_bytes(const mx_moe_layer *layer, int64_t t) {
+    if (!layer || t < 0) return 0;
+    const Plan p = plan_for(layer, t);
+    return carve(layer, t, p, nullptr).bytes;
+}
+
+}  // extern "C"
+
+namespace {
+// Records a HIP event after each stage of a forward (profiling variant only).
+struct StageTimer {
+    hipEvent_t ev[17];
+    int n = 0;
+    mx_status mark(hipStream_t s) {
+        if (n >= 17) return fail(MX_ERR_SHAPE, "too many stages");
+        MX_HIP(hipEventCreate(&ev[n]));
+        MX_HIP(hipEventRecord(ev[n], s));
+        n++;
+        return MX_OK;
+    }
+    ~StageTimer() {
+        for (int i = 0; i < n; i++) (void)hipEventDestroy(ev[i]);
+    }
+};
+#define MX_STAGE() \
+    do {           \
+        if (tm) MX_TRY(tm->mark(s)); \
+    } while (0)
+
+mx_status moe_forward_impl(const mx_moe_layer *L, const float *x, int64_t t, const float *residual, float *out,
+                           uint32_t *ids_out, float *w_out, void *workspace, size_t workspace_bytes,
+                           hipStream_t s, StageTimer *tm) {
+    StackGeom gg, gu, gd, sg{}, su{}, sd{};
+    MX_TRY(check_layer(L, t, gg, gu, gd, sg, su, sd));
+    if (t == 0) return MX_OK;
+    MX_TRY(check_f32(x, "x"));
+    MX_TRY(check_f32(out, "out"));
+    if (residual) MX_TRY(check_f32(residual, "residual"));
+    if (!workspace) return fail(MX_ERR_NULL, "moe: workspace is NULL");
+    const Plan p = plan_for(L, t);
+    const Layout o = carve(L, t, p, workspace);
+    if (workspace_bytes < o.bytes)
+        return fail(MX_ERR_SCRATCH, "moe: workspace of %zu bytes, need %zu", workspace_bytes, o.bytes);
+    MX_STAGE();
+    const int64_t H = L->hidden, FF = L->expert_ff, K = L->top_k, E = L->gate.n_expert;
+    const float scale = (float)L->weights_scale;
+    const int apply = (L->weights_scale != 0.0 && L->weights_scale != 1.0) ? 1 : 0;
+    uint32_t *ids = ids_out ? ids_out : o.ids;
+    float *w = w_out ? w_out : o.w;
+    const float *xin = x;
+
+    // routing (+ the RMSNorm of the FFN half when requested)
+    if (p.fused_router) {
+        MX_TRY(launch_route_fused(x, L->rms_alpha, L->rms_eps, o.x_normed, L->router_t, L->exp_probs_b, (int)t,
+                                  (int)H, (int)E, (int)K, scale, apply, L->weights_norm, ids, w, o.route_ws, s));
+        if (L->rms_alpha) xin = o.x_normed;
+    } else {
+        if (L->rms_alpha) {
+            MX_TRY(launch_rms_norm(x, L->rms_alpha, (int)t, (int)H, L->rms_eps, o.x_normed, s));
+            xin = o.x_normed;
+        }
+        MX_TRY(launch_route_logits(xin, L->router_t, (int)t, (int)H, (int)E, o.logits, s));
+        MX_TRY(launch_route_select(o.logits, L->exp_probs_b, (int)t, (int)E, (int)K, scale, apply,
+                                   L->weights_norm, ids, w, s));
+    }
+    MX_STAGE();
+
+    if (!p.mm) {
+        DecodeGateUpArgs ga{gg.w, gu.w, gg.expert_bytes, gg.row_bytes, sg.w, su.w, sg.row_bytes,
+                            (int)E, (int)FF, (int)H, xin, ids, (int)t, (int)K, o.act};
+        MX_TRY(launch_decode_gate_up(L->gate.dtype, L->shared_gate.dtype, ga, s));
+        MX_STAGE();
+        DecodeDownArgs da{gd.w, gd.expert_bytes, gd.row_bytes, sd.w, sd.row_bytes, (int)E, (int)FF, (int)H,
+                          o.act, ids, w, residual, (int)t, (int)K, out};
+        MX_TRY(launch_decode_down(L->down.dtype, L->shared_down.dtype, da, s));
+        MX_STAGE();
+        return MX_OK;
+    }
+
+    // prefill / verify: bucket once, three grouped GEMMs (moe.rs:242-323)
+    MX_TRY(launch_map0(ids, (int)t, (int)K, (int)E, o.map, s));
+    MX_STAGE();
+    MmArgs ma{gg.w, gg.expert_bytes, gg.row_bytes, (int)E, (int)FF, (int)H, xin, 1, (int)t, (int)K, o.map, o.gate};
+    MX_TRY(launch_mul_mm_id(L->gate.dtype, ma, s));
+    MX_STAGE();
+    ma.w = gu.w; ma.dst = o.up;
+    MX_TRY(launch_mul_mm_id(L->up.dtype, ma, s));
+    MX_STAGE();
+    MX_TRY(launch_silu_mul(o.gate, o.up, t * K * FF, o.gate, s));
+    MX_STAGE();
+    MmArgs md{gd.w, gd.expert_bytes, gd.row_bytes, (int)E, (int)H, (int)FF, o.gate, (int)K, (int)t, (int)K,
+              o.map, o.down};
+    MX_TRY(launch_mul_mm_id(L->down.dtype, md, s));
+    MX_STAGE();
+    float *routed = (p.has_shared || residual) ? o.routed : out;
+    MX_TRY(launch_combine(o.down, nullptr, w, (int)t, (int)K, (int)H, routed, s));
+    MX_STAGE();
+    if (!p.has_shared) {
+        if (residual) MX_TRY(launch_add3(residual, routed, nullptr, t * H, out, s));
+        MX_STAGE();
+        return MX_OK;
+    }
+    // the shared expert is a one-expert grouped GEMM over every token
+    hipLaunchKernelGGL(k_fill_u32, dim3((unsigned)((t + 255) / 256)), dim3(256), 0, s, o.zero_ids, t, 0u);
+    MX_LAUNCH("k_fill_u32");
+    MX_TRY(launch_map0(o.zero_ids, (int)t, 1, 1, o.map_sh, s));
+    MmArgs sa{sg.w, sg.expert_bytes, sg.row_bytes, 1, (int)FF, (int)H, xin, 1, (int)t, 1, o.map_sh, o.sh_g};
+    MX_TRY(launch_mul_mm_id(L->shared_gate.dtype, sa, s));
+    sa.w = su.w;
+    sa.dst = o.sh_u;
+    MX_TRY(launch_mul_mm_id(L->shared_up.dtype, sa, s));
+    MX_TRY(launch_silu_mul(o.sh_g, o.sh_u, t * FF, o.sh_g, s));
+    MmArgs sdn{sd.w, sd.expert_bytes, sd.row_bytes, 1, (int)H, (int)FF, o.sh_g, 1, (int)t, 1, o.map_sh, o.sh_out};
+    MX_TRY(launch_mul_mm_id(L->shared_down.dtype, sdn, s));
+    MX_STAGE();
+    // out = residual + (routed + shared)   (moe.rs:78, model.rs:351)
+    MX_TRY(launch_add3(routed, o.sh_out, residual, t * H, out, s));
+    MX_STAGE();
+    return MX_OK;
+}
+}  // namespace
+
+extern "C" {
+
+mx_status mx_moe_forward(const mx_moe_layer *L, const float *x, int64_t t, const float *residual, float *out,
+                         uint32_t *ids_out, float *w_out, void *workspace, size_t workspace_bytes,
+                         mx_stream_t stream) {
+    return moe_forward_impl(L, x, t, residual, out, ids_out, w_out, workspace, workspace_bytes,
+                            (hipStream_t)stream, nullptr);
+}
+
+mx_status mx_moe_forward_profiled(const mx_moe_layer *L, const float *x, int64_t t, const float *residual,
+                                  float *out, uint32_t *ids_out, float *w_out, void *workspace,
+                                  size_t workspace_bytes, mx_stream_t stream, float *stage_ms,
+                                  int32_t max_stages, int32_t *n_stages) {
+    if (!stage_ms || !n_stages) return fail(MX_ERR_NULL, "moe_forward_profiled: NULL stage output");
+    StageTimer tm;
+    MX_TRY(moe_forward_impl(L, x, t, residual, out, ids_out, w_out, workspace, workspace_bytes,
+                            (hipStream_t)stream, &tm));
+    if (tm.n == 0) {
+        *n_stages = 0;
+        return MX_OK;
+    }
+    MX_HIP(hipEventSynchronize(tm.ev[tm.n - 1]));
+    int k = 0;
+    for (int i = 1; i < tm.n && k < max_stages; i++, k++)
+        MX_HIP(hipEventElapsedTime(&stage_ms[k], tm.ev[i - 1], tm.ev[i]));
+    *n_stages = k;
+    return MX_OK;
+}
+
+uint64_t mx_tensor_key(uint64_t seed, uint32_t layer, uint32_t tensor_id) {
+    return tensor_key(seed, layer, tensor_id);
+}
+
+mx_status mx_synth_blocks(int32_t dtype, uint64_t key, void *dst, int64_t nbytes, mx_stream_t stream) {
+    if (!supported(dtype)) return fail(MX_ERR_DTYPE, "synth: unsupported ggml type %d", (int)dtype);
+    if (nbytes < 0 || nbytes % type_size(dtype))
+        return fail(MX_ERR_BLOCK, "synth: nbytes must be a multiple of the %s block size", dt_name(dtype));
+    if (nbytes == 0) return MX_OK;
+    if (!dst) return fail(MX_ERR_NULL, "synth: dst is NULL");
+    if (!aligned(dst, 2)) return fail(MX_ERR_ALIGN, "synth: dst must be 2-byte aligned");
+    return launch_synth(dtype, key, static_cast<uint8_t *>(dst), nbytes, (hipStream_t)stream);
+}
+
+}  // extern "C"

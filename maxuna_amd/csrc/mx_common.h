@@ -1,0 +1,98 @@
+// Shared device/host helpers for the maxuna_moe gfx950 kernels.
+//
+// Block layouts are the public GGUF/ggml formats (reference: mv.metal:55-80):
+//   Q4_K 144 B: f16 d | f16 dmin | u8 scales[12] | u8 qs[128]
+//   Q6_K 210 B: u8 ql[128] | u8 qh[64] | i8 scales[16] | f16 d
+//   Q8_0  34 B: f16 d | i8 qs[32]
+// Q6_K and Q8_0 blocks are only 2-byte aligned inside a row, so every load of
+// their bytes here is either a 16-bit load or a 4-byte-aligned dword load that
+// contains at least one requested byte (see load8_a2).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#include "../../include/maxuna_moe.h"
+
+namespace mx {
+
+constexpr int kQ8_0 = MX_Q8_0;
+constexpr int kQ4_K = MX_Q4_K;
+constexpr int kQ6_K = MX_Q6_K;
+constexpr int QK_K = 256;
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef float float16_t __attribute__((ext_vector_type(16)));
+
+__host__ __device__ constexpr int block_size(int dt) {
+    return dt == kQ8_0 ? 32 : (dt == kQ4_K || dt == kQ6_K) ? 256 : -1;
+}
+__host__ __device__ constexpr int type_size(int dt) {
+    return dt == kQ8_0 ? 34 : dt == kQ4_K ? 144 : dt == kQ6_K ? 210 : -1;
+}
+
+__device__ __forceinline__ float h2f(uint16_t h) {
+    return (float)__builtin_bit_cast(_Float16, h);
+}
+
+__device__ __forceinline__ uint16_t ld_u16(const uint8_t *p) {
+    return *reinterpret_cast<const uint16_t *>(p);
+}
+__device__ __forceinline__ uint32_t ld_u32(const uint8_t *p) {
+    return *reinterpret_cast<const uint32_t *>(p);
+}
+
+// 8 bytes from a 2-byte-aligned address p, using only 4-byte-aligned dword
+// loads, each of which contains at least one of the 8 requested bytes (so it
+// never touches a page the requested bytes do not).
+__device__ __forceinline__ uint2 load8_a2(const uint8_t *p) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    const uint32_t *q = reinterpret_cast<const uint32_t *>(a & ~uintptr_t(3));
+    if ((a & 2) == 0) {
+        return make_uint2(q[0], q[1]);
+    }
+    const uint32_t d0 = q[0], d1 = q[1], d2 = q[2];
+    return make_uint2(__builtin_amdgcn_alignbit(d1, d0, 16), __builtin_amdgcn_alignbit(d2, d1, 16));
+}
+
+// Q4_K 6-bit scale/min of sub-block j (0..7) from the 12 scale bytes, held as
+// three little-endian dwords s0 (bytes 0-3), s1 (4-7), s2 (8-11).
+// Restates get_scale_min_k4 (mm_id.metal:89-92).
+__device__ __forceinline__ void q4k_scale_min(int j, uint32_t s0, uint32_t s1, uint32_t s2,
+                                              uint32_t &sc, uint32_t &m) {
+    if (j < 4) {
+        sc = (s0 >> (8 * j)) & 63u;
+        m = (s1 >> (8 * j)) & 63u;
+    } else {
+        const int jj = j - 4;
+        const uint32_t b8 = (s2 >> (8 * jj)) & 0xFFu;  // scales[j+4]
+        sc = (b8 & 0xFu) | (((s0 >> (8 * jj)) >> 6 & 3u) << 4);
+        m = (b8 >> 4) | (((s1 >> (8 * jj)) >> 6 & 3u) << 4);
+    }
+}
+
+__device__ __forceinline__ float warp_sum_width(float v, int width) {
+    for (int off = width >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+}  // namespace mx
+
+// ---- host-side status plumbing (shared by every translation unit) ---------------
+namespace mx {
+mx_status fail(mx_status code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+mx_status hip_check(hipError_t e, const char *what);
+}  // namespace mx
+
+#define MX_TRY(expr)                          \
+    do {                                      \
+        mx_status _s = (expr);                \
+        if (_s != MX_OK) return _s;           \
+    } while (0)
+
+#define MX_HIP(expr) MX_TRY(::mx::hip_check((expr), #expr))
+#define MX_LAUNCH(name) MX_TRY(::mx::hip_check(hipGetLastError(), name))

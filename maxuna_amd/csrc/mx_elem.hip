@@ -1,0 +1,102 @@
+// Elementwise glue of the MoE block: SwiGLU activation, weighted combine,
+// RMSNorm.  f32 throughout, each operation rounded on its own (the library is
+// compiled with -ffp-contract=off).
+#include "mx_launch.h"
+
+namespace mx {
+
+// act = silu(g) * u, silu(g) = g / (1 + exp(-g))  (silu_mul.metal:57-72)
+__global__ void __launch_bounds__(256) k_silu_mul(const float *__restrict__ g,
+                                                  const float *__restrict__ u, int64_t n,
+                                                  float *__restrict__ dst) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float gv = g[i];
+    const float s = gv / (1.0f + expf(-gv));
+    dst[i] = s * u[i];
+}
+
+mx_status launch_silu_mul(const float *g, const float *u, int64_t n, float *dst, hipStream_t s) {
+    if (n == 0) return MX_OK;
+    hipLaunchKernelGGL(k_silu_mul, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, g, u, n, dst);
+    MX_LAUNCH("k_silu_mul");
+    return MX_OK;
+}
+
+// dst[s,c] = sum_k down[s,k,c] * w[s,k], k in slot order (combine.metal:70-97);
+// rescale form ((down * l2) * 2^-15) * w (combine.metal:102-133).
+__global__ void __launch_bounds__(256) k_combine(const float *__restrict__ down,
+                                                 const float *__restrict__ l2,
+                                                 const float *__restrict__ w, int seq, int top_k,
+                                                 int n_out, float *__restrict__ dst) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)seq * n_out) return;
+    const int s = (int)(i / n_out), c = (int)(i % n_out);
+    float acc = 0.f;
+    for (int k = 0; k < top_k; k++) {
+        float d = down[((int64_t)s * top_k + k) * n_out + c];
+        if (l2) {
+            d = d * l2[s * top_k + k];
+            d = d * (1.0f / 32768.0f);
+        }
+        acc = acc + d * w[s * top_k + k];
+    }
+    dst[i] = acc;
+}
+
+mx_status launch_combine(const float *down, const float *col_l2, const float *w, int seq,
+                         int top_k, int n_out, float *dst, hipStream_t s) {
+    const int64_t n = (int64_t)seq * n_out;
+    if (n == 0) return MX_OK;
+    hipLaunchKernelGGL(k_combine, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, down, col_l2,
+                       w, seq, top_k, n_out, dst);
+    MX_LAUNCH("k_combine");
+    return MX_OK;
+}
+
+// dst = x / sqrt(mean(x^2) + eps) * alpha, one block per row.
+__global__ void __launch_bounds__(256) k_rms_norm(const float *__restrict__ x,
+                                                  const float *__restrict__ alpha, int dim,
+                                                  float eps, float *__restrict__ dst) {
+    __shared__ float s_red[4];
+    __shared__ float s_m;
+    const int row = blockIdx.x, tid = threadIdx.x;
+    const float *xr = x + (int64_t)row * dim;
+    float ss = 0.f;
+    for (int i = tid; i < dim; i += 256) ss = __builtin_fmaf(xr[i], xr[i], ss);
+    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+    if ((tid & 63) == 0) s_red[tid >> 6] = ss;
+    __syncthreads();
+    if (tid == 0) s_m = sqrtf((((s_red[0] + s_red[1]) + s_red[2]) + s_red[3]) / (float)dim + eps);
+    __syncthreads();
+    const float m = s_m;
+    for (int i = tid; i < dim; i += 256) dst[(int64_t)row * dim + i] = xr[i] / m * alpha[i];
+}
+
+mx_status launch_rms_norm(const float *x, const float *alpha, int rows, int dim, float eps,
+                          float *dst, hipStream_t s) {
+    if (rows == 0) return MX_OK;
+    hipLaunchKernelGGL(k_rms_norm, dim3(rows), dim3(256), 0, s, x, alpha, dim, eps, dst);
+    MX_LAUNCH("k_rms_norm");
+    return MX_OK;
+}
+
+// dst = (a + b) + c, c optional (residual + (routed + shared)).
+__global__ void __launch_bounds__(256) k_add3(const float *a, const float *b, const float *c,
+                                              int64_t n, float *dst) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    float v = a[i] + b[i];
+    if (c) v = c[i] + v;
+    dst[i] = v;
+}
+
+mx_status launch_add3(const float *a, const float *b, const float *c, int64_t n, float *dst,
+                      hipStream_t s) {
+    if (n == 0) return MX_OK;
+    hipLaunchKernelGGL(k_add3, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a, b, c, n, dst);
+    MX_LAUNCH("k_add3");
+    return MX_OK;
+}
+
+}  // namespace mx

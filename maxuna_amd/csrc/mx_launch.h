@@ -1,0 +1,98 @@
+// Internal launcher interface between the C-ABI layer (mx_api.hip) and the
+// kernel translation units.  Launchers assume validated arguments.
+#pragma once
+
+#include "mx_common.h"
+
+namespace mx {
+
+// mx_dequant.hip
+mx_status launch_dequantize(int dtype, const uint8_t *blocks, int64_t n, float *out,
+                            hipStream_t s);
+mx_status launch_synth(int dtype, uint64_t key, uint8_t *dst, int64_t nbytes, hipStream_t s);
+uint64_t tensor_key(uint64_t seed, uint32_t layer, uint32_t tensor_id);
+
+// mx_mv.hip -- gather mat-vec.  `ids` may be NULL (plain mat-vec: expert 0).
+struct MvArgs {
+    const uint8_t *w;       // first block of expert 0
+    int64_t expert_bytes;   // n_out * row_bytes
+    int64_t row_bytes;
+    int n_expert, n_out, k;
+    const float *x;
+    int x_per_row;
+    const uint32_t *ids;    // [t, top_k] or NULL
+    int t, top_k;
+    float *dst;             // [t, top_k, n_out]
+};
+mx_status launch_mul_mv_id(int dtype, const MvArgs &a, hipStream_t s);
+
+// Fused decode layer pieces (mx_mv.hip).
+struct DecodeGateUpArgs {
+    const uint8_t *gate, *up;            // routed stacks (first block of expert 0)
+    int64_t gu_expert_bytes, gu_row_bytes;
+    const uint8_t *sh_gate, *sh_up;      // shared expert (or NULL)
+    int64_t sh_row_bytes;
+    int n_expert, ff, hidden;
+    const float *x;                      // [t, hidden]
+    const uint32_t *ids;                 // [t, top_k]
+    int t, top_k;
+    float *act;                          // [t, top_k + has_shared, ff]
+};
+mx_status launch_decode_gate_up(int dtype, int sh_dtype, const DecodeGateUpArgs &a,
+                                hipStream_t s);
+
+struct DecodeDownArgs {
+    const uint8_t *down;
+    int64_t d_expert_bytes, d_row_bytes;
+    const uint8_t *sh_down;              // or NULL
+    int64_t sh_row_bytes;
+    int n_expert, ff, hidden;
+    const float *act;                    // [t, top_k + has_shared, ff]
+    const uint32_t *ids;                 // [t, top_k]
+    const float *w;                      // [t, top_k]
+    const float *residual;               // [t, hidden] or NULL
+    int t, top_k;
+    float *out;                          // [t, hidden]
+};
+mx_status launch_decode_down(int dtype, int sh_dtype, const DecodeDownArgs &a, hipStream_t s);
+
+// mx_route.hip
+mx_status launch_route_logits(const float *x, const float *router_t, int t, int hidden,
+                              int n_expert, float *logits, hipStream_t s);
+mx_status launch_route_select(const float *logits, const float *bias, int t, int n_expert,
+                              int top_k, float scale, int apply_scale, int norm, uint32_t *ids,
+                              float *w, hipStream_t s);
+// Decode router: RMSNorm (optional) + logits + select for t tokens in one
+// launch using a last-block reduction.  ws: partial sums + counter (zeroed once).
+size_t route_fused_ws_bytes(int t, int hidden, int n_expert);
+mx_status launch_route_fused(const float *x, const float *rms_alpha, float rms_eps,
+                             float *x_normed, const float *router_t, const float *bias, int t,
+                             int hidden, int n_expert, int top_k, float scale, int apply_scale,
+                             int norm, uint32_t *ids, float *w, void *ws, hipStream_t s);
+
+// mx_elem.hip
+mx_status launch_silu_mul(const float *g, const float *u, int64_t n, float *dst, hipStream_t s);
+mx_status launch_combine(const float *down, const float *col_l2, const float *w, int seq,
+                         int top_k, int n_out, float *dst, hipStream_t s);
+mx_status launch_rms_norm(const float *x, const float *alpha, int rows, int dim, float eps,
+                          float *dst, hipStream_t s);
+mx_status launch_add3(const float *a, const float *b, const float *c, int64_t n, float *dst,
+                      hipStream_t s);
+
+// mx_mm.hip -- bucketing + grouped GEMM
+size_t map0_bytes(int n_expert, int t, int top_k);
+mx_status launch_map0(const uint32_t *ids, int t, int top_k, int n_expert, int32_t *scratch,
+                      hipStream_t s);
+struct MmArgs {
+    const uint8_t *w;
+    int64_t expert_bytes, row_bytes;
+    int n_expert, n_out, k;
+    const float *x;          // [t, x_per_row, k] f32
+    int x_per_row;
+    int t, top_k;
+    const int32_t *map;      // map0 scratch
+    float *dst;              // [t, top_k, n_out]
+};
+mx_status launch_mul_mm_id(int dtype, const MmArgs &a, hipStream_t s);
+
+}  // namespace mx
