@@ -158,9 +158,11 @@ mx_status mx_rms_norm(const float *x, const float *alpha, int64_t rows, int64_t 
                       float *dst, mx_stream_t stream);
 
 /* ---- routing -------------------------------------------------------------------
- * logits[t,E] = x[t,H] . router_t[H,E] in f32.  Replaces route_logits
- * (src/moe.rs:84-87). */
-mx_status mx_route_logits(const float *x, const float *router_t, int64_t t, int64_t hidden,
+ * logits[t,e] = <x[t,:], router[e,:]> in f32.  Replaces route_logits
+ * (src/moe.rs:84-87).  `router` is [n_expert, hidden] -- the GGUF
+ * `ffn_gate_inp` tensor as stored; the reference's load-time transpose
+ * (moe.rs:43) is not needed. */
+mx_status mx_route_logits(const float *x, const float *router, int64_t t, int64_t hidden,
                           int64_t n_expert, float *logits, mx_stream_t stream);
 
 /* probs = sigmoid(logits); selection = probs + bias; stable descending top_k of
@@ -185,7 +187,7 @@ mx_status mx_route_from_logits(const float *logits, const float *bias, int64_t t
  * (model.rs:340-351).  `residual` may equal `out` (in-place update of the
  * residual stream) but neither may overlap `x` unless it IS `x` exactly. */
 typedef struct mx_moe_layer {
-    const float *router_t;      /* [hidden, n_expert] f32 (moe.rs:43)       */
+    const float *router;        /* [n_expert, hidden] f32, ffn_gate_inp      */
     const float *exp_probs_b;   /* [n_expert] f32 selection bias (moe.rs:44) */
     mx_expert_stack gate, up, down;           /* routed experts            */
     mx_expert_stack shared_gate, shared_up, shared_down; /* n_expert == 1  */

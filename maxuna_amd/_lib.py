@@ -53,7 +53,7 @@ class Map0C(C.Structure):
 
 class MoeLayerC(C.Structure):
     _fields_ = [
-        ("router_t", C.c_void_p),
+        ("router", C.c_void_p),
         ("exp_probs_b", C.c_void_p),
         ("gate", ExpertStackC),
         ("up", ExpertStackC),

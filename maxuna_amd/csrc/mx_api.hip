@@ -237,13 +237,13 @@ mx_status mx_rms_norm(const float *x, const float *alpha, int64_t rows, int64_t 
     return launch_rms_norm(x, alpha, (int)rows, (int)dim, eps, dst, (hipStream_t)stream);
 }
 
-mx_status mx_route_logits(const float *x, const float *router_t, int64_t t, int64_t hidden, int64_t n_expert,
+mx_status mx_route_logits(const float *x, const float *router, int64_t t, int64_t hidden, int64_t n_expert,
                           float *logits, mx_stream_t stream) {
     if (t < 0 || hidden <= 0 || n_expert <= 0 || t > INT32_MAX / 2)
         return fail(MX_ERR_SHAPE, "route_logits: bad shape");
     if (t == 0) return MX_OK;
-    if (!x || !router_t || !logits) return fail(MX_ERR_NULL, "route_logits: NULL operand");
-    return launch_route_logits(x, router_t, (int)t, (int)hidden, (int)n_expert, logits, (hipStream_t)stream);
+    if (!x || !router || !logits) return fail(MX_ERR_NULL, "route_logits: NULL operand");
+    return launch_route_logits(x, router, (int)t, (int)hidden, (int)n_expert, logits, (hipStream_t)stream);
 }
 
 static mx_status check_route(int64_t t, int64_t n_expert, int64_t top_k) {
@@ -270,7 +270,6 @@ mx_status mx_route_from_logits(const float *logits, const float *bias, int64_t t
 namespace {
 
 constexpr int64_t kDefaultMmMinSeq = 32;  // ops/mod.rs:31 MM_ID_MIN_SEQ
-constexpr int64_t kFusedRouterMaxT = 16;
 
 struct Ws {
     uint8_t *base;
@@ -286,6 +285,7 @@ struct Ws {
 
 struct Plan {
     bool mm, fused_router, has_shared;
+    bool shared_in_decode;  // shared expert rides in the fused decode kernels (same quant types)
     int64_t min_seq;
 };
 
@@ -293,8 +293,10 @@ Plan plan_for(const mx_moe_layer *L, int64_t t) {
     Plan p;
     p.min_seq = L->mm_min_seq > 0 ? L->mm_min_seq : kDefaultMmMinSeq;
     p.mm = L->mm_min_seq >= 0 && t >= p.min_seq;  // < 0: never (LAGUNA_NO_MM_ID)
-    p.fused_router = !p.mm && t <= kFusedRouterMaxT;
+    p.fused_router = !p.mm && t <= route_fused_max_t();
     p.has_shared = L->shared_gate.data != nullptr;
+    p.shared_in_decode = p.has_shared && L->shared_gate.dtype == L->gate.dtype &&
+                         L->shared_down.dtype == L->down.dtype;
     return p;
 }
 
@@ -303,6 +305,8 @@ struct Layout {
     uint8_t *route_ws = nullptr;
     float *x_normed = nullptr, *logits = nullptr, *w = nullptr, *act = nullptr;
     uint32_t *ids = nullptr, *zero_ids = nullptr;
+    float *part = nullptr;
+    unsigned *counters = nullptr;
     int32_t *map = nullptr, *map_sh = nullptr;
     float *gate = nullptr, *up = nullptr, *down = nullptr, *routed = nullptr;
     float *sh_g = nullptr, *sh_u = nullptr, *sh_out = nullptr;
@@ -322,7 +326,15 @@ Layout carve(const mx_moe_layer *L, int64_t t, const Plan &p, void *base) {
         o.logits = ws.take<float>(t * E);
     }
     if (!p.mm) {
-        o.act = ws.take<float>(t * (K + (p.has_shared ? 1 : 0)) * FF);
+        const int64_t slots = K + (p.shared_in_decode ? 1 : 0);
+        o.act = ws.take<float>(t * slots * FF);
+        o.part = ws.take<float>(t * slots * H);
+        o.counters = ws.take<unsigned>(decode_down_counter_words((int)t, (int)H));
+        if (p.has_shared && !p.shared_in_decode) {
+            o.sh_g = ws.take<float>(t * FF);
+            o.sh_u = ws.take<float>(t * FF);
+            o.sh_out = ws.take<float>(t * H);
+        }
     } else {
         o.map = ws.take<int32_t>(map0_bytes((int)E, (int)t, (int)K) / 4);
         o.gate = ws.take<float>(t * K * FF);
@@ -366,7 +378,7 @@ mx_status check_layer(const mx_moe_layer *L, int64_t t, StackGeom &gg, StackGeom
         return fail(MX_ERR_DTYPE, "moe: gate (%s) and up (%s) experts must share a quant type",
                     dt_name(L->gate.dtype), dt_name(L->up.dtype));
     MX_TRY(check_route(t, E, L->top_k));
-    if (!L->router_t || !L->exp_probs_b) return fail(MX_ERR_NULL, "moe: router or exp_probs_b is NULL");
+    if (!L->router || !L->exp_probs_b) return fail(MX_ERR_NULL, "moe: router or exp_probs_b is NULL");
     if (L->shared_gate.data) {
         MX_TRY(check_stack(&L->shared_gate, "ffn_gate_shexp", sg));
         MX_TRY(check_stack(&L->shared_up, "ffn_up_shexp", su));
@@ -442,7 +454,7 @@ mx_status moe_forward_impl(const mx_moe_layer *L, const float *x, int64_t t, con
 
     // routing (+ the RMSNorm of the FFN half when requested)
     if (p.fused_router) {
-        MX_TRY(launch_route_fused(x, L->rms_alpha, L->rms_eps, o.x_normed, L->router_t, L->exp_probs_b, (int)t,
+        MX_TRY(launch_route_fused(x, L->rms_alpha, L->rms_eps, o.x_normed, L->router, L->exp_probs_b, (int)t,
                                   (int)H, (int)E, (int)K, scale, apply, L->weights_norm, ids, w, o.route_ws, s));
         if (L->rms_alpha) xin = o.x_normed;
     } else {
@@ -450,20 +462,34 @@ mx_status moe_forward_impl(const mx_moe_layer *L, const float *x, int64_t t, con
             MX_TRY(launch_rms_norm(x, L->rms_alpha, (int)t, (int)H, L->rms_eps, o.x_normed, s));
             xin = o.x_normed;
         }
-        MX_TRY(launch_route_logits(xin, L->router_t, (int)t, (int)H, (int)E, o.logits, s));
+        MX_TRY(launch_route_logits(xin, L->router, (int)t, (int)H, (int)E, o.logits, s));
         MX_TRY(launch_route_select(o.logits, L->exp_probs_b, (int)t, (int)E, (int)K, scale, apply,
                                    L->weights_norm, ids, w, s));
     }
     MX_STAGE();
 
     if (!p.mm) {
-        DecodeGateUpArgs ga{gg.w, gu.w, gg.expert_bytes, gg.row_bytes, sg.w, su.w, sg.row_bytes,
-                            (int)E, (int)FF, (int)H, xin, ids, (int)t, (int)K, o.act};
-        MX_TRY(launch_decode_gate_up(L->gate.dtype, L->shared_gate.dtype, ga, s));
+        const bool shf = p.shared_in_decode;
+        const float *shared_out = nullptr;
+        if (p.has_shared && !shf) {
+            // shared expert of another quant type: its own gather mat-vecs (expert 0)
+            MvArgs mg{sg.w, sg.expert_bytes, sg.row_bytes, 1, (int)FF, (int)H, xin, 1, nullptr, (int)t, 1, o.sh_g};
+            MX_TRY(launch_mul_mv_id(L->shared_gate.dtype, mg, s));
+            mg.w = su.w;
+            mg.dst = o.sh_u;
+            MX_TRY(launch_mul_mv_id(L->shared_up.dtype, mg, s));
+            MX_TRY(launch_silu_mul(o.sh_g, o.sh_u, t * FF, o.sh_g, s));
+            MvArgs md{sd.w, sd.expert_bytes, sd.row_bytes, 1, (int)H, (int)FF, o.sh_g, 1, nullptr, (int)t, 1, o.sh_out};
+            MX_TRY(launch_mul_mv_id(L->shared_down.dtype, md, s));
+            shared_out = o.sh_out;
+        }
+        DecodeGateUpArgs ga{gg.w, gu.w, gg.expert_bytes, gg.row_bytes, shf ? sg.w : nullptr, shf ? su.w : nullptr,
+                            sg.row_bytes, (int)E, (int)FF, (int)H, xin, ids, (int)t, (int)K, o.act};
+        MX_TRY(launch_decode_gate_up(L->gate.dtype, ga, s));
         MX_STAGE();
-        DecodeDownArgs da{gd.w, gd.expert_bytes, gd.row_bytes, sd.w, sd.row_bytes, (int)E, (int)FF, (int)H,
-                          o.act, ids, w, residual, (int)t, (int)K, out};
-        MX_TRY(launch_decode_down(L->down.dtype, L->shared_down.dtype, da, s));
+        DecodeDownArgs da{gd.w, gd.expert_bytes, gd.row_bytes, shf ? sd.w : nullptr, sd.row_bytes, shared_out,
+                          (int)E, (int)FF, (int)H, o.act, ids, w, residual, (int)t, (int)K, out, o.part, o.counters};
+        MX_TRY(launch_decode_down(L->down.dtype, da, s));
         MX_STAGE();
         return MX_OK;
     }

@@ -36,28 +36,33 @@ struct DecodeGateUpArgs {
     const float *x;                      // [t, hidden]
     const uint32_t *ids;                 // [t, top_k]
     int t, top_k;
-    float *act;                          // [t, top_k + has_shared, ff]
+    float *act;                          // [t, top_k + (sh_gate != NULL), ff]
 };
-mx_status launch_decode_gate_up(int dtype, int sh_dtype, const DecodeGateUpArgs &a,
-                                hipStream_t s);
+// the shared expert (sh_gate/sh_up != NULL) must have the routed experts' quant type
+mx_status launch_decode_gate_up(int dtype, const DecodeGateUpArgs &a, hipStream_t s);
 
 struct DecodeDownArgs {
     const uint8_t *down;
     int64_t d_expert_bytes, d_row_bytes;
-    const uint8_t *sh_down;              // or NULL
+    const uint8_t *sh_down;              // shared down of the routed quant type, or NULL
     int64_t sh_row_bytes;
+    const float *shared_out;             // [t, hidden] precomputed shared expert, or NULL
     int n_expert, ff, hidden;
-    const float *act;                    // [t, top_k + has_shared, ff]
+    const float *act;                    // [t, top_k + (sh_down != NULL), ff]
     const uint32_t *ids;                 // [t, top_k]
     const float *w;                      // [t, top_k]
     const float *residual;               // [t, hidden] or NULL
     int t, top_k;
     float *out;                          // [t, hidden]
+    float *part;                         // [t, top_k + (sh_down != NULL), hidden] scratch
+    unsigned *counters;                  // decode_down_counter_words(t, hidden), zero, self-resetting
 };
-mx_status launch_decode_down(int dtype, int sh_dtype, const DecodeDownArgs &a, hipStream_t s);
+mx_status launch_decode_down(int dtype, const DecodeDownArgs &a, hipStream_t s);
+size_t decode_down_counter_words(int t, int hidden);
 
 // mx_route.hip
-mx_status launch_route_logits(const float *x, const float *router_t, int t, int hidden,
+// router: [n_expert, hidden] (GGUF ffn_gate_inp layout)
+mx_status launch_route_logits(const float *x, const float *router, int t, int hidden,
                               int n_expert, float *logits, hipStream_t s);
 mx_status launch_route_select(const float *logits, const float *bias, int t, int n_expert,
                               int top_k, float scale, int apply_scale, int norm, uint32_t *ids,
@@ -65,8 +70,9 @@ mx_status launch_route_select(const float *logits, const float *bias, int t, int
 // Decode router: RMSNorm (optional) + logits + select for t tokens in one
 // launch using a last-block reduction.  ws: partial sums + counter (zeroed once).
 size_t route_fused_ws_bytes(int t, int hidden, int n_expert);
+int route_fused_max_t();
 mx_status launch_route_fused(const float *x, const float *rms_alpha, float rms_eps,
-                             float *x_normed, const float *router_t, const float *bias, int t,
+                             float *x_normed, const float *router, const float *bias, int t,
                              int hidden, int n_expert, int top_k, float scale, int apply_scale,
                              int norm, uint32_t *ids, float *w, void *ws, hipStream_t s);
 

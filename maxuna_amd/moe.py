@@ -21,9 +21,9 @@ from .gguf import ExpertStack, null_stack
 WEIGHTS_SUM_FLOOR = 6.103515625e-5
 
 
-def route_logits(router_t: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
-    """moe.rs:84-87."""
-    return ops.route_logits(router_t, x)
+def route_logits(router: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+    """moe.rs:84-87 (router in its GGUF layout [n_expert, hidden])."""
+    return ops.route_logits(router, x)
 
 
 def route_from_logits(logits, bias, n_expert_used, scale, norm):
@@ -93,11 +93,11 @@ class MoeConfig:
 class MoeBlock:
     """One MoE FFN block: `routed(x, route(x)) + shared(x)` (moe.rs:28-79)."""
 
-    def __init__(self, router_t: torch.Tensor, exp_probs_b: torch.Tensor, gate: ExpertStack,
+    def __init__(self, router: torch.Tensor, exp_probs_b: torch.Tensor, gate: ExpertStack,
                  up: ExpertStack, down: ExpertStack, cfg: MoeConfig,
                  shared: SharedExpert | None = None, rms_alpha: torch.Tensor | None = None,
                  rms_eps: float = 1e-6):
-        self.router_t = router_t.contiguous()
+        self.router = router.contiguous()  # [n_expert, hidden], ffn_gate_inp as stored
         self.exp_probs_b = exp_probs_b.contiguous()
         self.experts = FusedExperts(gate, up, down)
         self.shared = shared
@@ -109,13 +109,13 @@ class MoeBlock:
 
     @property
     def hidden(self) -> int:
-        return self.router_t.shape[0]
+        return self.router.shape[1]
 
     def _layer_struct(self) -> MoeLayerC:
         e = self.experts
         sh = self.shared
         return MoeLayerC(
-            self.router_t.data_ptr(), self.exp_probs_b.data_ptr(),
+            self.router.data_ptr(), self.exp_probs_b.data_ptr(),
             e.gate.to_c(), e.up.to_c(), e.down.to_c(),
             sh.gate.to_c() if sh else null_stack(), sh.up.to_c() if sh else null_stack(),
             sh.down.to_c() if sh else null_stack(),
@@ -134,7 +134,7 @@ class MoeBlock:
 
     def route(self, x_normed: torch.Tensor):
         """(ids [t, k] u32, weights [t, k] f32) (moe.rs:62-71)."""
-        logits = route_logits(self.router_t, x_normed)
+        logits = route_logits(self.router, x_normed)
         return route_from_logits(logits, self.exp_probs_b, self.cfg.n_expert_used,
                                  self.cfg.expert_weights_scale, self.cfg.expert_weights_norm)
 

@@ -218,16 +218,17 @@ def dequantize(blocks: torch.Tensor, dtype: GgmlDType, n: int) -> torch.Tensor:
     return out
 
 
-def route_logits(router_t: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
-    """logits[t, e] = <x[t], router[e]> in f32; router_t is [hidden, n_expert] (moe.rs:84-87)."""
+def route_logits(router: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+    """logits[t, e] = <x[t], router[e]> in f32 (moe.rs:84-87).  `router` is the GGUF
+    `ffn_gate_inp` weight [n_expert, hidden] as stored (no transpose needed)."""
     _f32(x, "x", 2)
-    _f32(router_t, "router_t", 2)
+    _f32(router, "router", 2)
     t, hidden = x.shape
-    if router_t.shape[0] != hidden:
-        raise MaxunaError(2, f"router_t {tuple(router_t.shape)} does not match hidden {hidden}")
-    n_expert = router_t.shape[1]
+    if router.shape[1] != hidden:
+        raise MaxunaError(2, f"router {tuple(router.shape)} does not match hidden {hidden}")
+    n_expert = router.shape[0]
     out = torch.empty((t, n_expert), dtype=torch.float32, device=x.device)
-    check(lib().mx_route_logits(x.data_ptr(), router_t.data_ptr(), t, hidden, n_expert, out.data_ptr(),
+    check(lib().mx_route_logits(x.data_ptr(), router.data_ptr(), t, hidden, n_expert, out.data_ptr(),
                                 _stream()))
     return out
 

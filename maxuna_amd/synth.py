@@ -114,17 +114,21 @@ class SynthLayer:
     seed: int
     layer: int
     block: MoeBlock
-    router_t: np.ndarray        # host copy [hidden, n_expert]
+    router: np.ndarray          # host copy [n_expert, hidden] (GGUF ffn_gate_inp layout)
     bias: np.ndarray            # host copy [n_expert]
     keys: dict = field(default_factory=dict)
+
+    @property
+    def router_t(self) -> np.ndarray:
+        """[hidden, n_expert], the reference's pre-transposed router (moe.rs:43)."""
+        return np.ascontiguousarray(self.router.T)
 
 
 def build_layer(spec: LayerSpec, seed: int, layer: int = 0, device="cuda", rms: bool = False) -> SynthLayer:
     """Allocates and fills one layer on the device."""
     key = lambda name: tensor_key(seed, layer, TENSOR_IDS[name])  # noqa: E731
-    # router ~ N(0, sigma) as the ggml [n_expert, hidden] weight, pre-transposed (moe.rs:43)
+    # router ~ N(0, sigma) in the GGUF ffn_gate_inp layout [n_expert, hidden]
     router = normal(key("router"), spec.n_expert * spec.hidden, spec.router_sigma).reshape(spec.n_expert, spec.hidden)
-    router_t = np.ascontiguousarray(router.T)
     bias = (normal(key("bias"), spec.n_expert, spec.bias_sigma) if spec.bias_sigma > 0
             else np.zeros(spec.n_expert, dtype=np.float32))
     keys = {n: key(n) for n in TENSOR_IDS}
@@ -139,10 +143,10 @@ def build_layer(spec: LayerSpec, seed: int, layer: int = 0, device="cuda", rms: 
             synth_stack(spec.down_dt, 1, spec.hidden, spec.ff, keys["down_shexp"], device))
     # RMSNorm weight = 1 (declared for the C4 chain)
     alpha = torch.ones(spec.hidden, dtype=torch.float32, device=device) if rms else None
-    block = MoeBlock(torch.from_numpy(router_t).to(device), torch.from_numpy(bias).to(device), gate, up, down,
+    block = MoeBlock(torch.from_numpy(router).to(device), torch.from_numpy(bias).to(device), gate, up, down,
                      MoeConfig(spec.top_k, spec.weights_scale, spec.weights_norm), shared=shared,
                      rms_alpha=alpha, rms_eps=1e-6)
-    return SynthLayer(spec, seed, layer, block, router_t, bias, keys)
+    return SynthLayer(spec, seed, layer, block, router, bias, keys)
 
 
 def make_x(spec: LayerSpec, seed: int, t: int, layer: int = 0, sigma: float = 1.0) -> np.ndarray:

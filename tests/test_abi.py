@@ -111,7 +111,7 @@ def test_route_validation():
 
 def _layer(**kw):
     H, FF, E = 256, 512, 8
-    d = dict(router_t=FAKE, exp_probs_b=FAKE, gate=stack(12, E, FF, H), up=stack(12, E, FF, H),
+    d = dict(router=FAKE, exp_probs_b=FAKE, gate=stack(12, E, FF, H), up=stack(12, E, FF, H),
              down=stack(14, E, H, FF), shared_gate=ExpertStackC(), shared_up=ExpertStackC(),
              shared_down=ExpertStackC(), hidden=H, expert_ff=FF, top_k=2, weights_scale=1.0,
              weights_norm=1, mm_min_seq=0, rms_alpha=None, rms_eps=1e-6, reserved=0)
@@ -126,7 +126,7 @@ def test_moe_forward_validation():
     assert run(_layer(up=stack(12, 7, 512, 256))) == 2 and "disagree on n_expert" in err()
     assert run(_layer(up=stack(14, 8, 512, 256))) == 3 and "share a quant type" in err()
     assert run(_layer(top_k=9)) == 8
-    assert run(_layer(router_t=None)) == 1
+    assert run(_layer(router=None)) == 1
     lay = _layer()
     need = L.mx_moe_workspace_bytes(C.byref(lay), 1)
     assert need > 0

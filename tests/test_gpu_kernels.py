@@ -150,9 +150,9 @@ def test_route_logits(dev, orc):
     rng = np.random.default_rng(5)
     for t in (1, 70):
         x = rng.standard_normal((t, 1024)).astype(np.float32)
-        r = (rng.standard_normal((1024, 256)) * 0.02).astype(np.float32)
+        r = (rng.standard_normal((256, 1024)) * 0.02).astype(np.float32)  # [n_expert, hidden]
         got = host(ops.route_logits(dev_f32(r), dev_f32(x)))
-        assert_close(got, orc.route_logits(x, r), rel=1e-5, what="logits")
+        assert_close(got, orc.route_logits(x, np.ascontiguousarray(r.T)), rel=1e-5, what="logits")
 
 
 def _distinct_ids(rng, t, k, E):
