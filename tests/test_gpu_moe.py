@@ -79,8 +79,12 @@ def test_prefill_grouped_gemm_small(dev, orc):
 
 
 def test_prefill_full_size_mm_vs_decode_and_sample(dev, orc):
-    """C3 at its full size t = 2048 (skewed bias): grouped GEMM vs the decode path on
-    every row (same routing), plus the oracle on a sample of 24 token rows."""
+    """C3 at its full size t = 2048 (skewed bias).  The grouped-GEMM output is held
+    to the contract's tolerance against the oracle on a sample of 64 token rows,
+    and compared with the decode path (same routing) on every row.  Both GPU paths
+    are approximations of the oracle, so the all-rows cross-check bounds rel-L2
+    only by the sum of the two paths' budgets (2e-3); the max-abs bound applies to
+    the oracle comparison."""
     cfg = CONFIGS["C3"]
     spec = cfg["spec"]
     _log("C3 t=2048")
@@ -89,6 +93,12 @@ def test_prefill_full_size_mm_vs_decode_and_sample(dev, orc):
     out, ids, w = run_block(layer, x)
     counts = np.bincount(ids.ravel(), minlength=spec.n_expert)
     assert counts.max() > 4 * counts.mean()  # the skewed bias really is imbalanced
+    rows = np.linspace(0, 2047, 64).astype(int)
+    want, _, _ = orc.moe_layer(spec, layer.keys, layer.router_t, layer.bias, x[rows], ids=ids[rows], w=w[rows])
+    assert_close(out[rows], want, what="C3 sample vs oracle")
+    logits = orc.route_logits(x[rows], layer.router_t)
+    oid, _ = orc.route_from_logits(logits, layer.bias, spec.top_k, 1.0, True)
+    check_ids(ids[rows], oid, selection_margin(logits, layer.bias, spec.top_k))
     xd = dev_f32(x)
     # decode path on the same routing, through the reference-shaped ops
     gate, up, down = layer.block.experts.gate, layer.block.experts.up, layer.block.experts.down
@@ -97,14 +107,9 @@ def test_prefill_full_size_mm_vs_decode_and_sample(dev, orc):
     xg = xd.reshape(2048, 1, -1)
     act = ops.silu_mul(ops.mul_mv_id(gate, xg, ids_d), ops.mul_mv_id(up, xg, ids_d))
     routed = ops.combine(ops.mul_mv_id(down, act, ids_d), None, w_d)
-    ref = host(routed + layer.block.shared.forward(xd))
-    assert_close(out, ref, what="C3 mm vs mv (all rows)")
-    rows = np.linspace(0, 2047, 24).astype(int)
-    want, _, _ = orc.moe_layer(spec, layer.keys, layer.router_t, layer.bias, x[rows], ids=ids[rows], w=w[rows])
-    assert_close(out[rows], want, what="C3 sample vs oracle")
-    logits = orc.route_logits(x[rows], layer.router_t)
-    oid, _ = orc.route_from_logits(logits, layer.bias, spec.top_k, 1.0, True)
-    check_ids(ids[rows], oid, selection_margin(logits, layer.bias, spec.top_k))
+    mv = host(routed + layer.block.shared.forward(xd))
+    assert_close(mv[rows], want, what="C3 decode path sample vs oracle")
+    assert_close(out, mv, rel=2e-3, max_of_rms=np.inf, what="C3 mm vs mv (all rows)")
 
 
 def test_fused_experts_ops_match_block(dev, orc):
