@@ -305,6 +305,7 @@ struct Layout {
     uint8_t *route_ws = nullptr;
     float *x_normed = nullptr, *logits = nullptr, *w = nullptr, *act = nullptr;
     uint32_t *ids = nullptr, *zero_ids = nullptr;
+    uint8_t *xstage = nullptr;
     float *part = nullptr;
     unsigned *counters = nullptr;
     int32_t *map = nullptr, *map_sh = nullptr;
@@ -327,6 +328,7 @@ Layout carve(const mx_moe_layer *L, int64_t t, const Plan &p, void *base) {
     }
     if (!p.mm) {
         const int64_t slots = K + (p.shared_in_decode ? 1 : 0);
+        o.xstage = ws.take<uint8_t>(t * stage_row_bytes((int)H));
         o.act = ws.take<float>(t * slots * FF);
         o.part = ws.take<float>(t * slots * H);
         o.counters = ws.take<unsigned>(decode_down_counter_words((int)t, (int)H));
@@ -454,8 +456,10 @@ mx_status moe_forward_impl(const mx_moe_layer *L, const float *x, int64_t t, con
 
     // routing (+ the RMSNorm of the FFN half when requested)
     if (p.fused_router) {
+        // the router also stages the (normalised) rows for the decode expert kernels
         MX_TRY(launch_route_fused(x, L->rms_alpha, L->rms_eps, o.x_normed, L->router, L->exp_probs_b, (int)t,
-                                  (int)H, (int)E, (int)K, scale, apply, L->weights_norm, ids, w, o.route_ws, s));
+                                  (int)H, (int)E, (int)K, scale, apply, L->weights_norm, ids, w, o.route_ws,
+                                  o.xstage, s));
         if (L->rms_alpha) xin = o.x_normed;
     } else {
         if (L->rms_alpha) {
@@ -465,6 +469,7 @@ mx_status moe_forward_impl(const mx_moe_layer *L, const float *x, int64_t t, con
         MX_TRY(launch_route_logits(xin, L->router, (int)t, (int)H, (int)E, o.logits, s));
         MX_TRY(launch_route_select(o.logits, L->exp_probs_b, (int)t, (int)E, (int)K, scale, apply,
                                    L->weights_norm, ids, w, s));
+        if (!p.mm) MX_TRY(launch_stage_rows(xin, (int)t, (int)H, o.xstage, s));
     }
     MX_STAGE();
 
@@ -484,11 +489,12 @@ mx_status moe_forward_impl(const mx_moe_layer *L, const float *x, int64_t t, con
             shared_out = o.sh_out;
         }
         DecodeGateUpArgs ga{gg.w, gu.w, gg.expert_bytes, gg.row_bytes, shf ? sg.w : nullptr, shf ? su.w : nullptr,
-                            sg.row_bytes, (int)E, (int)FF, (int)H, xin, ids, (int)t, (int)K, o.act};
+                            sg.row_bytes, (int)E, (int)FF, (int)H, o.xstage, ids, (int)t, (int)K, o.act};
         MX_TRY(launch_decode_gate_up(L->gate.dtype, ga, s));
         MX_STAGE();
         DecodeDownArgs da{gd.w, gd.expert_bytes, gd.row_bytes, shf ? sd.w : nullptr, sd.row_bytes, shared_out,
-                          (int)E, (int)FF, (int)H, o.act, ids, w, residual, (int)t, (int)K, out, o.part, o.counters};
+                          (int)E, (int)FF, (int)H, o.act, ids, w, residual, (int)t, (int)K, out, o.part,
+                          o.counters};
         MX_TRY(launch_decode_down(L->down.dtype, da, s));
         MX_STAGE();
         return MX_OK;

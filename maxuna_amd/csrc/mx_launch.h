@@ -33,10 +33,10 @@ struct DecodeGateUpArgs {
     const uint8_t *sh_gate, *sh_up;      // shared expert (or NULL)
     int64_t sh_row_bytes;
     int n_expert, ff, hidden;
-    const float *x;                      // [t, hidden]
+    const uint8_t *xstage;               // [t] staged rows of x (mx_stage.h), xstage_bytes(hidden) each
     const uint32_t *ids;                 // [t, top_k]
     int t, top_k;
-    float *act;                          // [t, top_k + (sh_gate != NULL), ff]
+    float *act;                          // [t, slots, ff], slots = top_k + (sh_gate != NULL)
 };
 // the shared expert (sh_gate/sh_up != NULL) must have the routed experts' quant type
 mx_status launch_decode_gate_up(int dtype, const DecodeGateUpArgs &a, hipStream_t s);
@@ -68,13 +68,19 @@ mx_status launch_route_select(const float *logits, const float *bias, int t, int
                               int top_k, float scale, int apply_scale, int norm, uint32_t *ids,
                               float *w, hipStream_t s);
 // Decode router: RMSNorm (optional) + logits + select for t tokens in one
-// launch using a last-block reduction.  ws: partial sums + counter (zeroed once).
+// launch using a last-block reduction; also stages the (normalised) rows into
+// `xstage` (mx_stage.h layout) and/or writes them to `x_normed` when non-NULL.
+// ws: logits + counter (zeroed once, self-resetting).
 size_t route_fused_ws_bytes(int t, int hidden, int n_expert);
 int route_fused_max_t();
 mx_status launch_route_fused(const float *x, const float *rms_alpha, float rms_eps,
                              float *x_normed, const float *router, const float *bias, int t,
                              int hidden, int n_expert, int top_k, float scale, int apply_scale,
-                             int norm, uint32_t *ids, float *w, void *ws, hipStream_t s);
+                             int norm, uint32_t *ids, float *w, void *ws, uint8_t *xstage,
+                             hipStream_t s);
+// Stages t rows of k values (mx_stage.h layout, xstage_bytes(k) per row).
+mx_status launch_stage_rows(const float *x, int t, int k, uint8_t *xstage, hipStream_t s);
+size_t stage_row_bytes(int k);
 
 // mx_elem.hip
 mx_status launch_silu_mul(const float *g, const float *u, int64_t n, float *dst, hipStream_t s);

@@ -1,59 +1,86 @@
 // Decode-time gather mat-vec over raw GGUF blocks (the mul_mv_id hot path) and
 // the fused decode MoE kernels built from it.
 //
+// Activations are consumed in the staged integer form of mx_stage.h: per
+// 32-value group a scale s_g and integers x16 = 256 * xh + xl in two int8 digit
+// planes, plus sums of x16 over every 8 and 32 values.  The gate/up kernel
+// reads the token rows staged once by the router kernel (global memory); the
+// down kernel and the generic mat-vec stage their row into LDS per workgroup
+// (activation loads issued before the weight loads).  The weight quants are unpacked to bytes with masks and shifts and contracted with both
+// digit planes on v_dot4_i32_i8, so each sub-block's sum of q * x16 is exact in
+// int32; the per-sub-block scales (d*sc, dmin*m) and the group scale s_g are
+// applied once per sub-block in f32 (the factored form of mv.metal:263-267).
+// Relative error per activation value <= 2^-16 of its group maximum.
+//
 // Work layout (gfx950, wave64).  A row of k weights is cut into "groups":
-//   Q4_K  group = one 64-weight super-block pair (sub-blocks 2i, 2i+1)   (4 per block)
-//   Q6_K  group = 32 weights: half n, 8-wide l-slice j of all 4 parts      (8 per block)
-//   Q8_0  group = one 34-byte block of 32 weights                          (1 per block)
+//   Q4_K  group = one 64-weight sub-block pair (2i, 2i+1) of a super-block (4 per block)
+//   Q6_K  group = 32 weights: half n, 8-wide l-slice j of all 4 parts        (8 per block)
+//   Q8_0  group = one 34-byte block of 32 weights                            (1 per block)
 // P lanes share a row; lane `sub` owns groups sub, sub+P, ... (NG of them, the
 // last possibly masked), so the activation slice a lane needs is the same for
-// every row.  It is quantised once per wave to int16 with an exact per-group
-// power-of-two scale (|x| * 2^-e < 2^14: 15 significant bits, ~2^-15 relative
-// to the group maximum) and kept in registers while the wave streams its rows.
-// Weight bytes are read straight from the GGUF layout, NB row-iterations per
-// batch so that several rows' loads are in flight per wave.
+// every row and is held in registers.
 //
-// Inner product: quants are unpacked into int16 pairs with shifts and masks and
-// multiplied with the int16 activations by v_dot2_i32_i16 -- exact int32
-// accumulation per sub-block (bounds: 32 * 255 * 16384 < 2^31).  The super-block
-// scales (d*sc, dmin*m) are applied per sub-block in f32.
+// Weight bytes never pass through the lanes' own load pattern: each wave copies
+// the contiguous byte span of its next batch of rows into a private, double-
+// buffered LDS ring with global_load_lds_dwordx4 (every wave instruction moves
+// 1 KB of consecutive aligned 16-byte chunks -- fully coalesced, no VGPRs), and
+// the lanes then read their groups from LDS.  The copy of batch i+1 is in
+// flight while batch i is computed; the wave waits on its own copy with an
+// explicit vmcnt.  Aligned 16-byte chunks never cross a page, so copying the
+// chunks that cover a span never touches an unmapped page.
 //
 // Reference kernels replaced: kernel_mul_mv_id_*_f32_v (mv.metal:680-731, dispatch
 // geometry dispatch.rs:409-462), silu_mul.metal:57-72, combine.metal:70-97.
 #include "mx_launch.h"
+#include "mx_stage.h"
 
 namespace mx {
 
-typedef short short2_t __attribute__((ext_vector_type(2)));
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ int sdot2(uint32_t a, uint32_t b, int c) {
-    return __builtin_amdgcn_sdot2(__builtin_bit_cast(short2_t, a), __builtin_bit_cast(short2_t, b), c, false);
+__device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }
 
-// 16-byte load of streamed weight bytes, marked non-temporal (read once per pass)
-__device__ __forceinline__ uint4 ld_stream16(const uint8_t *p) {
-    const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p));
-    return make_uint4(v.x, v.y, v.z, v.w);
+// ---- wave-private LDS weight staging ------------------------------------------------
+#define MX_AS_LDS __attribute__((address_space(3)))
+#define MX_AS_GLB __attribute__((address_space(1)))
+
+// one 16-byte global -> LDS copy per lane; `lds_dst` must be wave-uniform (the
+// hardware writes lane i's 16 bytes at lds_dst + 16 * i)
+__device__ __forceinline__ void dma16(const uint8_t *src, uint8_t *lds_dst) {
+    __builtin_amdgcn_global_load_lds((MX_AS_GLB void *)src, (MX_AS_LDS void *)lds_dst, 16, 0, 0);
 }
 
-// Activation quantiser for one group: xi = round(x * 2^-e) with e chosen so that
-// max|x| * 2^-e lies in [2^13, 2^14).  Rounding is the f32 add of 1.5 * 2^23
-// (round-to-nearest-even); the low 16 bits of the sum's bit pattern are the
-// int16 two's-complement value.
-struct XQ {
-    float inv, scale;
-    __device__ __forceinline__ explicit XQ(float mx) {
-        const int e = mx > 0.f ? ilogbf(mx) - 13 : 0;
-        inv = ldexpf(1.f, -e);
-        scale = ldexpf(1.f, e);
+// s_waitcnt vmcnt(n) for a wave-uniform n in 0..63 (expcnt / lgkmcnt not waited)
+#define MX_VMW(n) \
+    case n: __builtin_amdgcn_s_waitcnt(0x0F70 | ((n) & 15) | (((n) >> 4) << 14)); break;
+__device__ __forceinline__ void wait_vmcnt(int n) {
+    switch (n) {
+        MX_VMW(0) MX_VMW(1) MX_VMW(2) MX_VMW(3) MX_VMW(4) MX_VMW(5) MX_VMW(6) MX_VMW(7)
+        MX_VMW(8) MX_VMW(9) MX_VMW(10) MX_VMW(11) MX_VMW(12) MX_VMW(13) MX_VMW(14) MX_VMW(15)
+        MX_VMW(16) MX_VMW(17) MX_VMW(18) MX_VMW(19) MX_VMW(20) MX_VMW(21) MX_VMW(22) MX_VMW(23)
+        MX_VMW(24) MX_VMW(25) MX_VMW(26) MX_VMW(27) MX_VMW(28) MX_VMW(29) MX_VMW(30) MX_VMW(31)
+        default: __builtin_amdgcn_s_waitcnt(0x0F70); break;
     }
-    __device__ __forceinline__ uint32_t pack(float a, float b) const {
-        const float ra = a * inv + 12582912.0f, rb = b * inv + 12582912.0f;
-        return __builtin_amdgcn_perm(__float_as_uint(rb), __float_as_uint(ra), 0x05040100u);
+    asm volatile("" ::: "memory");
+}
+#undef MX_VMW
+
+// DMA instructions for a batch of `rows` rows of `row_bytes` of nm matrices
+// (worst-case alignment: one extra chunk per matrix span)
+__host__ __device__ inline int dma_insts(int nm, int rows, int64_t row_bytes) {
+    const int64_t chunks = nm * ((rows * row_bytes + 15) / 16 + 1);
+    return (int)((chunks + 63) / 64);
+}
+constexpr int DMA_MAX_INSTS = 15;  // per batch (vmcnt budget of the waits, up to 2 batches ahead)
+
+__device__ __forceinline__ void lds_words(const int8_t *p, uint32_t *dst, int n16) {
+    // n16 16-byte reads from a 16-byte-aligned LDS address
+    const uint4 *q = reinterpret_cast<const uint4 *>(p);
+    for (int i = 0; i < n16; i++) {
+        const uint4 v = q[i];
+        dst[4 * i] = v.x; dst[4 * i + 1] = v.y; dst[4 * i + 2] = v.z; dst[4 * i + 3] = v.w;
     }
-};
-constexpr uint32_t ONES = 0x00010001u;  // sdot2 with (1, 1): sum of an int16 pair
+}
 
 template <int DT> struct Q;
 
@@ -61,64 +88,55 @@ template <int DT> struct Q;
 template <> struct Q<kQ4_K> {
     static constexpr int GPB = 4;
     struct X {
-        uint32_t lo[16], hi[16];  // qs dword w: [2w] = (x[4w], x[4w+2]), [2w+1] = (x[4w+1], x[4w+3])
-        int slo, shi;
-        float scale;
+        uint32_t h[16], l[16];  // [0..8): sub-block 2i positions 0..31, [8..16): sub-block 2i+1
+        float sa, sb, ssa, ssb;  // group scales and scale * sum(x16)
     };
-    struct Raw { uint4 h, qa, qb; };
-    __device__ static void load_x(const float *__restrict__ xrow, int g, X &x) {
-        float v[64];
-        const float4 *p = reinterpret_cast<const float4 *>(xrow + 64 * g);
-        float mx = 0.f;
+    struct Raw { uint4 hd, qa, qb; };
+    __device__ static void load_x(const XView &xv, int g, X &x) {
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const float4 f = p[i];
-            v[4 * i] = f.x; v[4 * i + 1] = f.y; v[4 * i + 2] = f.z; v[4 * i + 3] = f.w;
-            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(f.x), fabsf(f.y)), fmaxf(fabsf(f.z), fabsf(f.w))));
+        for (int half = 0; half < 2; half++) {
+            lds_words(xv.xh + 64 * g + 32 * half, x.h + 8 * half, 2);
+            lds_words(xv.xl + 64 * g + 32 * half, x.l + 8 * half, 2);
         }
-        const XQ qz(mx);
-        x.scale = qz.scale;
-        int slo = 0, shi = 0;
-#pragma unroll
-        for (int w = 0; w < 8; w++) {
-            x.lo[2 * w] = qz.pack(v[4 * w], v[4 * w + 2]);
-            x.lo[2 * w + 1] = qz.pack(v[4 * w + 1], v[4 * w + 3]);
-            x.hi[2 * w] = qz.pack(v[32 + 4 * w], v[32 + 4 * w + 2]);
-            x.hi[2 * w + 1] = qz.pack(v[32 + 4 * w + 1], v[32 + 4 * w + 3]);
-            slo = sdot2(x.lo[2 * w], ONES, sdot2(x.lo[2 * w + 1], ONES, slo));
-            shi = sdot2(x.hi[2 * w], ONES, sdot2(x.hi[2 * w + 1], ONES, shi));
-        }
-        x.slo = slo; x.shi = shi;
+        x.sa = xv.s[2 * g];
+        x.sb = xv.s[2 * g + 1];
+        x.ssa = x.sa * (float)xv.S32[2 * g];
+        x.ssb = x.sb * (float)xv.S32[2 * g + 1];
     }
     __device__ static Raw load(const uint8_t *__restrict__ row, int g) {
         const uint8_t *blk = row + (g >> 2) * 144;
         const int i = g & 3;
         Raw r;
-        r.h = ld_stream16(blk);
-        r.qa = ld_stream16(blk + 16 + 32 * i);
-        r.qb = ld_stream16(blk + 32 + 32 * i);
+        r.hd = *reinterpret_cast<const uint4 *>(blk);
+        r.qa = *reinterpret_cast<const uint4 *>(blk + 16 + 32 * i);
+        r.qb = *reinterpret_cast<const uint4 *>(blk + 32 + 32 * i);
         return r;
     }
     __device__ static float dot(const Raw &r, int g, const X &x) {
+#ifdef MX_FAKE_DOT
+        return (float)(r.hd.x ^ r.hd.y ^ r.hd.z ^ r.hd.w ^ r.qa.x ^ r.qa.y ^ r.qa.z ^ r.qa.w ^ r.qb.x ^ r.qb.y ^ r.qb.z ^ r.qb.w ^ x.h[0]);
+#endif
         const uint32_t q[8] = {r.qa.x, r.qa.y, r.qa.z, r.qa.w, r.qb.x, r.qb.y, r.qb.z, r.qb.w};
-        int alo = 0, ahi = 0;
+        int ah = 0, al = 0, bh = 0, bl = 0;
 #pragma unroll
         for (int w = 0; w < 8; w++) {
-            const uint32_t v = q[w];
-            alo = sdot2(v & 0x000F000Fu, x.lo[2 * w], alo);
-            alo = sdot2((v >> 8) & 0x000F000Fu, x.lo[2 * w + 1], alo);
-            ahi = sdot2((v >> 4) & 0x000F000Fu, x.hi[2 * w], ahi);
-            ahi = sdot2((v >> 12) & 0x000F000Fu, x.hi[2 * w + 1], ahi);
+            const uint32_t lo = q[w] & 0x0F0F0F0Fu;
+            const uint32_t hi = (q[w] >> 4) & 0x0F0F0F0Fu;
+            ah = dot4(lo, x.h[w], ah);
+            al = dot4(lo, x.l[w], al);
+            bh = dot4(hi, x.h[8 + w], bh);
+            bl = dot4(hi, x.l[8 + w], bl);
         }
+        const int A = (ah << 8) + al, B = (bh << 8) + bl;
         uint32_t sc0, m0, sc1, m1;
         const int i = g & 3;
-        q4k_scale_min(2 * i, r.h.y, r.h.z, r.h.w, sc0, m0);
-        q4k_scale_min(2 * i + 1, r.h.y, r.h.z, r.h.w, sc1, m1);
-        const float d = h2f((uint16_t)(r.h.x & 0xFFFFu));
-        const float dmin = h2f((uint16_t)(r.h.x >> 16));
-        const float a = __builtin_fmaf((float)sc0, (float)alo, (float)sc1 * (float)ahi);
-        const float b = __builtin_fmaf((float)m0, (float)x.slo, (float)m1 * (float)x.shi);
-        return __builtin_fmaf(d, a, -dmin * b) * x.scale;
+        q4k_scale_min(2 * i, r.hd.y, r.hd.z, r.hd.w, sc0, m0);
+        q4k_scale_min(2 * i + 1, r.hd.y, r.hd.z, r.hd.w, sc1, m1);
+        const float d = h2f((uint16_t)(r.hd.x & 0xFFFFu));
+        const float dmin = h2f((uint16_t)(r.hd.x >> 16));
+        const float p = __builtin_fmaf((float)sc0 * x.sa, (float)A, (float)sc1 * x.sb * (float)B);
+        const float m = __builtin_fmaf((float)m0, x.ssa, (float)m1 * x.ssb);
+        return __builtin_fmaf(d, p, -dmin * m);
     }
 };
 
@@ -126,55 +144,55 @@ template <> struct Q<kQ4_K> {
 template <> struct Q<kQ6_K> {
     static constexpr int GPB = 8;
     struct X {
-        uint32_t v[16];  // part p, dword w: [4p+2w] = (l0, l2), [4p+2w+1] = (l1, l3)
-        int s[4];
-        float scale;
+        uint32_t h[8], l[8];  // part p: [2p], [2p+1] = 8 activation digits
+        int S8[4];            // sum of x16 over the part's 8 positions
+        float s[4];           // group scale of the part's positions
     };
-    struct Raw { uint2 a, b, h, s; uint32_t d; };
-    __device__ static void load_x(const float *__restrict__ xrow, int g, X &x) {
+    // raw dwords of the 8-byte fields (3 aligned dwords each, funnel-shifted in dot()
+    // so that no arithmetic on loaded values sits between the loads and their use)
+    struct Raw { uint32_t a[3], b[3], hq[3], sc[3]; uint32_t sh, d; };
+    __device__ static void load_x(const XView &xv, int g, X &x) {
         const int b = g >> 3, gi = g & 7, n = gi >> 2, j = gi & 3;
-        const float *base = xrow + b * 256 + 128 * n + 8 * j;
-        float v[32];
-        float mx = 0.f;
 #pragma unroll
         for (int p = 0; p < 4; p++) {
-            const float4 f0 = *reinterpret_cast<const float4 *>(base + 32 * p);
-            const float4 f1 = *reinterpret_cast<const float4 *>(base + 32 * p + 4);
-            v[8 * p + 0] = f0.x; v[8 * p + 1] = f0.y; v[8 * p + 2] = f0.z; v[8 * p + 3] = f0.w;
-            v[8 * p + 4] = f1.x; v[8 * p + 5] = f1.y; v[8 * p + 6] = f1.z; v[8 * p + 7] = f1.w;
+            const int pos = 256 * b + 128 * n + 32 * p + 8 * j;
+            const uint2 vh = *reinterpret_cast<const uint2 *>(xv.xh + pos);
+            const uint2 vl = *reinterpret_cast<const uint2 *>(xv.xl + pos);
+            x.h[2 * p] = vh.x; x.h[2 * p + 1] = vh.y;
+            x.l[2 * p] = vl.x; x.l[2 * p + 1] = vl.y;
+            x.S8[p] = xv.S8[pos >> 3];
+            x.s[p] = xv.s[pos >> 5];
         }
-#pragma unroll
-        for (int i = 0; i < 32; i++) mx = fmaxf(mx, fabsf(v[i]));
-        const XQ qz(mx);
-        x.scale = qz.scale;
-#pragma unroll
-        for (int p = 0; p < 4; p++) {
-            int s = 0;
-#pragma unroll
-            for (int w = 0; w < 2; w++) {
-                const float *q = v + 8 * p + 4 * w;
-                x.v[4 * p + 2 * w] = qz.pack(q[0], q[2]);
-                x.v[4 * p + 2 * w + 1] = qz.pack(q[1], q[3]);
-                s = sdot2(x.v[4 * p + 2 * w], ONES, sdot2(x.v[4 * p + 2 * w + 1], ONES, s));
-            }
-            x.s[p] = s;
-        }
+    }
+    // 3 aligned dwords covering the 8 bytes at p (p 2-byte aligned; the third
+    // dword holds field bytes or, for dword-aligned p, bytes of the same block)
+    __device__ static void ld3(const uint8_t *p, uint32_t (&d)[3]) {
+        // pointer arithmetic (not an integer round trip) keeps the LDS address space visible
+        const uint32_t *q = reinterpret_cast<const uint32_t *>(p - (reinterpret_cast<uintptr_t>(p) & 3));
+        d[0] = q[0]; d[1] = q[1]; d[2] = q[2];
     }
     __device__ static Raw load(const uint8_t *__restrict__ row, int g) {
         const int b = g >> 3, gi = g & 7, n = gi >> 2, j = gi & 3;
         const uint8_t *blk = row + b * 210;
         Raw r;
-        r.a = load8_a2(blk + 64 * n + 8 * j);         // ql[l]     : q1 low nibble, q3 high
-        r.b = load8_a2(blk + 64 * n + 32 + 8 * j);    // ql[l+32]  : q2 low nibble, q4 high
-        r.h = load8_a2(blk + 128 + 32 * n + 8 * j);   // qh[l]     : 2 bits of each of q1..q4
-        r.s = load8_a2(blk + 192 + 8 * n);            // scales[8n .. 8n+7]
+        r.sh = (uint32_t)(reinterpret_cast<uintptr_t>(blk) & 2) << 3;  // every field shares the block's parity
+        ld3(blk + 64 * n + 8 * j, r.a);          // ql[l]    : part 0 low nibble, part 2 high
+        ld3(blk + 64 * n + 32 + 8 * j, r.b);     // ql[l+32] : part 1 low nibble, part 3 high
+        ld3(blk + 128 + 32 * n + 8 * j, r.hq);   // qh[l]    : 2 bits of each part
+        ld3(blk + 192 + 8 * n, r.sc);            // scales[8n .. 8n+7]
         r.d = ld_u16(blk + 208);
         return r;
     }
     __device__ static float dot(const Raw &r, int g, const X &x) {
-        const int is = ((g & 7) & 3) >> 1;
-        int acc[4] = {0, 0, 0, 0};
-        const uint32_t A[2] = {r.a.x, r.a.y}, B[2] = {r.b.x, r.b.y}, H[2] = {r.h.x, r.h.y};
+#ifdef MX_FAKE_DOT
+        return (float)(r.a[0] ^ r.a[1] ^ r.a[2] ^ r.b[0] ^ r.b[1] ^ r.b[2] ^ r.hq[0] ^ r.hq[1] ^ r.hq[2] ^ r.sc[0] ^ r.sc[1] ^ r.sc[2] ^ r.d ^ x.h[0]);
+#endif
+        const int jh = ((g & 7) & 3) >> 1;  // scale byte is scales[8n + jh + 2p]
+        int hacc[4] = {0, 0, 0, 0}, lacc[4] = {0, 0, 0, 0};
+        auto fun = [&](const uint32_t (&d)[3], int w) { return __builtin_amdgcn_alignbit(d[w + 1], d[w], r.sh); };
+        const uint32_t A[2] = {fun(r.a, 0), fun(r.a, 1)}, B[2] = {fun(r.b, 0), fun(r.b, 1)},
+                       H[2] = {fun(r.hq, 0), fun(r.hq, 1)};
+        const uint32_t SC[2] = {fun(r.sc, 0), fun(r.sc, 1)};
 #pragma unroll
         for (int w = 0; w < 2; w++) {
             const uint32_t qp[4] = {
@@ -184,76 +202,64 @@ template <> struct Q<kQ6_K> {
                 ((B[w] >> 4) & 0x0F0F0F0Fu) | ((H[w] >> 2) & 0x30303030u)};
 #pragma unroll
             for (int p = 0; p < 4; p++) {
-                acc[p] = sdot2(qp[p] & 0x003F003Fu, x.v[4 * p + 2 * w], acc[p]);
-                acc[p] = sdot2((qp[p] >> 8) & 0x003F003Fu, x.v[4 * p + 2 * w + 1], acc[p]);
+                hacc[p] = dot4(qp[p], x.h[2 * p + w], hacc[p]);
+                lacc[p] = dot4(qp[p], x.l[2 * p + w], lacc[p]);
             }
         }
         float tot = 0.f;
 #pragma unroll
         for (int p = 0; p < 4; p++) {
-            const int byte = is + 2 * p;  // scales[8n + is + 2p]
-            const uint32_t src = byte < 4 ? r.s.x : r.s.y;
-            const float sc = (float)(int8_t)((src >> (8 * (byte & 3))) & 0xFFu);
-            tot = __builtin_fmaf(sc, (float)(acc[p] - 32 * x.s[p]), tot);  // sum (q - 32) x, exact in int32
+            const uint32_t src = SC[p >> 1];
+            const int sc = (int)(int8_t)((src >> (8 * (jh + 2 * (p & 1)))) & 0xFFu);
+            const int acc = (hacc[p] << 8) + lacc[p] - 32 * x.S8[p];  // sum (q - 32) x16, exact
+            tot = __builtin_fmaf((float)sc * x.s[p], (float)acc, tot);
         }
-        return h2f((uint16_t)r.d) * tot * x.scale;
+        return h2f((uint16_t)r.d) * tot;
     }
 };
 
 // ---- Q8_0 -------------------------------------------------------------------------
 template <> struct Q<kQ8_0> {
     static constexpr int GPB = 1;
-    struct X { uint32_t v[16]; int s; float scale; };
-    struct Raw { uint2 q[4]; uint32_t d; };
-    __device__ static void load_x(const float *__restrict__ xrow, int g, X &x) {
-        float v[32];
-        const float4 *p = reinterpret_cast<const float4 *>(xrow + 32 * g);
-        float mx = 0.f;
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const float4 f = p[i];
-            v[4 * i] = f.x; v[4 * i + 1] = f.y; v[4 * i + 2] = f.z; v[4 * i + 3] = f.w;
-            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(f.x), fabsf(f.y)), fmaxf(fabsf(f.z), fabsf(f.w))));
-        }
-        const XQ qz(mx);
-        x.scale = qz.scale;
-        int s = 0;
-#pragma unroll
-        for (int w = 0; w < 8; w++) {
-            x.v[2 * w] = qz.pack(v[4 * w], v[4 * w + 2]);
-            x.v[2 * w + 1] = qz.pack(v[4 * w + 1], v[4 * w + 3]);
-            s = sdot2(x.v[2 * w], ONES, sdot2(x.v[2 * w + 1], ONES, s));
-        }
-        x.s = s;
+    struct X { uint32_t h[8], l[8]; float s; };
+    struct Raw { uint32_t q[9]; uint32_t sh, d; };
+    __device__ static void load_x(const XView &xv, int g, X &x) {
+        lds_words(xv.xh + 32 * g, x.h, 2);
+        lds_words(xv.xl + 32 * g, x.l, 2);
+        x.s = xv.s[g];
     }
     __device__ static Raw load(const uint8_t *__restrict__ row, int g) {
         const uint8_t *blk = row + g * 34;
+        const uint8_t *qs = blk + 2;
+        const uintptr_t mis = reinterpret_cast<uintptr_t>(qs) & 3;
+        const uint32_t *p = reinterpret_cast<const uint32_t *>(qs - mis);
         Raw r;
+        r.sh = (uint32_t)(mis & 2) << 3;
 #pragma unroll
-        for (int i = 0; i < 4; i++) r.q[i] = load8_a2(blk + 2 + 8 * i);
+        for (int i = 0; i < 8; i++) r.q[i] = p[i];
+        r.q[8] = p[8];  // LDS: the dword past the block is padding or the next block
         r.d = ld_u16(blk);
         return r;
     }
     __device__ static float dot(const Raw &r, int, const X &x) {
-        int acc = 0;
+        int ah = 0, al = 0;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-#pragma unroll
-            for (int h = 0; h < 2; h++) {
-                const uint32_t u = (h ? r.q[i].y : r.q[i].x) ^ 0x80808080u;  // q + 128, unsigned
-                const int w = 2 * i + h;
-                acc = sdot2(u & 0x00FF00FFu, x.v[2 * w], acc);
-                acc = sdot2((u >> 8) & 0x00FF00FFu, x.v[2 * w + 1], acc);
-            }
+        for (int w = 0; w < 8; w++) {
+            const uint32_t v = __builtin_amdgcn_alignbit(r.q[w + 1], r.q[w], r.sh);
+            ah = dot4(v, x.h[w], ah);
+            al = dot4(v, x.l[w], al);
         }
-        return h2f((uint16_t)r.d) * (float)(acc - 128 * x.s) * x.scale;  // sum (u - 128) x
+        return h2f((uint16_t)r.d) * (x.s * (float)((ah << 8) + al));
     }
 };
 
 // ---- lane geometry ----------------------------------------------------------------------
 // P = largest power of two <= 64 dividing the row's group count G; if that leaves
 // more than NG_MAX groups per lane, P = 64 with the tail groups masked.
-constexpr int NG_MAX = 8;
+#ifndef MX_NG_MAX
+#define MX_NG_MAX 8
+#endif
+constexpr int NG_MAX = MX_NG_MAX;
 
 template <int DT> struct Geo {
     int G, P, NG, RPI;
@@ -315,66 +321,89 @@ __device__ __forceinline__ void reduce_tuples(float (&v)[NB][NM], int P, int sub
 }
 
 // Streams the rows [r_begin, r_end) of NM matrices that share one activation
-// through this wave, NB row-iterations (NB * RPI rows) per batch.  The first
-// batch's weight loads are issued before `xload` fills `xs` (so the activation
-// load and quantisation overlap them), and each batch's loads are issued before
-// the previous batch is reduced and published.  sink(row, sums[NM]) runs once
-// per row with the fully reduced sums.
-template <int DT, int NG, int NB, int NM, class XLoad, class Sink>
+// through this wave, NIT row-iterations (NIT * RPI rows) per batch, through the
+// wave's LDS ring `ring` of RING buffers of ni KB (ni = dma_insts(NM, rows per
+// batch, row_bytes)): batches i+1 .. i+RING-1 are in flight while batch i is
+// computed.  A batch's image in a buffer is the NM matrices' row spans, each
+// as the aligned 16-byte chunks covering it, packed back to back.  `pre`
+// issues the activation loads before the first copies, `post` finishes filling
+// `xs`.  sink(row, sums[NM]) runs once per row with the fully reduced sums.
+template <int DT, int NG, int NIT, int NM, int RING, class XPreF, class XPostF, class Sink>
 __device__ __forceinline__ void stream_rows(const uint8_t *const (&w)[NM], int64_t row_bytes, const Geo<DT> &geo,
-                                            typename Q<DT>::X (&xs)[NG], int r_begin, int r_end, XLoad &&xload,
-                                            Sink &&sink) {
+                                            typename Q<DT>::X (&xs)[NG], int r_begin, int r_end, uint8_t *ring,
+                                            int ni, XPreF &&pre, XPostF &&post, Sink &&sink) {
     const int lane = threadIdx.x & 63;
     const int sub = lane & (geo.P - 1);
     const int rsub = lane / geo.P;
-    const int step = NB * geo.RPI;
-    typename Q<DT>::Raw raw[NM][NB][NG];
-    auto issue = [&](int r0) {
+    const int step = NIT * geo.RPI;
+    const int bstride = ni * 1024;
+    const int nbatch = (r_end - r_begin + step - 1) / step;
+    // the chunk range [base_m, base_m + 16 * nch_m) of matrix m's span for the batch at r0
+    auto span = [&](int m, int r0, uintptr_t &base, int &nch) {
+        const int r1 = min(r0 + step, r_end);
+        const uintptr_t S = reinterpret_cast<uintptr_t>(w[m] + (int64_t)r0 * row_bytes);
+        const uintptr_t E = reinterpret_cast<uintptr_t>(w[m] + (int64_t)r1 * row_bytes);
+        base = S & ~uintptr_t(15);
+        nch = (int)((E + 15 - base) >> 4);
+    };
+    auto issue = [&](int bi) {
+        const int r0 = r_begin + bi * step;
+        uintptr_t base[NM];
+        int nch[NM];
 #pragma unroll
-        for (int ib = 0; ib < NB; ib++) {
-            const int row = r0 + rsub + geo.RPI * ib;
-            if (row < r_end) {
-                const int64_t off = (int64_t)row * row_bytes;
+        for (int m = 0; m < NM; m++) span(m, r0, base[m], nch[m]);
+        int tot = 0;
 #pragma unroll
-                for (int jg = 0; jg < NG; jg++) {
-                    const int g = sub + geo.P * jg;
-#pragma unroll
-                    for (int m = 0; m < NM; m++) raw[m][ib][jg] = Q<DT>::load(w[m] + off, g < geo.G ? g : 0);
-                }
+        for (int m = 0; m < NM; m++) tot += nch[m];
+        uint8_t *dst = ring + (bi % RING) * bstride;
+        for (int j = 0; j < ni; j++) {
+            int ci = min(64 * j + lane, tot - 1);  // spare lanes re-copy the last chunk
+            uintptr_t src = base[0] + 16 * (uintptr_t)ci;
+            if (NM > 1) {
+                if (ci >= nch[0]) src = base[1] + 16 * (uintptr_t)(ci - nch[0]);
             }
+            dma16(reinterpret_cast<const uint8_t *>(src), dst + 1024 * j);
         }
     };
-    int r0 = r_begin;
-    issue(r0);
-    xload();
-    while (true) {
-        float acc[NB][NM];
+    // LDS address of row `row` of matrix m in the buffer of batch bi
+    auto row_at = [&](int bi, int m, int row) -> const uint8_t * {
+        const int r0 = r_begin + bi * step;
+        uintptr_t base0, base1 = 0;
+        int n0, n1 = 0;
+        span(0, r0, base0, n0);
+        if (NM > 1 && m == 1) span(1, r0, base1, n1);
+        const uintptr_t rp = reinterpret_cast<uintptr_t>(w[m] + (int64_t)row * row_bytes);
+        const uintptr_t off = m == 0 ? rp - base0 : 16 * (uintptr_t)n0 + (rp - base1);
+        return ring + (bi % RING) * bstride + off;
+    };
+    auto process = [&](int bi) {
+        const int r0 = r_begin + bi * step;
+        float acc[NIT][NM];
 #pragma unroll
-        for (int ib = 0; ib < NB; ib++) {
-            const bool ok = r0 + rsub + geo.RPI * ib < r_end;
+        for (int ib = 0; ib < NIT; ib++) {
+            const int row = r0 + rsub + geo.RPI * ib;
+            const bool ok = row < r_end;
 #pragma unroll
             for (int m = 0; m < NM; m++) {
                 float a = 0.f;
                 if (ok) {
+                    const uint8_t *rl = row_at(bi, m, row);
 #pragma unroll
                     for (int jg = 0; jg < NG; jg++) {
                         const int g = sub + geo.P * jg;
-                        if (NG == 1 || g < geo.G) a += Q<DT>::dot(raw[m][ib][jg], g, xs[jg]);
+                        if (NG == 1 || g < geo.G) a += Q<DT>::dot(Q<DT>::load(rl, g), g, xs[jg]);
                     }
                 }
                 acc[ib][m] = a;
             }
         }
-        const int r_next = r0 + step;
-        const bool more = r_next < r_end;
-        if (more) issue(r_next);
         int which;
         bool leader;
-        reduce_tuples<NM, NB>(acc, geo.P, sub, which, leader);
+        reduce_tuples<NM, NIT>(acc, geo.P, sub, which, leader);
         if (leader) {
-            if (geo.P < NB) {
+            if (geo.P < NIT) {
 #pragma unroll
-                for (int ib = 0; ib < NB; ib++) {
+                for (int ib = 0; ib < NIT; ib++) {
                     const int row = r0 + rsub + geo.RPI * ib;
                     if (row < r_end) sink(row, acc[ib]);
                 }
@@ -383,33 +412,73 @@ __device__ __forceinline__ void stream_rows(const uint8_t *const (&w)[NM], int64
                 if (row < r_end) sink(row, acc[0]);
             }
         }
-        if (!more) break;
-        r0 = r_next;
+    };
+    pre();
+    for (int bi = 0; bi < RING - 1 && bi < nbatch; bi++) issue(bi);
+    post();
+    for (int bi = 0; bi < nbatch; bi++) {
+        if (bi + RING - 1 < nbatch) issue(bi + RING - 1);
+        // batch bi has landed once at most the copies of the later batches are outstanding
+        wait_vmcnt(ni * min(RING - 1, nbatch - 1 - bi));
+        process(bi);
     }
 }
 
+// Loads this lane's slices of a staged activation row (global memory or LDS).
 template <int DT, int NG>
-__device__ __forceinline__ void load_xs(const float *__restrict__ xrow, const Geo<DT> &geo,
+__device__ __forceinline__ void load_xs(const uint8_t *staged, int k, const Geo<DT> &geo,
                                         typename Q<DT>::X (&xs)[NG]) {
+    const XView xv(staged, k);
     const int sub = (threadIdx.x & 63) & (geo.P - 1);
 #pragma unroll
     for (int jg = 0; jg < NG; jg++) {
         const int g = sub + geo.P * jg;
-        Q<DT>::load_x(xrow, g < geo.G ? g : 0, xs[jg]);
+        Q<DT>::load_x(xv, g < geo.G ? g : 0, xs[jg]);
     }
 }
 
-constexpr int WAVES = 4;
-// rows per wave: generic mat-vec, fused gate/up (activation reused by 2 matrices),
-// fused down (every projection of a down tile shares one row tiling)
-constexpr int RW_MV = 16, RW_GU = 4, RW_DN = 16;
+#ifndef MX_WAVES
+#define MX_WAVES 4
+#endif
+// rows per wave and LDS ring depth per kernel (tuned on MI355X for the C1 layer)
+#ifndef MX_RW_GU
+#define MX_RW_GU 1
+#endif
+#ifndef MX_RING_GU
+#define MX_RING_GU 1
+#endif
+#ifndef MX_RW_DN
+#define MX_RW_DN 16
+#endif
+#ifndef MX_RING_DN
+#define MX_RING_DN 1
+#endif
+#ifndef MX_NIT1
+#define MX_NIT1 1
+#endif
+#ifndef MX_NIT2
+#define MX_NIT2 1
+#endif
+constexpr int WAVES = MX_WAVES;
+constexpr int RW_MV = 16, RW_GU = MX_RW_GU, RW_DN = MX_RW_DN;
+constexpr int RING_MV = 2, RING_GU = MX_RING_GU, RING_DN = MX_RING_DN;
 
-// NB (row-iterations per batch): keep ~4-8 row-loads per matrix in flight
-template <int NG, int NM> struct Batch { static constexpr int NB = NG == 1 ? 4 : (NG <= 4 ? 2 : 1); };
+// row-iterations per batch: NIT * RPI rows are copied per DMA batch
+template <int NG> struct Batch { static constexpr int NIT = NG == 1 ? MX_NIT1 : MX_NIT2; };
+
+// DMA instructions per batch for NM matrices of row_bytes rows at k
+template <int DT, int NG>
+static int ring_insts(int nm, int k, int64_t row_bytes) {
+    return dma_insts(nm, Batch<NG>::NIT * Geo<DT>(k).RPI, row_bytes);
+}
+__host__ __device__ inline size_t align16(size_t v) { return (v + 15) & ~size_t(15); }
 
 // ---- mul_mv_id -----------------------------------------------------------------------
+// grid (row tiles, t * top_k); one (token, slot) pair per block, its activation
+// row staged into LDS by the whole block, then one LDS ring per wave.
 template <int DT, int NG>
-__global__ void __launch_bounds__(64 * WAVES) k_mul_mv_id(MvArgs a) {
+__global__ void __launch_bounds__(64 * WAVES) k_mul_mv_id(MvArgs a, int ni) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int pair = blockIdx.y;  // token * top_k + slot
     const int tok = pair / a.top_k, slot = pair % a.top_k;
     int e = 0;
@@ -419,13 +488,24 @@ __global__ void __launch_bounds__(64 * WAVES) k_mul_mv_id(MvArgs a) {
     }
     const float *xrow = a.x + ((int64_t)tok * a.x_per_row + (a.x_per_row == 1 ? 0 : slot)) * a.k;
     const uint8_t *const w[1] = {a.w + (int64_t)e * a.expert_bytes};
-    const int r0 = blockIdx.x * (WAVES * RW_MV) + (threadIdx.x >> 6) * RW_MV;
-    if (r0 >= a.n_out) return;  // wave-uniform; no block barrier in this kernel
+    const int wave = threadIdx.x >> 6;
+    const int r0 = blockIdx.x * (WAVES * RW_MV) + wave * RW_MV;
     const Geo<DT> geo(a.k);
     typename Q<DT>::X xs[NG];
+    XPre xp;
+    uint8_t *ring = lds + align16(xstage_bytes(a.k)) + wave * (RING_MV * ni * 1024);
+    if (r0 >= a.n_out) {  // wave-uniform: take part in the staging, then leave
+        stage_pre(xrow, a.k, xp);
+        stage_post(xrow, a.k, xp, lds);
+        return;
+    }
     float *dst = a.dst + (int64_t)pair * a.n_out;
-    stream_rows<DT, NG, Batch<NG, 1>::NB, 1>(
-        w, a.row_bytes, geo, xs, r0, min(r0 + RW_MV, a.n_out), [&] { load_xs<DT, NG>(xrow, geo, xs); },
+    stream_rows<DT, NG, Batch<NG>::NIT, 1, RING_MV>(
+        w, a.row_bytes, geo, xs, r0, min(r0 + RW_MV, a.n_out), ring, ni, [&] { stage_pre(xrow, a.k, xp); },
+        [&] {
+            stage_post(xrow, a.k, xp, lds);
+            load_xs<DT, NG>(lds, a.k, geo, xs);
+        },
         [&](int row, const float (&s)[1]) { dst[row] = s[0]; });
 }
 
@@ -439,37 +519,53 @@ __global__ void __launch_bounds__(64 * WAVES) k_mul_mv_id(MvArgs a) {
     default: MACRO(8); break;   \
     }
 
+template <int DT, int NG>
+static mx_status launch_mv_ng(const MvArgs &a, dim3 grid, hipStream_t s) {
+    const int ni = ring_insts<DT, NG>(1, a.k, a.row_bytes);
+    if (ni > DMA_MAX_INSTS) return fail(MX_ERR_SHAPE, "mul_mv_id: rows of %lld bytes are too long", (long long)a.row_bytes);
+    const size_t lds = align16(xstage_bytes(a.k)) + (size_t)WAVES * RING_MV * ni * 1024;
+    if (lds > 160 * 1024) return fail(MX_ERR_SHAPE, "mul_mv_id: k = %d needs %zu bytes of LDS", a.k, lds);
+    hipLaunchKernelGGL((k_mul_mv_id<DT, NG>), grid, dim3(64 * WAVES), lds, s, a, ni);
+    return MX_OK;
+}
+
 template <int DT>
-static void launch_mv_dt(const MvArgs &a, dim3 grid, hipStream_t s) {
+static mx_status launch_mv_dt(const MvArgs &a, dim3 grid, hipStream_t s) {
     const int ng = ng_variant(Geo<DT>(a.k).NG);
-#define MX_L(N) hipLaunchKernelGGL((k_mul_mv_id<DT, N>), grid, dim3(64 * WAVES), 0, s, a)
+#define MX_L(N) return launch_mv_ng<DT, N>(a, grid, s)
     MX_NG_SWITCH(ng, MX_L)
 #undef MX_L
+    return MX_OK;
 }
 
 mx_status launch_mul_mv_id(int dtype, const MvArgs &a, hipStream_t s) {
     const dim3 grid((unsigned)((a.n_out + WAVES * RW_MV - 1) / (WAVES * RW_MV)), (unsigned)(a.t * a.top_k));
     if (grid.y == 0 || grid.x == 0) return MX_OK;
+    if (a.k % 32) return fail(MX_ERR_BLOCK, "mul_mv_id: k must be a multiple of 32");
     switch (dtype) {
-    case kQ4_K: launch_mv_dt<kQ4_K>(a, grid, s); break;
-    case kQ6_K: launch_mv_dt<kQ6_K>(a, grid, s); break;
-    default: launch_mv_dt<kQ8_0>(a, grid, s); break;
+    case kQ4_K: MX_TRY(launch_mv_dt<kQ4_K>(a, grid, s)); break;
+    case kQ6_K: MX_TRY(launch_mv_dt<kQ6_K>(a, grid, s)); break;
+    default: MX_TRY(launch_mv_dt<kQ8_0>(a, grid, s)); break;
     }
     MX_LAUNCH("k_mul_mv_id");
     return MX_OK;
 }
 
 // ---- fused decode: gate/up + SwiGLU ---------------------------------------------------
-// grid (ff / 64, slots, t); slot top_k (if present) is the shared expert, which
-// then has the routed experts' quant type and shape.
+// grid (ff / (WAVES * RW_GU), slots, t); slot top_k (if present) is the shared
+// expert, which then has the routed experts' quant type and shape.
 // act[tok, slot, r] = silu(gate_r . x) * (up_r . x), silu(g) = g / (1 + exp(-g)),
-// the product rounded on its own (silu_mul.metal:57-72).
+// the product rounded on its own (silu_mul.metal:57-72).  The token row comes
+// staged from the router kernel (global memory).  Waves are independent.
 template <int DT, int NG>
-__global__ void __launch_bounds__(64 * WAVES) k_decode_gate_up(DecodeGateUpArgs a) {
+__global__ void __launch_bounds__(64 * WAVES) k_decode_gate_up(DecodeGateUpArgs a, int ni) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int slot = blockIdx.y, tok = blockIdx.z;
-    const int r0 = blockIdx.x * (WAVES * RW_GU) + (threadIdx.x >> 6) * RW_GU;
-    if (r0 >= a.ff) return;
+    const int wave = threadIdx.x >> 6;
+    const int r0 = blockIdx.x * (WAVES * RW_GU) + wave * RW_GU;
+    if (r0 >= a.ff) return;  // wave-uniform; no block barrier in this kernel
     const int slots = a.top_k + (a.sh_gate ? 1 : 0);
+    float *act = a.act + ((int64_t)tok * slots + slot) * a.ff;
     const uint8_t *gw, *uw;
     int64_t rb;
     if (slot < a.top_k) {
@@ -486,55 +582,74 @@ __global__ void __launch_bounds__(64 * WAVES) k_decode_gate_up(DecodeGateUpArgs 
     const uint8_t *const w[2] = {gw, uw};
     const Geo<DT> geo(a.hidden);
     typename Q<DT>::X xs[NG];
-    float *act = a.act + ((int64_t)tok * slots + slot) * a.ff;
-    const float *xrow = a.x + (int64_t)tok * a.hidden;
-    stream_rows<DT, NG, Batch<NG, 2>::NB, 2>(w, rb, geo, xs, r0, min(r0 + RW_GU, a.ff),
-                                             [&] { load_xs<DT, NG>(xrow, geo, xs); },
-                                             [&](int row, const float (&s)[2]) {
-                                                 const float g = s[0];
-                                                 const float sg = g / (1.0f + expf(-g));
-                                                 act[row] = sg * s[1];
-                                             });
+    const uint8_t *staged = a.xstage + (int64_t)tok * xstage_bytes(a.hidden);
+    uint8_t *ring = lds + wave * (RING_GU * ni * 1024);
+    stream_rows<DT, NG, Batch<NG>::NIT, 2, RING_GU>(w, rb, geo, xs, r0, min(r0 + RW_GU, a.ff), ring, ni,
+                                                     [&] { load_xs<DT, NG>(staged, a.hidden, geo, xs); }, [] {},
+                                                     [&](int row, const float (&s)[2]) {
+                                                         const float g = s[0];
+                                                         const float sg = g / (1.0f + expf(-g));
+                                                         act[row] = sg * s[1];
+                                                     });
+}
+
+template <int DT, int NG>
+static mx_status launch_gu_ng(const DecodeGateUpArgs &a, dim3 grid, hipStream_t s) {
+    const int ni = ring_insts<DT, NG>(2, a.hidden, a.gu_row_bytes);
+    if (ni > DMA_MAX_INSTS) return fail(MX_ERR_SHAPE, "decode gate/up: rows too long for the LDS ring");
+    const size_t lds = (size_t)WAVES * RING_GU * ni * 1024;
+    if (lds > 160 * 1024) return fail(MX_ERR_SHAPE, "decode gate/up: hidden = %d needs %zu bytes of LDS", a.hidden, lds);
+    hipLaunchKernelGGL((k_decode_gate_up<DT, NG>), grid, dim3(64 * WAVES), lds, s, a, ni);
+    return MX_OK;
 }
 
 template <int DT>
-static void launch_gu_dt(const DecodeGateUpArgs &a, dim3 grid, hipStream_t s) {
+static mx_status launch_gu_dt(const DecodeGateUpArgs &a, dim3 grid, hipStream_t s) {
     const int ng = ng_variant(Geo<DT>(a.hidden).NG);
-#define MX_L(N) hipLaunchKernelGGL((k_decode_gate_up<DT, N>), grid, dim3(64 * WAVES), 0, s, a)
+#define MX_L(N) return launch_gu_ng<DT, N>(a, grid, s)
     MX_NG_SWITCH(ng, MX_L)
 #undef MX_L
+    return MX_OK;
 }
 
 mx_status launch_decode_gate_up(int dtype, const DecodeGateUpArgs &a, hipStream_t s) {
     const dim3 grid((unsigned)((a.ff + WAVES * RW_GU - 1) / (WAVES * RW_GU)),
                     (unsigned)(a.top_k + (a.sh_gate ? 1 : 0)), (unsigned)a.t);
     if (grid.x == 0 || a.t == 0) return MX_OK;
+    if (a.hidden % 32) return fail(MX_ERR_BLOCK, "decode gate/up: hidden must be a multiple of 32");
+    if (a.sh_gate && a.sh_row_bytes != a.gu_row_bytes)
+        return fail(MX_ERR_SHAPE, "decode gate/up: shared expert rows must match the routed rows");
     switch (dtype) {
-    case kQ4_K: launch_gu_dt<kQ4_K>(a, grid, s); break;
-    case kQ6_K: launch_gu_dt<kQ6_K>(a, grid, s); break;
-    default: launch_gu_dt<kQ8_0>(a, grid, s); break;
+    case kQ4_K: MX_TRY(launch_gu_dt<kQ4_K>(a, grid, s)); break;
+    case kQ6_K: MX_TRY(launch_gu_dt<kQ6_K>(a, grid, s)); break;
+    default: MX_TRY(launch_gu_dt<kQ8_0>(a, grid, s)); break;
     }
     MX_LAUNCH("k_decode_gate_up");
     return MX_OK;
 }
 
 // ---- fused decode: down (one slot per block) + last-block weighted combine ---------------
-// grid (hidden / 64, n_slot_blocks, t).  Each block writes its slot's 64 down rows
-// to part[tok, slot, :]; the last of the n_slot_blocks blocks of a (tok, row tile)
-// to finish (device-scope counter) combines them in slot order:
+// grid (hidden / (WAVES * RW_DN), n_slot_blocks, t).  Each block writes its slot's
+// down rows to part[tok, slot, :]; the last of the n_slot_blocks blocks of a
+// (tok, row tile) to finish (device-scope counter) combines them in slot order:
 //   out[c] = residual[c] + ( sum_k w[k] * part[k][c] + part[shared][c] )
 // (combine.metal:70-97, moe.rs:73-78, model.rs:351) and resets the counter.  When
 // the shared expert has another quant type than the routed experts, the host
 // computes it separately and passes it as a.shared_out (a.sh_down == NULL).
 template <int DT, int NG>
-__global__ void __launch_bounds__(64 * WAVES) k_decode_down(DecodeDownArgs a) {
+__global__ void __launch_bounds__(64 * WAVES) k_decode_down(DecodeDownArgs a, int ni) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     __shared__ int s_last;
     const int slot = blockIdx.y, tok = blockIdx.z;
     constexpr int ROWS_PER_WG = WAVES * RW_DN;
     const int tile0 = blockIdx.x * ROWS_PER_WG;
-    const int r0 = tile0 + (threadIdx.x >> 6) * RW_DN;
+    const int wave = threadIdx.x >> 6;
+    const int r0 = tile0 + wave * RW_DN;
     const int slots = a.top_k + (a.sh_down ? 1 : 0);
-    if (r0 < a.hidden) {  // wave-uniform; the barrier below is reached by every wave
+    const float *xrow = a.act + ((int64_t)tok * slots + slot) * a.ff;
+    uint8_t *ring = lds + align16(xstage_bytes(a.ff)) + wave * (RING_DN * ni * 1024);
+    XPre xp;
+    if (r0 < a.hidden) {  // wave-uniform; every wave takes part in the staging barrier
         const uint8_t *wp;
         int64_t rb;
         if (slot < a.top_k) {
@@ -549,11 +664,17 @@ __global__ void __launch_bounds__(64 * WAVES) k_decode_down(DecodeDownArgs a) {
         const uint8_t *const w[1] = {wp};
         const Geo<DT> geo(a.ff);
         typename Q<DT>::X xs[NG];
-        const float *xrow = a.act + ((int64_t)tok * slots + slot) * a.ff;
         float *part = a.part + ((int64_t)tok * slots + slot) * a.hidden;
-        stream_rows<DT, NG, Batch<NG, 1>::NB, 1>(w, rb, geo, xs, r0, min(r0 + RW_DN, a.hidden),
-                                                 [&] { load_xs<DT, NG>(xrow, geo, xs); },
-                                                 [&](int row, const float (&s)[1]) { st_agent(part + row, s[0]); });
+        stream_rows<DT, NG, Batch<NG>::NIT, 1, RING_DN>(w, rb, geo, xs, r0, min(r0 + RW_DN, a.hidden), ring, ni,
+                                                         [&] { stage_pre(xrow, a.ff, xp); },
+                                                         [&] {
+                                                             stage_post(xrow, a.ff, xp, lds);
+                                                             load_xs<DT, NG>(lds, a.ff, geo, xs);
+                                                         },
+                                                         [&](int row, const float (&s)[1]) { st_agent(part + row, s[0]); });
+    } else {
+        stage_pre(xrow, a.ff, xp);
+        stage_post(xrow, a.ff, xp, lds);
     }
     // publish this block's partial rows (completed agent-coherent stores), then count in
     drain_vmem();
@@ -578,12 +699,23 @@ __global__ void __launch_bounds__(64 * WAVES) k_decode_down(DecodeDownArgs a) {
     if (threadIdx.x == 0) reset_counter(counter);
 }
 
+template <int DT, int NG>
+static mx_status launch_dn_ng(const DecodeDownArgs &a, dim3 grid, hipStream_t s) {
+    const int ni = ring_insts<DT, NG>(1, a.ff, a.d_row_bytes);
+    if (ni > DMA_MAX_INSTS) return fail(MX_ERR_SHAPE, "decode down: rows too long for the LDS ring");
+    const size_t lds = align16(xstage_bytes(a.ff)) + (size_t)WAVES * RING_DN * ni * 1024;
+    if (lds > 160 * 1024) return fail(MX_ERR_SHAPE, "decode down: expert_ff = %d needs %zu bytes of LDS", a.ff, lds);
+    hipLaunchKernelGGL((k_decode_down<DT, NG>), grid, dim3(64 * WAVES), lds, s, a, ni);
+    return MX_OK;
+}
+
 template <int DT>
-static void launch_dn_dt(const DecodeDownArgs &a, dim3 grid, hipStream_t s) {
+static mx_status launch_dn_dt(const DecodeDownArgs &a, dim3 grid, hipStream_t s) {
     const int ng = ng_variant(Geo<DT>(a.ff).NG);
-#define MX_L(N) hipLaunchKernelGGL((k_decode_down<DT, N>), grid, dim3(64 * WAVES), 0, s, a)
+#define MX_L(N) return launch_dn_ng<DT, N>(a, grid, s)
     MX_NG_SWITCH(ng, MX_L)
 #undef MX_L
+    return MX_OK;
 }
 
 size_t decode_down_counter_words(int t, int hidden) {
@@ -594,10 +726,13 @@ mx_status launch_decode_down(int dtype, const DecodeDownArgs &a, hipStream_t s) 
     const dim3 grid((unsigned)((a.hidden + WAVES * RW_DN - 1) / (WAVES * RW_DN)),
                     (unsigned)(a.top_k + (a.sh_down ? 1 : 0)), (unsigned)a.t);
     if (grid.x == 0 || a.t == 0) return MX_OK;
+    if (a.ff % 32) return fail(MX_ERR_BLOCK, "decode down: expert_ff must be a multiple of 32");
+    if (a.sh_down && a.sh_row_bytes != a.d_row_bytes)
+        return fail(MX_ERR_SHAPE, "decode down: shared expert rows must match the routed rows");
     switch (dtype) {
-    case kQ4_K: launch_dn_dt<kQ4_K>(a, grid, s); break;
-    case kQ6_K: launch_dn_dt<kQ6_K>(a, grid, s); break;
-    default: launch_dn_dt<kQ8_0>(a, grid, s); break;
+    case kQ4_K: MX_TRY(launch_dn_dt<kQ4_K>(a, grid, s)); break;
+    case kQ6_K: MX_TRY(launch_dn_dt<kQ6_K>(a, grid, s)); break;
+    default: MX_TRY(launch_dn_dt<kQ8_0>(a, grid, s)); break;
     }
     MX_LAUNCH("k_decode_down");
     return MX_OK;

@@ -13,6 +13,7 @@
 // fully coalesced 16-byte loads; the reference transposes it at load time for
 // its matmul (moe.rs:43), which this layout makes unnecessary.
 #include "mx_launch.h"
+#include "mx_stage.h"
 
 namespace mx {
 
@@ -20,39 +21,61 @@ constexpr int RT_THREADS = 256;
 constexpr int RT_MAX_E = 1024;
 constexpr int RT_MAX_K = 32;
 
-// Block-wide stable top-k for one token, by rank: expert e's rank is the number
-// of experts whose selection score is larger, or equal with a lower id -- exactly
-// its position in a stable descending sort.  `logits` may be in shared or global
-// memory; all RT_THREADS threads must call.
+// Sort key of a stable descending sort on the selection score: the score's
+// bits mapped to an unsigned order (-0 folded to +0 first, so equal floats get
+// equal keys) in the high word, the complemented expert id in the low word
+// (equal scores -> the lower id ranks first).  Larger key = earlier position.
+__device__ __forceinline__ uint64_t sel_key(float v, int e) {
+    v = v + 0.0f;  // -0 -> +0
+    const uint32_t b = __float_as_uint(v);
+    const uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((uint64_t)o << 32) | (uint32_t)(~(uint32_t)e);
+}
+
+// Block-wide stable top-k for one token.  Each expert's position in the stable
+// descending order is its rank: the number of experts with a larger key.  The
+// keys sit in LDS and every thread counts against all of them with 16-byte
+// broadcast reads (independent, so they pipeline).  `logits` may be in shared
+// or global memory; all RT_THREADS threads must call.
 __device__ void select_token(const float *logits, const float *__restrict__ bias, int n_expert, int top_k,
                              float scale, int apply_scale, int norm, uint32_t *__restrict__ ids_out,
                              float *__restrict__ w_out) {
-    __shared__ float s_sel[RT_MAX_E];
+    constexpr int PER = RT_MAX_E / RT_THREADS;
+    __shared__ __attribute__((aligned(16))) uint64_t s_key[RT_MAX_E];
     __shared__ float s_prob[RT_MAX_K];
     __shared__ int s_pick[RT_MAX_K];
     const int tid = threadIdx.x;
-    float prob[RT_MAX_E / RT_THREADS];
+    float prob[PER];
+    uint64_t key[PER];
 #pragma unroll
-    for (int j = 0; j < RT_MAX_E / RT_THREADS; j++) {
+    for (int j = 0; j < PER; j++) {
         const int e = tid + RT_THREADS * j;
+        prob[j] = 0.f;
+        key[j] = 0;
         if (e < n_expert) {
             const float ex = expf(-logits[e]);
             prob[j] = 1.0f / (ex + 1.0f);
-            s_sel[e] = prob[j] + bias[e];
+            key[j] = sel_key(prob[j] + bias[e], e);
+            s_key[e] = key[j];
         }
     }
+    // pad to a multiple of 2 keys with key 0 (no real key is smaller)
+    if (tid == 0 && (n_expert & 1)) s_key[n_expert] = 0;
     __syncthreads();
+    const int npair = (n_expert + 1) >> 1;
+    const ulonglong2 *kp = reinterpret_cast<const ulonglong2 *>(s_key);
 #pragma unroll
-    for (int j = 0; j < RT_MAX_E / RT_THREADS; j++) {
+    for (int j = 0; j < PER; j++) {
         const int e = tid + RT_THREADS * j;
-        if (e < n_expert) {
-            const float mine = s_sel[e];
+        if (j * RT_THREADS < n_expert) {  // block-uniform skip of empty rounds
             int rank = 0;
-            for (int o = 0; o < n_expert; o++) {
-                const float v = s_sel[o];
-                rank += (v > mine) || (v == mine && o < e);
+            const uint64_t mine = key[j];
+#pragma unroll 8
+            for (int i = 0; i < npair; i++) {
+                const ulonglong2 v = kp[i];
+                rank += (v.x > mine) + (v.y > mine);
             }
-            if (rank < top_k) {
+            if (e < n_expert && rank < top_k) {
                 s_pick[rank] = e;
                 s_prob[rank] = prob[j];
             }
@@ -154,118 +177,155 @@ mx_status launch_route_logits(const float *x, const float *router, int t, int hi
 }
 
 // ---- fused decode router (t <= RF_MAX_T) ------------------------------------------------
-// One wave per expert computes that expert's full logits (its router row is
-// contiguous); block b covers experts [4b, 4b+4).  Optional RMSNorm of the token
-// rows is folded in (every block recomputes the row statistics; block 0 writes
-// the normalised rows for the expert kernels).  The last block to finish
-// (device-scope counter in `ws`, self-resetting) runs the selection.
-constexpr int RF_WAVES = 4;
+// One workgroup per expert: its 256 threads split the expert's router row
+// (contiguous in the GGUF layout) and the token rows, so every expert's logit
+// costs one memory round trip.  Optional RMSNorm of the token rows is folded in:
+// every block reduces sum(x^2) alongside the dot product and forms
+//   logit = sum(x * alpha * r) / sqrt(mean(x^2) + eps).
+// The first blocks also stage the (normalised) token rows for the expert
+// kernels (mx_stage.h layout, written to `xstage`, one row of xstage_bytes(hidden)
+// per token) and, if requested, write them as f32 to `x_normed`.  The last block
+// to finish (device-scope counter in `ws`, self-resetting) runs the selection.
 constexpr int RF_MAX_T = 4;
-constexpr int RF_VEC = 8;  // float4 per lane per load batch
+constexpr int RF_THREADS = 256;
+constexpr int RF_UNROLL = 4;  // float4 loads per thread per pass
+constexpr int RF_SUB = 16;    // arrival sub-counters (ws words 1..RF_SUB; word 0 is the top counter)
 
 size_t route_fused_ws_bytes(int t, int hidden, int n_expert) {
     (void)hidden;
     return 256 + (size_t)t * (size_t)n_expert * sizeof(float);
 }
 
-__global__ void __launch_bounds__(64 * RF_WAVES) k_route_fused(
+// Normalised token value block: x / m * alpha (alpha == NULL: x as is).
+__device__ __forceinline__ void norm8(float (&v)[8], const float *alpha, int h0, float m) {
+    if (!alpha) return;
+    float a[8];
+    load8f(alpha + h0, a);
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = v[i] / m * a[i];
+}
+
+__global__ void __launch_bounds__(RF_THREADS) k_route_fused(
     const float *__restrict__ x, const float *__restrict__ rms_alpha, float rms_eps, float *__restrict__ x_normed,
     const float *__restrict__ router, const float *__restrict__ bias, int t, int hidden, int n_expert, int top_k,
     float scale, int apply_scale, int norm, uint32_t *__restrict__ ids, float *__restrict__ w,
-    uint8_t *__restrict__ ws) {
-    __shared__ float s_red[RF_MAX_T][RF_WAVES];
-    __shared__ float s_rms[RF_MAX_T];
+    uint8_t *__restrict__ ws, uint8_t *__restrict__ xstage, int n_stage_blocks) {
+    __shared__ float s_red[2 * RF_MAX_T][RF_THREADS / 64];
+    __shared__ float s_m[RF_MAX_T];
     __shared__ int s_last;
     unsigned *counter = reinterpret_cast<unsigned *>(ws);
     float *logits = reinterpret_cast<float *>(ws + 256);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    if (rms_alpha) {
-        for (int tok = 0; tok < t; tok++) {
-            const float *xr = x + (int64_t)tok * hidden;
-            float ss = 0.f;
-            for (int i = 4 * tid; i < hidden; i += 4 * 64 * RF_WAVES) {
-                const float4 v = *reinterpret_cast<const float4 *>(xr + i);
-                ss = __builtin_fmaf(v.x, v.x, ss);
-                ss = __builtin_fmaf(v.y, v.y, ss);
-                ss = __builtin_fmaf(v.z, v.z, ss);
-                ss = __builtin_fmaf(v.w, v.w, ss);
-            }
-            for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
-            if (lane == 0) s_red[tok][wave] = ss;
+    const int e = blockIdx.x;
+    const float *rr = router + (int64_t)e * hidden;
+    float dot[RF_MAX_T] = {}, ss[RF_MAX_T] = {};
+    for (int c0 = 4 * tid; c0 < hidden; c0 += 4 * RF_THREADS * RF_UNROLL) {
+        float4 rv[RF_UNROLL], av[RF_UNROLL], xv[RF_MAX_T][RF_UNROLL];
+#pragma unroll
+        for (int i = 0; i < RF_UNROLL; i++) {
+            const int h = c0 + 4 * RF_THREADS * i;
+            const bool ok = h < hidden;
+            const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+            rv[i] = ok ? *reinterpret_cast<const float4 *>(rr + h) : z;
+            av[i] = (ok && rms_alpha) ? *reinterpret_cast<const float4 *>(rms_alpha + h) : make_float4(1.f, 1.f, 1.f, 1.f);
+#pragma unroll
+            for (int tok = 0; tok < RF_MAX_T; tok++)
+                xv[tok][i] = (ok && tok < t) ? *reinterpret_cast<const float4 *>(x + (int64_t)tok * hidden + h) : z;
         }
-        __syncthreads();
-        if (tid < t) {
-            float tot = 0.f;
-            for (int wv = 0; wv < RF_WAVES; wv++) tot += s_red[tid][wv];
-            s_rms[tid] = sqrtf(tot / (float)hidden + rms_eps);
-        }
-        __syncthreads();
-        if (blockIdx.x == 0 && x_normed) {
-            for (int i = tid; i < t * hidden; i += 64 * RF_WAVES) {
-                const int tok = i / hidden, h = i % hidden;
-                x_normed[i] = x[i] / s_rms[tok] * rms_alpha[h];
+#pragma unroll
+        for (int tok = 0; tok < RF_MAX_T; tok++) {
+#pragma unroll
+            for (int i = 0; i < RF_UNROLL; i++) {
+                const float4 v = xv[tok][i];
+                ss[tok] = __builtin_fmaf(v.x, v.x, ss[tok]);
+                ss[tok] = __builtin_fmaf(v.y, v.y, ss[tok]);
+                ss[tok] = __builtin_fmaf(v.z, v.z, ss[tok]);
+                ss[tok] = __builtin_fmaf(v.w, v.w, ss[tok]);
+                dot[tok] = __builtin_fmaf(v.x * av[i].x, rv[i].x, dot[tok]);
+                dot[tok] = __builtin_fmaf(v.y * av[i].y, rv[i].y, dot[tok]);
+                dot[tok] = __builtin_fmaf(v.z * av[i].z, rv[i].z, dot[tok]);
+                dot[tok] = __builtin_fmaf(v.w * av[i].w, rv[i].w, dot[tok]);
             }
         }
     }
-    const int e = blockIdx.x * RF_WAVES + wave;
-    if (e < n_expert) {
-        // all loads of a chunk (RF_VEC float4 per lane of the router row, the
-        // token rows and the norm weight) are issued before any arithmetic
-        const float *rr = router + (int64_t)e * hidden;
-        float acc[RF_MAX_T] = {};
-        for (int c0 = 4 * lane; c0 < hidden; c0 += 256 * RF_VEC) {
-            float4 rv[RF_VEC], xv[RF_MAX_T][RF_VEC], al[RF_VEC];
 #pragma unroll
-            for (int i = 0; i < RF_VEC; i++) {
-                const int h = c0 + 256 * i;
-                const bool ok = h < hidden;
-                rv[i] = ok ? *reinterpret_cast<const float4 *>(rr + h) : make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-                for (int tok = 0; tok < RF_MAX_T; tok++)
-                    xv[tok][i] = (ok && tok < t) ? *reinterpret_cast<const float4 *>(x + (int64_t)tok * hidden + h)
-                                                 : make_float4(0.f, 0.f, 0.f, 0.f);
-                if (rms_alpha) al[i] = ok ? *reinterpret_cast<const float4 *>(rms_alpha + h) : make_float4(0.f, 0.f, 0.f, 0.f);
-            }
-#pragma unroll
-            for (int tok = 0; tok < RF_MAX_T; tok++) {
-                if (tok >= t) break;
-                float a = acc[tok];
-#pragma unroll
-                for (int i = 0; i < RF_VEC; i++) {
-                    float4 v = xv[tok][i];
-                    if (rms_alpha) {
-                        const float m = s_rms[tok];
-                        v.x = v.x / m * al[i].x; v.y = v.y / m * al[i].y;
-                        v.z = v.z / m * al[i].z; v.w = v.w / m * al[i].w;
-                    }
-                    a = __builtin_fmaf(v.x, rv[i].x, a);
-                    a = __builtin_fmaf(v.y, rv[i].y, a);
-                    a = __builtin_fmaf(v.z, rv[i].z, a);
-                    a = __builtin_fmaf(v.w, rv[i].w, a);
-                }
-                acc[tok] = a;
-            }
+    for (int tok = 0; tok < RF_MAX_T; tok++) {
+        float a = dot[tok], b = ss[tok];
+        for (int off = 32; off > 0; off >>= 1) {
+            a += __shfl_xor(a, off, 64);
+            b += __shfl_xor(b, off, 64);
         }
-        for (int tok = 0; tok < t; tok++) {
-            float v = acc[tok];
-            for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-            if (lane == 0) st_agent(logits + (int64_t)tok * n_expert + e, v);
+        if (lane == 0) {
+            s_red[2 * tok][wave] = a;
+            s_red[2 * tok + 1][wave] = b;
         }
     }
-    // publish (completed agent-coherent stores), then count this block in
+    __syncthreads();
+    if (tid < t) {
+        float a = 0.f, b = 0.f;
+        for (int wv = 0; wv < RF_THREADS / 64; wv++) {
+            a += s_red[2 * tid][wv];
+            b += s_red[2 * tid + 1][wv];
+        }
+        const float m = rms_alpha ? sqrtf(b / (float)hidden + rms_eps) : 1.0f;
+        s_m[tid] = m;
+#ifdef MX_RT_PLAINST
+        logits[(int64_t)tid * n_expert + e] = rms_alpha ? a / m : a;
+#else
+        st_agent(logits + (int64_t)tid * n_expert + e, rms_alpha ? a / m : a);
+#endif
+    }
+    __syncthreads();
+    // staging of the token rows for the expert kernels
+#ifdef MX_RT_NOSTAGE
+    n_stage_blocks = 0;
+#endif
+    if (blockIdx.x < n_stage_blocks) {
+        const int nq = hidden / 8;
+        const int qi = blockIdx.x * RF_THREADS + tid;
+        const int tok = qi / nq, q = qi % nq;
+        const bool valid = tok < t;
+        float v[8] = {};
+        if (valid) {
+            load8f(x + (int64_t)tok * hidden + 8 * q, v);
+            norm8(v, rms_alpha, 8 * q, s_m[tok]);
+            if (x_normed) {
+                float4 *o = reinterpret_cast<float4 *>(x_normed + (int64_t)tok * hidden + 8 * q);
+                o[0] = make_float4(v[0], v[1], v[2], v[3]);
+                o[1] = make_float4(v[4], v[5], v[6], v[7]);
+            }
+        }
+        if (xstage) stage_quarter(v, q, valid, xstage + (int64_t)(valid ? tok : 0) * xstage_bytes(hidden), hidden);
+    }
+#ifdef MX_RT_NOSYNC
+    return;
+#endif
+    // publish (completed agent-coherent stores), then count this block in: blocks
+    // arrive on one of RF_SUB sub-counters, the last of each group on the top
+    // counter (bounded contention per address); the block that completes the top
+    // counter has seen every block's arrival.
     drain_vmem();
     __syncthreads();
-    if (tid == 0) s_last = arrive_last(counter, gridDim.x);
+    if (tid == 0) {
+        const int grp = blockIdx.x % RF_SUB;
+        const unsigned in_grp = (gridDim.x - grp + RF_SUB - 1) / RF_SUB;
+        const unsigned groups = min((unsigned)RF_SUB, gridDim.x);
+        s_last = arrive_last(counter + 1 + grp, in_grp) && arrive_last(counter, groups);
+    }
     __syncthreads();
     if (!s_last) return;  // block-uniform
+#ifdef MX_RT_NOSEL
+    if (tid == 0) reset_counter(counter);
+    return;
+#endif
     __shared__ float s_logit[RT_MAX_E];
     for (int tok = 0; tok < t; tok++) {
-        for (int e2 = tid; e2 < n_expert; e2 += 64 * RF_WAVES) s_logit[e2] = ld_agent(logits + (int64_t)tok * n_expert + e2);
+        for (int e2 = tid; e2 < n_expert; e2 += RF_THREADS) s_logit[e2] = ld_agent(logits + (int64_t)tok * n_expert + e2);
         __syncthreads();
         select_token(s_logit, bias, n_expert, top_k, scale, apply_scale, norm, ids + (int64_t)tok * top_k,
                      w + (int64_t)tok * top_k);
     }
-    if (tid == 0) reset_counter(counter);
+    if (tid <= RF_SUB) reset_counter(counter + tid);
 }
 
 int route_fused_max_t() { return RF_MAX_T; }
@@ -273,15 +333,41 @@ int route_fused_max_t() { return RF_MAX_T; }
 mx_status launch_route_fused(const float *x, const float *rms_alpha, float rms_eps, float *x_normed,
                              const float *router, const float *bias, int t, int hidden, int n_expert, int top_k,
                              float scale, int apply_scale, int norm, uint32_t *ids, float *w, void *ws,
-                             hipStream_t s) {
+                             uint8_t *xstage, hipStream_t s) {
     if (t == 0) return MX_OK;
     if (t > RF_MAX_T) return fail(MX_ERR_SHAPE, "fused router handles at most %d tokens", RF_MAX_T);
-    if (hidden % 4) return fail(MX_ERR_SHAPE, "fused router needs hidden %% 4 == 0");
-    const dim3 grid((unsigned)((n_expert + RF_WAVES - 1) / RF_WAVES));
-    hipLaunchKernelGGL(k_route_fused, grid, dim3(64 * RF_WAVES), 0, s, x, rms_alpha, rms_eps, x_normed, router,
-                       bias, t, hidden, n_expert, top_k, scale, apply_scale, norm, ids, w,
-                       reinterpret_cast<uint8_t *>(ws));
+    if (hidden % 32) return fail(MX_ERR_SHAPE, "fused router needs hidden %% 32 == 0");
+    const int nq = t * (hidden / 8);
+    const int n_stage = (xstage || x_normed) ? (nq + RF_THREADS - 1) / RF_THREADS : 0;
+    if (n_stage > n_expert)
+        return fail(MX_ERR_SHAPE, "fused router: %d experts cannot stage %d tokens of hidden %d", n_expert, t, hidden);
+    hipLaunchKernelGGL(k_route_fused, dim3((unsigned)n_expert), dim3(RF_THREADS), 0, s, x, rms_alpha, rms_eps,
+                       x_normed, router, bias, t, hidden, n_expert, top_k, scale, apply_scale, norm, ids, w,
+                       reinterpret_cast<uint8_t *>(ws), xstage, n_stage);
     MX_LAUNCH("k_route_fused");
+    return MX_OK;
+}
+
+// ---- activation staging for the decode expert kernels (rows of t tokens) ---------------
+__global__ void __launch_bounds__(256) k_stage_rows(const float *__restrict__ x, int t, int k,
+                                                    uint8_t *__restrict__ xstage) {
+    const int nq = k / 8;
+    const int qi = blockIdx.x * 256 + threadIdx.x;
+    const int tok = qi / nq, q = qi % nq;
+    const bool valid = tok < t;
+    float v[8] = {};
+    if (valid) load8f(x + (int64_t)tok * k + 8 * q, v);
+    stage_quarter(v, q, valid, xstage + (int64_t)(valid ? tok : 0) * xstage_bytes(k), k);
+}
+
+size_t stage_row_bytes(int k) { return (size_t)xstage_bytes(k); }
+
+mx_status launch_stage_rows(const float *x, int t, int k, uint8_t *xstage, hipStream_t s) {
+    if (t == 0) return MX_OK;
+    if (k % 32) return fail(MX_ERR_SHAPE, "staging needs k %% 32 == 0");
+    const int64_t nq = (int64_t)t * (k / 8);
+    hipLaunchKernelGGL(k_stage_rows, dim3((unsigned)((nq + 255) / 256)), dim3(256), 0, s, x, t, k, xstage);
+    MX_LAUNCH("k_stage_rows");
     return MX_OK;
 }
 
