@@ -113,9 +113,6 @@ template <> struct Q<kQ4_K> {
         return r;
     }
     __device__ static float dot(const Raw &r, int g, const X &x) {
-#ifdef MX_FAKE_DOT
-        return (float)(r.hd.x ^ r.hd.y ^ r.hd.z ^ r.hd.w ^ r.qa.x ^ r.qa.y ^ r.qa.z ^ r.qa.w ^ r.qb.x ^ r.qb.y ^ r.qb.z ^ r.qb.w ^ x.h[0]);
-#endif
         const uint32_t q[8] = {r.qa.x, r.qa.y, r.qa.z, r.qa.w, r.qb.x, r.qb.y, r.qb.z, r.qb.w};
         int ah = 0, al = 0, bh = 0, bl = 0;
 #pragma unroll
@@ -184,9 +181,6 @@ template <> struct Q<kQ6_K> {
         return r;
     }
     __device__ static float dot(const Raw &r, int g, const X &x) {
-#ifdef MX_FAKE_DOT
-        return (float)(r.a[0] ^ r.a[1] ^ r.a[2] ^ r.b[0] ^ r.b[1] ^ r.b[2] ^ r.hq[0] ^ r.hq[1] ^ r.hq[2] ^ r.sc[0] ^ r.sc[1] ^ r.sc[2] ^ r.d ^ x.h[0]);
-#endif
         const int jh = ((g & 7) & 3) >> 1;  // scale byte is scales[8n + jh + 2p]
         int hacc[4] = {0, 0, 0, 0}, lacc[4] = {0, 0, 0, 0};
         auto fun = [&](const uint32_t (&d)[3], int w) { return __builtin_amdgcn_alignbit(d[w + 1], d[w], r.sh); };
@@ -582,7 +576,7 @@ __global__ void __launch_bounds__(64 * WAVES) k_decode_gate_up(DecodeGateUpArgs 
     const uint8_t *const w[2] = {gw, uw};
     const Geo<DT> geo(a.hidden);
     typename Q<DT>::X xs[NG];
-    const uint8_t *staged = a.xstage + (int64_t)tok * xstage_bytes(a.hidden);
+    const uint8_t *staged = a.xstage + (int64_t)tok * xstage_stride(a.hidden);
     uint8_t *ring = lds + wave * (RING_GU * ni * 1024);
     stream_rows<DT, NG, Batch<NG>::NIT, 2, RING_GU>(w, rb, geo, xs, r0, min(r0 + RW_GU, a.ff), ring, ni,
                                                      [&] { load_xs<DT, NG>(staged, a.hidden, geo, xs); }, [] {},
@@ -671,7 +665,7 @@ __global__ void __launch_bounds__(64 * WAVES) k_decode_down(DecodeDownArgs a, in
                                                              stage_post(xrow, a.ff, xp, lds);
                                                              load_xs<DT, NG>(lds, a.ff, geo, xs);
                                                          },
-                                                         [&](int row, const float (&s)[1]) { st_agent(part + row, s[0]); });
+                                                 [&](int row, const float (&s)[1]) { st_agent(part + row, s[0]); });
     } else {
         stage_pre(xrow, a.ff, xp);
         stage_post(xrow, a.ff, xp, lds);

@@ -97,6 +97,70 @@ __device__ void select_token(const float *logits, const float *__restrict__ bias
     __syncthreads();
 }
 
+// Top-k from published sort keys and probabilities (device-scope coherent
+// loads): rank = number of larger keys, in LDS with 16-byte broadcast reads.
+// The weight sum runs in slot order on one thread, the divisions one slot per
+// thread.  All RT_THREADS threads must call.
+__device__ void select_from_keys(const uint64_t *keys, const float *probs, int n_expert, int top_k, float scale,
+                                 int apply_scale, int norm, uint32_t *__restrict__ ids_out,
+                                 float *__restrict__ w_out) {
+    constexpr int PER = RT_MAX_E / RT_THREADS;
+    __shared__ __attribute__((aligned(16))) uint64_t s_key[RT_MAX_E];
+    __shared__ float s_prob[RT_MAX_K];
+    __shared__ int s_pick[RT_MAX_K];
+    __shared__ float s_sum;
+    const int tid = threadIdx.x;
+    uint64_t key[PER];
+    float prob[PER];
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        const int e = tid + RT_THREADS * j;
+        key[j] = 0;
+        prob[j] = 0.f;
+        if (e < n_expert) {
+            key[j] = __hip_atomic_load(const_cast<uint64_t *>(keys) + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            prob[j] = ld_agent(probs + e);
+            s_key[e] = key[j];
+        }
+    }
+    if (tid == 0 && (n_expert & 1)) s_key[n_expert] = 0;  // pad with key 0 (no real key is smaller)
+    __syncthreads();
+    const int npair = (n_expert + 1) >> 1;
+    const ulonglong2 *kp = reinterpret_cast<const ulonglong2 *>(s_key);
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        const int e = tid + RT_THREADS * j;
+        if (j * RT_THREADS < n_expert) {  // block-uniform skip of empty rounds
+            int rank = 0;
+            const uint64_t mine = key[j];
+#pragma unroll 8
+            for (int i = 0; i < npair; i++) {
+                const ulonglong2 v = kp[i];
+                rank += (v.x > mine) + (v.y > mine);
+            }
+            if (e < n_expert && rank < top_k) {
+                s_pick[rank] = e;
+                s_prob[rank] = prob[j];
+            }
+        }
+    }
+    __syncthreads();
+    if (tid == 0) {
+        float sum = 0.f;
+        for (int k = 0; k < top_k; k++) sum = sum + s_prob[k];
+        s_sum = sum < 6.103515625e-5f ? 6.103515625e-5f : sum;
+    }
+    __syncthreads();
+    if (tid < top_k) {
+        float wk = s_prob[tid];
+        if (norm) wk = wk / s_sum;
+        if (apply_scale) wk = wk * scale;
+        ids_out[tid] = (uint32_t)s_pick[tid];
+        w_out[tid] = wk;
+    }
+    __syncthreads();
+}
+
 __global__ void __launch_bounds__(RT_THREADS) k_route_select(const float *__restrict__ logits,
                                                              const float *__restrict__ bias, int n_expert,
                                                              int top_k, float scale, int apply_scale, int norm,
@@ -177,23 +241,28 @@ mx_status launch_route_logits(const float *x, const float *router, int t, int hi
 }
 
 // ---- fused decode router (t <= RF_MAX_T) ------------------------------------------------
-// One workgroup per expert: its 256 threads split the expert's router row
-// (contiguous in the GGUF layout) and the token rows, so every expert's logit
-// costs one memory round trip.  Optional RMSNorm of the token rows is folded in:
-// every block reduces sum(x^2) alongside the dot product and forms
+// Blocks [0, n_expert): one expert each.  Its 256 threads split the expert's
+// router row (contiguous in the GGUF layout) and the token rows, so every
+// logit costs one memory round trip.  Optional RMSNorm is folded in: the block
+// reduces sum(x^2) alongside the dot product and forms
 //   logit = sum(x * alpha * r) / sqrt(mean(x^2) + eps).
-// The first blocks also stage the (normalised) token rows for the expert
-// kernels (mx_stage.h layout, written to `xstage`, one row of xstage_bytes(hidden)
-// per token) and, if requested, write them as f32 to `x_normed`.  The last block
-// to finish (device-scope counter in `ws`, self-resetting) runs the selection.
+// The block then turns the logit into the expert's sigmoid probability and
+// its stable-sort key (bias added for selection only) and publishes both.  The
+// last of these blocks to finish (two-level device-scope counter in `ws`,
+// self-resetting) ranks the keys and writes ids and weights.
+// Blocks [n_expert, n_expert + n_stage): stage the (normalised) token rows for
+// the expert kernels (mx_stage.h layout, one row of xstage_bytes(hidden) per
+// token in `xstage`) and, if requested, write them as f32 to `x_normed`; they
+// run alongside the expert blocks and take no part in the count.
 constexpr int RF_MAX_T = 4;
 constexpr int RF_THREADS = 256;
 constexpr int RF_UNROLL = 4;  // float4 loads per thread per pass
 constexpr int RF_SUB = 16;    // arrival sub-counters (ws words 1..RF_SUB; word 0 is the top counter)
 
+// ws: counters (256 B) | keys u64 [t][E] | probs f32 [t][E]
 size_t route_fused_ws_bytes(int t, int hidden, int n_expert) {
     (void)hidden;
-    return 256 + (size_t)t * (size_t)n_expert * sizeof(float);
+    return 256 + (size_t)t * (size_t)n_expert * (sizeof(uint64_t) + sizeof(float));
 }
 
 // Normalised token value block: x / m * alpha (alpha == NULL: x as is).
@@ -205,18 +274,69 @@ __device__ __forceinline__ void norm8(float (&v)[8], const float *alpha, int h0,
     for (int i = 0; i < 8; i++) v[i] = v[i] / m * a[i];
 }
 
+// Block-wide sum of each token's partial (t <= RF_MAX_T, all threads call).
+__device__ __forceinline__ void block_sums(float (&v)[RF_MAX_T], int t, float (*s_red)[RF_THREADS / 64]) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int tok = 0; tok < t; tok++) {
+        float a = v[tok];
+        for (int off = 32; off > 0; off >>= 1) a += __shfl_xor(a, off, 64);
+        if (lane == 0) s_red[tok][wave] = a;
+    }
+    __syncthreads();
+    for (int tok = 0; tok < t; tok++) {
+        float a = 0.f;
+        for (int wv = 0; wv < RF_THREADS / 64; wv++) a += s_red[tok][wv];
+        v[tok] = a;
+    }
+    __syncthreads();
+}
+
 __global__ void __launch_bounds__(RF_THREADS) k_route_fused(
     const float *__restrict__ x, const float *__restrict__ rms_alpha, float rms_eps, float *__restrict__ x_normed,
     const float *__restrict__ router, const float *__restrict__ bias, int t, int hidden, int n_expert, int top_k,
     float scale, int apply_scale, int norm, uint32_t *__restrict__ ids, float *__restrict__ w,
-    uint8_t *__restrict__ ws, uint8_t *__restrict__ xstage, int n_stage_blocks) {
-    __shared__ float s_red[2 * RF_MAX_T][RF_THREADS / 64];
-    __shared__ float s_m[RF_MAX_T];
+    uint8_t *__restrict__ ws, uint8_t *__restrict__ xstage) {
+    __shared__ float s_red[RF_MAX_T][RF_THREADS / 64];
     __shared__ int s_last;
     unsigned *counter = reinterpret_cast<unsigned *>(ws);
-    float *logits = reinterpret_cast<float *>(ws + 256);
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    uint64_t *keys = reinterpret_cast<uint64_t *>(ws + 256);
+    float *probs = reinterpret_cast<float *>(keys + (int64_t)t * n_expert);
+    const int tid = threadIdx.x;
+    if (blockIdx.x >= n_expert) {
+        // ---- staging blocks
+        float ss[RF_MAX_T] = {};
+        if (rms_alpha) {
+            for (int h = 4 * tid; h < hidden; h += 4 * RF_THREADS) {
+                for (int tok = 0; tok < t; tok++) {
+                    const float4 v = *reinterpret_cast<const float4 *>(x + (int64_t)tok * hidden + h);
+                    ss[tok] = __builtin_fmaf(v.x, v.x, ss[tok]);
+                    ss[tok] = __builtin_fmaf(v.y, v.y, ss[tok]);
+                    ss[tok] = __builtin_fmaf(v.z, v.z, ss[tok]);
+                    ss[tok] = __builtin_fmaf(v.w, v.w, ss[tok]);
+                }
+            }
+            block_sums(ss, t, s_red);
+        }
+        const int nq = hidden / 8;
+        const int qi = (blockIdx.x - n_expert) * RF_THREADS + tid;
+        const int tok = qi / nq, q = qi % nq;
+        const bool valid = tok < t;
+        float v[8] = {};
+        if (valid) {
+            load8f(x + (int64_t)tok * hidden + 8 * q, v);
+            if (rms_alpha) norm8(v, rms_alpha, 8 * q, sqrtf(ss[tok] / (float)hidden + rms_eps));
+            if (x_normed) {
+                float4 *o = reinterpret_cast<float4 *>(x_normed + (int64_t)tok * hidden + 8 * q);
+                o[0] = make_float4(v[0], v[1], v[2], v[3]);
+                o[1] = make_float4(v[4], v[5], v[6], v[7]);
+            }
+        }
+        if (xstage) stage_quarter(v, q, valid, xstage + (int64_t)(valid ? tok : 0) * xstage_stride(hidden), hidden);
+        return;
+    }
+    // ---- expert blocks
     const int e = blockIdx.x;
+    const float be = bias[e];  // issued early: needed only after the reduction
     const float *rr = router + (int64_t)e * hidden;
     float dot[RF_MAX_T] = {}, ss[RF_MAX_T] = {};
     for (int c0 = 4 * tid; c0 < hidden; c0 += 4 * RF_THREADS * RF_UNROLL) {
@@ -234,6 +354,7 @@ __global__ void __launch_bounds__(RF_THREADS) k_route_fused(
         }
 #pragma unroll
         for (int tok = 0; tok < RF_MAX_T; tok++) {
+            if (tok >= t) break;
 #pragma unroll
             for (int i = 0; i < RF_UNROLL; i++) {
                 const float4 v = xv[tok][i];
@@ -248,58 +369,15 @@ __global__ void __launch_bounds__(RF_THREADS) k_route_fused(
             }
         }
     }
-#pragma unroll
-    for (int tok = 0; tok < RF_MAX_T; tok++) {
-        float a = dot[tok], b = ss[tok];
-        for (int off = 32; off > 0; off >>= 1) {
-            a += __shfl_xor(a, off, 64);
-            b += __shfl_xor(b, off, 64);
-        }
-        if (lane == 0) {
-            s_red[2 * tok][wave] = a;
-            s_red[2 * tok + 1][wave] = b;
-        }
-    }
-    __syncthreads();
+    block_sums(dot, t, s_red);
+    if (rms_alpha) block_sums(ss, t, s_red);
     if (tid < t) {
-        float a = 0.f, b = 0.f;
-        for (int wv = 0; wv < RF_THREADS / 64; wv++) {
-            a += s_red[2 * tid][wv];
-            b += s_red[2 * tid + 1][wv];
-        }
-        const float m = rms_alpha ? sqrtf(b / (float)hidden + rms_eps) : 1.0f;
-        s_m[tid] = m;
-#ifdef MX_RT_PLAINST
-        logits[(int64_t)tid * n_expert + e] = rms_alpha ? a / m : a;
-#else
-        st_agent(logits + (int64_t)tid * n_expert + e, rms_alpha ? a / m : a);
-#endif
+        const float lg = rms_alpha ? dot[tid] / sqrtf(ss[tid] / (float)hidden + rms_eps) : dot[tid];
+        const float p = 1.0f / (expf(-lg) + 1.0f);  // sigmoid (moe.rs:101)
+        const int64_t o = (int64_t)tid * n_expert + e;
+        __hip_atomic_store(keys + o, sel_key(p + be, e), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        st_agent(probs + o, p);
     }
-    __syncthreads();
-    // staging of the token rows for the expert kernels
-#ifdef MX_RT_NOSTAGE
-    n_stage_blocks = 0;
-#endif
-    if (blockIdx.x < n_stage_blocks) {
-        const int nq = hidden / 8;
-        const int qi = blockIdx.x * RF_THREADS + tid;
-        const int tok = qi / nq, q = qi % nq;
-        const bool valid = tok < t;
-        float v[8] = {};
-        if (valid) {
-            load8f(x + (int64_t)tok * hidden + 8 * q, v);
-            norm8(v, rms_alpha, 8 * q, s_m[tok]);
-            if (x_normed) {
-                float4 *o = reinterpret_cast<float4 *>(x_normed + (int64_t)tok * hidden + 8 * q);
-                o[0] = make_float4(v[0], v[1], v[2], v[3]);
-                o[1] = make_float4(v[4], v[5], v[6], v[7]);
-            }
-        }
-        if (xstage) stage_quarter(v, q, valid, xstage + (int64_t)(valid ? tok : 0) * xstage_bytes(hidden), hidden);
-    }
-#ifdef MX_RT_NOSYNC
-    return;
-#endif
     // publish (completed agent-coherent stores), then count this block in: blocks
     // arrive on one of RF_SUB sub-counters, the last of each group on the top
     // counter (bounded contention per address); the block that completes the top
@@ -308,23 +386,15 @@ __global__ void __launch_bounds__(RF_THREADS) k_route_fused(
     __syncthreads();
     if (tid == 0) {
         const int grp = blockIdx.x % RF_SUB;
-        const unsigned in_grp = (gridDim.x - grp + RF_SUB - 1) / RF_SUB;
-        const unsigned groups = min((unsigned)RF_SUB, gridDim.x);
+        const unsigned in_grp = (n_expert - grp + RF_SUB - 1) / RF_SUB;
+        const unsigned groups = min(RF_SUB, n_expert);
         s_last = arrive_last(counter + 1 + grp, in_grp) && arrive_last(counter, groups);
     }
     __syncthreads();
     if (!s_last) return;  // block-uniform
-#ifdef MX_RT_NOSEL
-    if (tid == 0) reset_counter(counter);
-    return;
-#endif
-    __shared__ float s_logit[RT_MAX_E];
-    for (int tok = 0; tok < t; tok++) {
-        for (int e2 = tid; e2 < n_expert; e2 += RF_THREADS) s_logit[e2] = ld_agent(logits + (int64_t)tok * n_expert + e2);
-        __syncthreads();
-        select_token(s_logit, bias, n_expert, top_k, scale, apply_scale, norm, ids + (int64_t)tok * top_k,
-                     w + (int64_t)tok * top_k);
-    }
+    for (int tok = 0; tok < t; tok++)
+        select_from_keys(keys + (int64_t)tok * n_expert, probs + (int64_t)tok * n_expert, n_expert, top_k, scale,
+                         apply_scale, norm, ids + (int64_t)tok * top_k, w + (int64_t)tok * top_k);
     if (tid <= RF_SUB) reset_counter(counter + tid);
 }
 
@@ -339,11 +409,9 @@ mx_status launch_route_fused(const float *x, const float *rms_alpha, float rms_e
     if (hidden % 32) return fail(MX_ERR_SHAPE, "fused router needs hidden %% 32 == 0");
     const int nq = t * (hidden / 8);
     const int n_stage = (xstage || x_normed) ? (nq + RF_THREADS - 1) / RF_THREADS : 0;
-    if (n_stage > n_expert)
-        return fail(MX_ERR_SHAPE, "fused router: %d experts cannot stage %d tokens of hidden %d", n_expert, t, hidden);
-    hipLaunchKernelGGL(k_route_fused, dim3((unsigned)n_expert), dim3(RF_THREADS), 0, s, x, rms_alpha, rms_eps,
-                       x_normed, router, bias, t, hidden, n_expert, top_k, scale, apply_scale, norm, ids, w,
-                       reinterpret_cast<uint8_t *>(ws), xstage, n_stage);
+    hipLaunchKernelGGL(k_route_fused, dim3((unsigned)(n_expert + n_stage)), dim3(RF_THREADS), 0, s, x, rms_alpha,
+                       rms_eps, x_normed, router, bias, t, hidden, n_expert, top_k, scale, apply_scale, norm, ids, w,
+                       reinterpret_cast<uint8_t *>(ws), xstage);
     MX_LAUNCH("k_route_fused");
     return MX_OK;
 }
@@ -357,10 +425,10 @@ __global__ void __launch_bounds__(256) k_stage_rows(const float *__restrict__ x,
     const bool valid = tok < t;
     float v[8] = {};
     if (valid) load8f(x + (int64_t)tok * k + 8 * q, v);
-    stage_quarter(v, q, valid, xstage + (int64_t)(valid ? tok : 0) * xstage_bytes(k), k);
+    stage_quarter(v, q, valid, xstage + (int64_t)(valid ? tok : 0) * xstage_stride(k), k);
 }
 
-size_t stage_row_bytes(int k) { return (size_t)xstage_bytes(k); }
+size_t stage_row_bytes(int k) { return (size_t)xstage_stride(k); }
 
 mx_status launch_stage_rows(const float *x, int t, int k, uint8_t *xstage, hipStream_t s) {
     if (t == 0) return MX_OK;

@@ -20,6 +20,9 @@ namespace mx {
 constexpr float XQ_RANGE = 32000.0f;
 
 __host__ __device__ constexpr int xstage_bytes(int k) { return 2 * k + (k / 32) * 8 + (k / 8) * 4; }
+// distance between staged rows in a buffer of several (256-byte aligned, so
+// every row can be copied with aligned 16-byte pieces)
+__host__ __device__ constexpr int xstage_stride(int k) { return (xstage_bytes(k) + 255) & ~255; }
 
 struct XView {
     const int8_t *xh, *xl;
