@@ -292,7 +292,13 @@ struct Plan {
 Plan plan_for(const mx_moe_layer *L, int64_t t) {
     Plan p;
     p.min_seq = L->mm_min_seq > 0 ? L->mm_min_seq : kDefaultMmMinSeq;
-    p.mm = L->mm_min_seq >= 0 && t >= p.min_seq;  // < 0: never (LAGUNA_NO_MM_ID)
+    // < 0: never (LAGUNA_NO_MM_ID).  The MFMA GEMM needs K % 256 == 0 for every
+    // stack; other shapes stay on the gather mat-vec kernels at any t.
+    bool shapes = gemm_supported(L->gate.dtype, (int)L->hidden) && gemm_supported(L->down.dtype, (int)L->expert_ff);
+    if (L->shared_gate.data)
+        shapes = shapes && gemm_supported(L->shared_gate.dtype, (int)L->hidden) &&
+                 gemm_supported(L->shared_down.dtype, (int)L->expert_ff);
+    p.mm = L->mm_min_seq >= 0 && t >= p.min_seq && shapes;
     p.fused_router = !p.mm && t <= route_fused_max_t();
     p.has_shared = L->shared_gate.data != nullptr;
     p.shared_in_decode = p.has_shared && L->shared_gate.dtype == L->gate.dtype &&
@@ -309,7 +315,9 @@ struct Layout {
     float *part = nullptr;
     unsigned *counters = nullptr;
     int32_t *map = nullptr, *map_sh = nullptr;
-    float *gate = nullptr, *up = nullptr, *down = nullptr, *routed = nullptr;
+    uint32_t *ids_aug = nullptr;
+    _Float16 *x16 = nullptr, *act16 = nullptr;
+    float *x16s = nullptr, *act16s = nullptr, *down = nullptr;
     float *sh_g = nullptr, *sh_u = nullptr, *sh_out = nullptr;
     size_t bytes = 0;
 };
@@ -338,18 +346,24 @@ Layout carve(const mx_moe_layer *L, int64_t t, const Plan &p, void *base) {
             o.sh_out = ws.take<float>(t * H);
         }
     } else {
-        o.map = ws.take<int32_t>(map0_bytes((int)E, (int)t, (int)K) / 4);
-        o.gate = ws.take<float>(t * K * FF);
-        o.up = ws.take<float>(t * K * FF);
-        o.down = ws.take<float>(t * K * H);
-        o.routed = ws.take<float>(t * H);
-        if (p.has_shared) {
-            o.zero_ids = ws.take<uint32_t>(t);
+        // one bucket map over routed + shared (expert E, every token) when the shared
+        // expert has the routed quant types, else a second one-expert map
+        const int64_t S = p.has_shared ? 1 : 0;
+        const int64_t KK = K + S;
+        const int64_t EM = E + (p.shared_in_decode ? 1 : 0);
+        const int64_t KM = K + (p.shared_in_decode ? 1 : 0);
+        if (p.has_shared) o.ids_aug = ws.take<uint32_t>(t * KK);
+        o.map = ws.take<int32_t>(map0_bytes((int)EM, (int)t, (int)KM) / 4);
+        if (p.has_shared && !p.shared_in_decode) {
             o.map_sh = ws.take<int32_t>(map0_bytes(1, (int)t, 1) / 4);
-            o.sh_g = ws.take<float>(t * FF);
-            o.sh_u = ws.take<float>(t * FF);
-            o.sh_out = ws.take<float>(t * H);
+            o.zero_ids = ws.take<uint32_t>(t);
         }
+        o.x16 = ws.take<_Float16>(t * H);
+        o.x16s = ws.take<float>(t);
+        o.act = ws.take<float>(t * KK * FF);
+        o.act16 = ws.take<_Float16>(t * KK * FF);
+        o.act16s = ws.take<float>(t * KK);
+        o.down = ws.take<float>(t * KK * H);
     }
     o.bytes = ws.off + 256;
     return o;
@@ -500,44 +514,67 @@ mx_status moe_forward_impl(const mx_moe_layer *L, const float *x, int64_t t, con
         return MX_OK;
     }
 
-    // prefill / verify: bucket once, three grouped GEMMs (moe.rs:242-323)
-    MX_TRY(launch_map0(ids, (int)t, (int)K, (int)E, o.map, s));
-    MX_STAGE();
-    MmArgs ma{gg.w, gg.expert_bytes, gg.row_bytes, (int)E, (int)FF, (int)H, xin, 1, (int)t, (int)K, o.map, o.gate};
-    MX_TRY(launch_mul_mm_id(L->gate.dtype, ma, s));
-    MX_STAGE();
-    ma.w = gu.w; ma.dst = o.up;
-    MX_TRY(launch_mul_mm_id(L->up.dtype, ma, s));
-    MX_STAGE();
-    MX_TRY(launch_silu_mul(o.gate, o.up, t * K * FF, o.gate, s));
-    MX_STAGE();
-    MmArgs md{gd.w, gd.expert_bytes, gd.row_bytes, (int)E, (int)H, (int)FF, o.gate, (int)K, (int)t, (int)K,
-              o.map, o.down};
-    MX_TRY(launch_mul_mm_id(L->down.dtype, md, s));
-    MX_STAGE();
-    float *routed = (p.has_shared || residual) ? o.routed : out;
-    MX_TRY(launch_combine(o.down, nullptr, w, (int)t, (int)K, (int)H, routed, s));
-    MX_STAGE();
-    if (!p.has_shared) {
-        if (residual) MX_TRY(launch_add3(residual, routed, nullptr, t * H, out, s));
-        MX_STAGE();
-        return MX_OK;
+    // prefill / verify (moe.rs:242-323): bucket once, x -> scaled f16, gate+up GEMM
+    // with SwiGLU, act -> scaled f16, down GEMM into rows token * KK + slot (slot K:
+    // shared expert), combine with the shared expert and the residual
+    const int S = p.has_shared ? 1 : 0;
+    const int KK = (int)K + S;
+    const bool one_map = p.shared_in_decode;  // shared joins the routed map as expert E
+    const int EM = (int)E + (one_map ? 1 : 0), KM = one_map ? KK : (int)K;
+    if (one_map) {
+        MX_TRY(launch_ids_with_shared(ids, (int)t, (int)K, (int)E, o.ids_aug, s));
+        MX_TRY(launch_map0(o.ids_aug, (int)t, KM, EM, o.map, s, GM_BM));
+    } else {
+        MX_TRY(launch_map0(ids, (int)t, (int)K, (int)E, o.map, s, GM_BM));
+        if (p.has_shared) {
+            hipLaunchKernelGGL(k_fill_u32, dim3((unsigned)((t + 255) / 256)), dim3(256), 0, s, o.zero_ids, t, 0u);
+            MX_LAUNCH("k_fill_u32");
+            MX_TRY(launch_map0(o.zero_ids, (int)t, 1, 1, o.map_sh, s, GM_BM));
+        }
     }
-    // the shared expert is a one-expert grouped GEMM over every token
-    hipLaunchKernelGGL(k_fill_u32, dim3((unsigned)((t + 255) / 256)), dim3(256), 0, s, o.zero_ids, t, 0u);
-    MX_LAUNCH("k_fill_u32");
-    MX_TRY(launch_map0(o.zero_ids, (int)t, 1, 1, o.map_sh, s));
-    MmArgs sa{sg.w, sg.expert_bytes, sg.row_bytes, 1, (int)FF, (int)H, xin, 1, (int)t, 1, o.map_sh, o.sh_g};
-    MX_TRY(launch_mul_mm_id(L->shared_gate.dtype, sa, s));
-    sa.w = su.w;
-    sa.dst = o.sh_u;
-    MX_TRY(launch_mul_mm_id(L->shared_up.dtype, sa, s));
-    MX_TRY(launch_silu_mul(o.sh_g, o.sh_u, t * FF, o.sh_g, s));
-    MmArgs sdn{sd.w, sd.expert_bytes, sd.row_bytes, 1, (int)H, (int)FF, o.sh_g, 1, (int)t, 1, o.map_sh, o.sh_out};
-    MX_TRY(launch_mul_mm_id(L->shared_down.dtype, sdn, s));
     MX_STAGE();
-    // out = residual + (routed + shared)   (moe.rs:78, model.rs:351)
-    MX_TRY(launch_add3(routed, o.sh_out, residual, t * H, out, s));
+    MX_TRY(launch_to_f16_rows(xin, t, (int)H, nullptr, o.x16, o.x16s, s));
+    MX_STAGE();
+    // one bucket map's gate+up (SwiGLU, act rows at its bucket positions from act_row0 on)
+    // and down (rows token * KK + slot + out_add)
+    auto experts = [&](const int32_t *map, int n_map_expert, int top_k, int n_routed, const uint8_t *wg,
+                       const uint8_t *wu, const uint8_t *wd, const uint8_t *shg, const uint8_t *shu,
+                       const uint8_t *shd, int64_t act_row0, int out_add, int dt_gu, int dt_d,
+                       const StackGeom &geo_gu, const StackGeom &geo_d, const StackGeom &geo_sgu,
+                       const StackGeom &geo_sd) -> mx_status {
+        const MapLayout LM(n_map_expert, (int)t, top_k);
+        GemmArgs ga{};
+        ga.w[0] = wg; ga.w[1] = wu;
+        ga.w_sh[0] = shg; ga.w_sh[1] = shu;
+        ga.expert_bytes = geo_gu.expert_bytes; ga.row_bytes = geo_gu.row_bytes; ga.sh_row_bytes = geo_sgu.row_bytes;
+        ga.n_expert = n_routed; ga.n_out = (int)FF; ga.k = (int)H;
+        ga.a = o.x16; ga.a_scale = o.x16s; ga.a_by_token = 1;
+        ga.t = (int)t; ga.top_k = top_k; ga.n_map_expert = n_map_expert; ga.map = map;
+        ga.out = o.act + act_row0 * FF;
+        MX_TRY(launch_gemm(dt_gu, true, ga, s));
+        MX_TRY(launch_to_f16_rows(ga.out, t * top_k, (int)FF, map + LM.off + n_map_expert,
+                                  o.act16 + act_row0 * FF, o.act16s + act_row0, s));
+        GemmArgs da = ga;
+        da.w[0] = wd; da.w[1] = nullptr;
+        da.w_sh[0] = shd; da.w_sh[1] = nullptr;
+        da.expert_bytes = geo_d.expert_bytes; da.row_bytes = geo_d.row_bytes; da.sh_row_bytes = geo_sd.row_bytes;
+        da.n_out = (int)H; da.k = (int)FF;
+        da.a = o.act16 + act_row0 * FF; da.a_scale = o.act16s + act_row0; da.a_by_token = 0;
+        da.out = o.down; da.out_stride = KK; da.out_add = out_add;
+        return launch_gemm(dt_d, false, da, s);
+    };
+    if (one_map) {
+        MX_TRY(experts(o.map, EM, KM, (int)E, gg.w, gu.w, gd.w, sg.w, su.w, sd.w, 0, 0, L->gate.dtype,
+                       L->down.dtype, gg, gd, sg, sd));
+    } else {
+        MX_TRY(experts(o.map, (int)E, (int)K, (int)E, gg.w, gu.w, gd.w, nullptr, nullptr, nullptr, 0, 0,
+                       L->gate.dtype, L->down.dtype, gg, gd, gg, gd));
+        if (p.has_shared)
+            MX_TRY(experts(o.map_sh, 1, 1, 0, nullptr, nullptr, nullptr, sg.w, su.w, sd.w, t * K, (int)K,
+                           L->shared_gate.dtype, L->shared_down.dtype, sg, sd, sg, sd));
+    }
+    MX_STAGE();
+    MX_TRY(launch_combine_prefill(o.down, w, residual, (int)t, (int)K, S, (int)H, out, s));
     MX_STAGE();
     return MX_OK;
 }

@@ -1,0 +1,506 @@
+// Grouped expert GEMM of the fused prefill / verify path on MFMA.
+//
+// Replaces the kernel_mul_mm_id_* dispatches of the reference's prefill block
+// (mm_id.metal:492-647, driven from moe.rs:242-323).  One workgroup computes a
+// 128-pair x 256-column tile of one expert:
+//
+//  * A (activations) are f16 rows, each scaled by its own power of two so any
+//    f32 magnitude lands in [2^14, 2^15) (the scale is applied back to the f32
+//    result, so the only rounding is the f16 rounding of x itself).  The tile's
+//    rows are gathered by pair (token = pair / top_k, or the bucket position)
+//    and copied straight into LDS with global_load_lds, 128 K-values per
+//    stage, double-buffered.  16-byte chunks are XOR-swizzled by row so the
+//    MFMA operand reads (16 consecutive rows, same chunk) hit distinct banks.
+//  * B (weights) are read from the raw GGUF blocks into registers, one stage
+//    ahead, and dequantised in registers directly into the MFMA B-operand
+//    layout: f32 dequantisation of the reference's formula, then one
+//    round-to-nearest f16 pack (the reference dequantises into half tiles).
+//    Each wave owns 64 output columns, so no weight is dequantised twice in a
+//    workgroup.
+//  * v_mfma_f32_32x32x16_f16, f32 accumulation: each wave holds 4 (pairs) x 2
+//    (columns) 32x32 accumulators.
+//
+// The K order inside a 128-value stage is permuted (identically for A and B):
+// MFMA step (p, h) gives lane half kh the 8 values at
+// 32p + 16kh + 8h + [0, 8) of the stage, which makes every lane's weight bytes
+// contiguous 16-byte pieces of the block.
+//
+// Epilogues: SwiGLU (wave columns = 32 gate rows and the same 32 up rows, so
+// act = silu(g) * u is lane-local; act is written f32 at the pair's bucket
+// position) or plain (f32 rows scattered to the pair's output row).
+//
+// Work items are (m-tile, n-tile) pairs, m-tile fastest; blocks are dealt to
+// the 8 XCDs round-robin by the hardware, so block b takes item
+// (b % 8) * per + b / 8: each XCD works through a contiguous run of items, and
+// the m-tiles of one expert that share a weight slice run together on one L2.
+#include "mx_launch.h"
+#include "mx_dma.h"
+
+namespace mx {
+
+namespace {
+
+constexpr int KS = 128;                // K per stage
+constexpr int ROWB = KS * 2;           // LDS bytes per A row and stage
+constexpr int STAGE_BYTES = GM_BM * ROWB;
+constexpr int NWAVE = 4;
+constexpr int DMA_PER_WAVE = STAGE_BYTES / 1024 / NWAVE;
+
+typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
+typedef float float2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint4 ld16(const uint8_t *p) {  // 4-byte aligned p
+    const u32x4a4 v = *reinterpret_cast<const u32x4a4 *>(p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// 16 bytes from a 2-byte aligned address: an aligned 16-byte load plus, when p
+// is not 4-byte aligned, the dword after it (funnel-shifted in `fix16`)
+struct Raw16 {
+    uint4 v;
+    uint32_t tail;
+    uint32_t sh;  // 0 or 16
+};
+__device__ __forceinline__ Raw16 ld16_a2(const uint8_t *p) {
+    Raw16 r;
+    const uintptr_t mis = reinterpret_cast<uintptr_t>(p) & 3;
+    const uint8_t *q = p - mis;
+    r.v = ld16(q);
+    r.tail = mis ? *reinterpret_cast<const uint32_t *>(q + 16) : 0u;
+    r.sh = (uint32_t)mis * 8;
+    return r;
+}
+__device__ __forceinline__ uint4 fix16(const Raw16 &r) {
+    return make_uint4(__builtin_amdgcn_alignbit(r.v.y, r.v.x, r.sh), __builtin_amdgcn_alignbit(r.v.z, r.v.y, r.sh),
+                      __builtin_amdgcn_alignbit(r.v.w, r.v.z, r.sh), __builtin_amdgcn_alignbit(r.tail, r.v.w, r.sh));
+}
+
+__device__ __forceinline__ half8_t pack8(const float (&f)[8]) {
+    half8_t h;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const half2_t p = __builtin_convertvector((float2_t){f[2 * i], f[2 * i + 1]}, half2_t);
+        h[2 * i] = p[0];
+        h[2 * i + 1] = p[1];
+    }
+    return h;
+}
+
+// 4 unsigned bytes of w -> floats (v_cvt_f32_ubyte0..3)
+__device__ __forceinline__ void ubytes(uint32_t w, float *f) {
+#pragma unroll
+    for (int b = 0; b < 4; b++) f[b] = (float)((w >> (8 * b)) & 0xFFu);
+}
+
+// ---- per-type weight registers: one stage, one weight row, one lane half --------------
+template <int DT> struct WB;
+
+// Q4_K: stage = half `par` of super-block ks / 2; 64-value chunks i = 2 par + c.
+// Lane half kh holds qs bytes [32 i + 16 kh, +16) of both chunks; step p = 2c + nib
+// uses the low (nib 0) or high nibbles, sub-block 2 i + nib (mm_id.metal:95-113).
+template <> struct WB<kQ4_K> {
+    uint4 h, q[2];
+    __device__ __forceinline__ void load(const uint8_t *row, int ks, int kh) {
+        const uint8_t *blk = row + (ks >> 1) * 144;
+        h = ld16(blk);
+        const uint8_t *qs = blk + 16 + 64 * (ks & 1) + 16 * kh;
+        q[0] = ld16(qs);
+        q[1] = ld16(qs + 32);
+    }
+    float d[4], m[4];
+    template <int PAR> __device__ __forceinline__ void prep(int kh) {
+        (void)kh;
+        const float dd = h2f((uint16_t)(h.x & 0xFFFFu)), dmin = h2f((uint16_t)(h.x >> 16));
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            uint32_t sc, mn;
+            q4k_scale_min(4 * PAR + p, h.y, h.z, h.w, sc, mn);
+            d[p] = dd * (float)sc;
+            m[p] = dmin * (float)mn;
+        }
+    }
+    __device__ __forceinline__ half8_t step(int p, int hh) const {
+        const uint4 &v = q[p >> 1];
+        const int sh = 4 * (p & 1);
+        const uint32_t w0 = ((hh ? v.z : v.x) >> sh) & 0x0F0F0F0Fu;
+        const uint32_t w1 = ((hh ? v.w : v.y) >> sh) & 0x0F0F0F0Fu;
+        float f[8];
+        ubytes(w0, f);
+        ubytes(w1, f + 4);
+#pragma unroll
+        for (int i = 0; i < 8; i++) f[i] = __builtin_fmaf(d[p], f[i], -m[p]);
+        return pack8(f);
+    }
+};
+
+// Q6_K: stage = half n = par of super-block ks / 2 (128 values).  Lane half kh
+// holds ql[64n + 16kh, +16), ql[64n + 32 + 16kh, +16), qh[32n + 16kh, +16);
+// step p takes the 4-bit part from the low (p even) / high (p odd) ql piece,
+// nibble p / 2, and bits 2p of qh; scale 8n + 2p + kh (mm_id.metal:115-135).
+template <> struct WB<kQ6_K> {
+    Raw16 lo, hi, qh;
+    uint2 sc;
+    uint16_t dh;
+    __device__ __forceinline__ void load(const uint8_t *row, int ks, int kh) {
+        const uint8_t *blk = row + (int64_t)(ks >> 1) * 210;
+        const int n = ks & 1;
+        lo = ld16_a2(blk + 64 * n + 16 * kh);
+        hi = ld16_a2(blk + 64 * n + 32 + 16 * kh);
+        qh = ld16_a2(blk + 128 + 32 * n + 16 * kh);
+        sc = load8_a2(blk + 192 + 8 * n);
+        dh = ld_u16(blk + 208);
+    }
+    float ds[4];
+    uint4 l4, h4, q4;
+    template <int PAR> __device__ __forceinline__ void prep(int kh) {
+        const float d = h2f(dh);
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            const int j = 2 * p + kh;  // byte j of the stage's 8 scales
+            const uint32_t word = j < 4 ? sc.x : sc.y;
+            const int8_t s8 = (int8_t)((word >> (8 * (j & 3))) & 0xFFu);
+            ds[p] = d * (float)s8;
+        }
+        l4 = fix16(lo);
+        h4 = fix16(hi);
+        q4 = fix16(qh);
+    }
+    __device__ __forceinline__ half8_t step(int p, int hh) const {
+        const uint4 &ql = (p & 1) ? h4 : l4;
+        const int shl = 4 * (p >> 1), shh = 2 * p;
+        const uint32_t a0 = ((hh ? ql.z : ql.x) >> shl) & 0x0F0F0F0Fu;
+        const uint32_t a1 = ((hh ? ql.w : ql.y) >> shl) & 0x0F0F0F0Fu;
+        const uint32_t b0 = (((hh ? q4.z : q4.x) >> shh) & 0x03030303u) << 4;
+        const uint32_t b1 = (((hh ? q4.w : q4.y) >> shh) & 0x03030303u) << 4;
+        float f[8];
+        ubytes(a0 | b0, f);
+        ubytes(a1 | b1, f + 4);
+        const float off = -32.0f * ds[p];
+#pragma unroll
+        for (int i = 0; i < 8; i++) f[i] = __builtin_fmaf(ds[p], f[i], off);
+        return pack8(f);
+    }
+};
+
+// Q8_0: stage = blocks 4 ks + p; lane half kh holds quants [16 kh, +16) of each.
+template <> struct WB<kQ8_0> {
+    Raw16 q[4];
+    uint16_t dh[4];
+    __device__ __forceinline__ void load(const uint8_t *row, int ks, int kh) {
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            const uint8_t *blk = row + (int64_t)(4 * ks + p) * 34;
+            q[p] = ld16_a2(blk + 2 + 16 * kh);
+            dh[p] = ld_u16(blk);
+        }
+    }
+    float d[4];
+    uint4 v[4];
+    template <int PAR> __device__ __forceinline__ void prep(int kh) {
+        (void)kh;
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            d[p] = h2f(dh[p]);
+            v[p] = fix16(q[p]);
+        }
+    }
+    __device__ __forceinline__ half8_t step(int p, int hh) const {
+        const uint32_t w0 = hh ? v[p].z : v[p].x, w1 = hh ? v[p].w : v[p].y;
+        float f[8];
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            f[b] = (float)((int32_t)(w0 << (24 - 8 * b)) >> 24);
+            f[4 + b] = (float)((int32_t)(w1 << (24 - 8 * b)) >> 24);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++) f[i] = d[p] * f[i];
+        return pack8(f);
+    }
+};
+
+struct Tile {
+    int e, pos0, mrows, nt;
+};
+
+// decodes this block's work item; false: nothing to do (block-uniform)
+__device__ __forceinline__ bool tile_of(const GemmArgs &a, int nt_count, Tile &t) {
+    const MapLayout L(a.n_map_expert, a.t, a.top_k);
+    const int n_mt = a.map[L.n_tiles];
+    const int n_items = n_mt * nt_count;
+    const int per = (n_items + 7) / 8;
+    const int xcd = blockIdx.x & 7, local = blockIdx.x >> 3;
+    if (local >= per) return false;
+    const int item = xcd * per + local;
+    if (item >= n_items) return false;
+    t.nt = item / n_mt;
+    const int word = a.map[L.tiles + item % n_mt];
+    t.e = word >> 16;
+    const int mt = word & 0xFFFF;
+    const int cnt = a.map[L.tpe + t.e];
+    t.mrows = min(GM_BM, cnt - mt * GM_BM);
+    t.pos0 = a.map[L.off + t.e] + mt * GM_BM;
+    return true;
+}
+
+template <int DT, bool SWIGLU>
+__global__ void __launch_bounds__(64 * NWAVE) k_gemm(GemmArgs a) {
+    __shared__ __attribute__((aligned(1024))) uint8_t sA[2][STAGE_BYTES];
+    __shared__ int64_t s_src[GM_BM];  // byte offset of the A row
+    __shared__ float s_scale[GM_BM];
+    __shared__ int s_out[GM_BM];      // output row
+    constexpr int BN = 256;           // columns per block (SwiGLU: 128 gate + 128 up)
+    constexpr int NCOL = SWIGLU ? BN / 2 : BN;
+    const int nt_count = (a.n_out + NCOL - 1) / NCOL;
+    Tile tl;
+    if (!tile_of(a, nt_count, tl)) return;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int j = lane & 31, kh = lane >> 5;
+    {
+        const MapLayout L(a.n_map_expert, a.t, a.top_k);
+        if (tid < GM_BM) {
+            const int r = min(tid, tl.mrows - 1);  // rows past the tile repeat its last row
+            const int pos = tl.pos0 + r;
+            const int pair = a.map[L.list + pos];
+            const int64_t arow = a.a_by_token ? pair / a.top_k : pos;
+            s_src[tid] = arow * a.k * 2;
+            s_scale[tid] = a.a_scale[arow];
+            s_out[tid] = SWIGLU ? pos : pair / a.top_k * a.out_stride + pair % a.top_k + a.out_add;
+        }
+    }
+    __syncthreads();
+
+    // this lane's two weight rows (one per 32-column MFMA block)
+    const bool shared = tl.e >= a.n_expert;
+    const int64_t rb = shared ? a.sh_row_bytes : a.row_bytes;
+    const uint8_t *wrow[2];
+    int col[2];
+#pragma unroll
+    for (int nb = 0; nb < 2; nb++) {
+        const int m = SWIGLU ? nb : 0;
+        const uint8_t *base = shared ? a.w_sh[m] : a.w[m] + (int64_t)tl.e * a.expert_bytes;
+        col[nb] = SWIGLU ? tl.nt * NCOL + wave * 32 + j : tl.nt * NCOL + wave * 64 + nb * 32 + j;
+        wrow[nb] = base + (int64_t)min(col[nb], a.n_out - 1) * rb;
+    }
+
+    const uint8_t *abase = reinterpret_cast<const uint8_t *>(a.a);
+    // A stage copy: wave instruction i fills LDS rows 4 (8 wave + i) + lane / 16
+    auto issue_a = [&](int ks, uint8_t *buf) {
+#pragma unroll
+        for (int i = 0; i < DMA_PER_WAVE; i++) {
+            const int inst = DMA_PER_WAVE * wave + i;
+            const int row = 4 * inst + (lane >> 4);
+            const int c = (lane & 15) ^ (row & 15);
+            dma16(abase + s_src[row] + ks * ROWB + c * 16, buf + inst * 1024);
+        }
+    };
+
+    // per-lane LDS offsets of the A operand for the 8 steps of a stage
+    int aoff[8];
+#pragma unroll
+    for (int s = 0; s < 8; s++) {
+        const int c = 4 * (s >> 1) + 2 * kh + (s & 1);
+        aoff[s] = j * ROWB + ((c ^ (j & 15)) << 4);
+    }
+
+    float16_t acc[4][2];
+#pragma unroll
+    for (int mb = 0; mb < 4; mb++)
+#pragma unroll
+        for (int nb = 0; nb < 2; nb++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[mb][nb][r] = 0.f;
+
+    auto compute = [&](const uint8_t *buf, WB<DT>(&wb)[2]) {
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            const int p = s >> 1, hh = s & 1;
+            half8_t bf[2];
+#pragma unroll
+            for (int nb = 0; nb < 2; nb++) bf[nb] = wb[nb].step(p, hh);
+#pragma unroll
+            for (int mb = 0; mb < 4; mb++) {
+                const half8_t af = *reinterpret_cast<const half8_t *>(buf + mb * 32 * ROWB + aoff[s]);
+#pragma unroll
+                for (int nb = 0; nb < 2; nb++)
+                    acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[nb], acc[mb][nb], 0, 0, 0);
+            }
+        }
+    };
+
+    WB<DT> w0[2], w1[2];
+    const int nks = a.k / KS;  // even
+    issue_a(0, sA[0]);
+#pragma unroll
+    for (int nb = 0; nb < 2; nb++) w0[nb].load(wrow[nb], 0, kh);
+    wait_vmcnt(0);
+    __syncthreads();
+    for (int ks = 0; ks < nks; ks += 2) {
+        issue_a(ks + 1, sA[1]);
+#pragma unroll
+        for (int nb = 0; nb < 2; nb++) w1[nb].load(wrow[nb], ks + 1, kh);
+#pragma unroll
+        for (int nb = 0; nb < 2; nb++) w0[nb].template prep<0>(kh);
+        compute(sA[0], w0);
+        wait_vmcnt(0);
+        __syncthreads();
+        if (ks + 2 < nks) {
+            issue_a(ks + 2, sA[0]);
+#pragma unroll
+            for (int nb = 0; nb < 2; nb++) w0[nb].load(wrow[nb], ks + 2, kh);
+        }
+#pragma unroll
+        for (int nb = 0; nb < 2; nb++) w1[nb].template prep<1>(kh);
+        compute(sA[1], w1);
+        wait_vmcnt(0);
+        __syncthreads();
+    }
+
+    // epilogue: acc[mb][nb][r] = D[row 32 mb + 8 (r / 4) + 4 kh + r % 4][col[nb]]
+#pragma unroll
+    for (int mb = 0; mb < 4; mb++) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int row = 32 * mb + 8 * (r >> 2) + 4 * kh + (r & 3);
+            if (row >= tl.mrows) continue;
+            const float sc = s_scale[row];
+            float *orow = a.out + (int64_t)s_out[row] * a.n_out;
+            if constexpr (SWIGLU) {
+                if (col[0] < a.n_out) {
+                    const float g = acc[mb][0][r] * sc, u = acc[mb][1][r] * sc;
+                    orow[col[0]] = g / (1.0f + expf(-g)) * u;  // silu(g) * u (silu_mul.metal:57-72)
+                }
+            } else {
+#pragma unroll
+                for (int nb = 0; nb < 2; nb++)
+                    if (col[nb] < a.n_out) orow[col[nb]] = acc[mb][nb][r] * sc;
+            }
+        }
+    }
+}
+
+// ---- f32 rows -> scaled f16 rows ----------------------------------------------------
+__global__ void __launch_bounds__(256) k_to_f16_rows(const float *__restrict__ x, int k,
+                                                     const int32_t *__restrict__ count,
+                                                     _Float16 *__restrict__ y, float *__restrict__ scale) {
+    const int64_t row = blockIdx.x;
+    if (count && row >= *count) return;
+    __shared__ float s_red[4];
+    const float4 *xr = reinterpret_cast<const float4 *>(x + row * k);
+    const int n4 = k / 4;
+    float mx = 0.f;
+    for (int i = threadIdx.x; i < n4; i += 256) {
+        const float4 v = xr[i];
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+    // exponent so that max * 2^-ex lies in [2^14, 2^15)
+    const int ex = mx > 0.f ? ilogbf(mx) - 14 : 0;
+    const float inv = ldexpf(1.0f, -ex);
+    half4_t *yr = reinterpret_cast<half4_t *>(y + row * k);
+    for (int i = threadIdx.x; i < n4; i += 256) {
+        const float4 v = xr[i];
+        const half2_t lo = __builtin_convertvector((float2_t){v.x * inv, v.y * inv}, half2_t);
+        const half2_t hi = __builtin_convertvector((float2_t){v.z * inv, v.w * inv}, half2_t);
+        yr[i] = (half4_t){lo[0], lo[1], hi[0], hi[1]};
+    }
+    if (threadIdx.x == 0) scale[row] = ldexpf(1.0f, ex);
+}
+
+__global__ void k_ids_with_shared(const uint32_t *__restrict__ ids, int t, int top_k, int n_expert,
+                                  uint32_t *__restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int kk = top_k + 1;
+    if (i >= (int64_t)t * kk) return;
+    const int64_t tok = i / kk;
+    const int s = (int)(i % kk);
+    out[i] = s < top_k ? ids[tok * top_k + s] : (uint32_t)n_expert;
+}
+
+// out = residual + (sum_s w_s down_s) + shared   (moe.rs:78; combine.metal:16-40 order)
+__global__ void __launch_bounds__(256) k_combine_prefill(const float *__restrict__ down, const float *__restrict__ w,
+                                                         const float *__restrict__ residual, int top_k,
+                                                         int has_shared, int n, float *__restrict__ out) {
+    const int64_t tok = blockIdx.y;
+    const int i = (blockIdx.x * 256 + threadIdx.x) * 4;
+    if (i >= n) return;
+    const int kk = top_k + has_shared;
+    const float *d = down + tok * kk * n + i;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s = 0; s < top_k; s++) {
+        const float ws = w[tok * top_k + s];
+        const float4 v = *reinterpret_cast<const float4 *>(d + (int64_t)s * n);
+        acc.x = __builtin_fmaf(ws, v.x, acc.x);
+        acc.y = __builtin_fmaf(ws, v.y, acc.y);
+        acc.z = __builtin_fmaf(ws, v.z, acc.z);
+        acc.w = __builtin_fmaf(ws, v.w, acc.w);
+    }
+    if (has_shared) {
+        const float4 v = *reinterpret_cast<const float4 *>(d + (int64_t)top_k * n);
+        acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+    }
+    if (residual) {
+        const float4 r = *reinterpret_cast<const float4 *>(residual + tok * n + i);
+        acc.x = r.x + acc.x; acc.y = r.y + acc.y; acc.z = r.z + acc.z; acc.w = r.w + acc.w;
+    }
+    *reinterpret_cast<float4 *>(out + tok * n + i) = acc;
+}
+
+}  // namespace
+
+bool gemm_supported(int dtype, int k) {
+    return (dtype == kQ4_K || dtype == kQ6_K || dtype == kQ8_0) && k > 0 && k % 256 == 0;
+}
+
+mx_status launch_gemm(int dtype, bool swiglu, const GemmArgs &a, hipStream_t s) {
+    if (a.t == 0) return MX_OK;
+    const MapLayout L(a.n_map_expert, a.t, a.top_k);
+    const int ncol = swiglu ? 128 : 256;
+    const int64_t nt = (a.n_out + ncol - 1) / ncol;
+    const int64_t t_max = ((int64_t)a.t * a.top_k + GM_BM - 1) / GM_BM + a.n_map_expert;  // m-tiles of GM_BM
+    const int64_t blocks = (t_max * nt + 7) / 8 * 8;
+    if (blocks > INT32_MAX) return fail(MX_ERR_OVERFLOW, "gemm: too many tiles");
+    const dim3 grid((unsigned)blocks), block(64 * NWAVE);
+#define MX_G(DT, SW) hipLaunchKernelGGL((k_gemm<DT, SW>), grid, block, 0, s, a)
+    switch (dtype) {
+    case kQ4_K: if (swiglu) MX_G(kQ4_K, true); else MX_G(kQ4_K, false); break;
+    case kQ6_K: if (swiglu) MX_G(kQ6_K, true); else MX_G(kQ6_K, false); break;
+    default: if (swiglu) MX_G(kQ8_0, true); else MX_G(kQ8_0, false); break;
+    }
+#undef MX_G
+    (void)L;
+    MX_LAUNCH("k_gemm");
+    return MX_OK;
+}
+
+mx_status launch_to_f16_rows(const float *x, int64_t rows, int k, const int32_t *count, _Float16 *y, float *scale,
+                             hipStream_t s) {
+    if (rows == 0) return MX_OK;
+    hipLaunchKernelGGL(k_to_f16_rows, dim3((unsigned)rows), dim3(256), 0, s, x, k, count, y, scale);
+    MX_LAUNCH("k_to_f16_rows");
+    return MX_OK;
+}
+
+mx_status launch_ids_with_shared(const uint32_t *ids, int t, int top_k, int n_expert, uint32_t *ids_aug,
+                                 hipStream_t s) {
+    const int64_t n = (int64_t)t * (top_k + 1);
+    if (n == 0) return MX_OK;
+    hipLaunchKernelGGL(k_ids_with_shared, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, ids, t, top_k,
+                       n_expert, ids_aug);
+    MX_LAUNCH("k_ids_with_shared");
+    return MX_OK;
+}
+
+mx_status launch_combine_prefill(const float *down, const float *w, const float *residual, int t, int top_k,
+                                 int has_shared, int n, float *out, hipStream_t s) {
+    if (t == 0) return MX_OK;
+    const dim3 grid((unsigned)((n / 4 + 255) / 256), (unsigned)t);
+    hipLaunchKernelGGL(k_combine_prefill, grid, dim3(256), 0, s, down, w, residual, top_k, has_shared, n, out);
+    MX_LAUNCH("k_combine_prefill");
+    return MX_OK;
+}
+
+}  // namespace mx

@@ -92,9 +92,36 @@ mx_status launch_add3(const float *a, const float *b, const float *c, int64_t n,
                       hipStream_t s);
 
 // mx_mm.hip -- bucketing + grouped GEMM
+//
+// Bucket map (map0 scratch), int32 words:
+//   tpe[E] pairs per expert | off[E+1] first list position per expert |
+//   n_tiles | dup flags | tiles[t_max] (expert << 16 | m-tile) |
+//   list[t*top_k] pair indices (token*top_k + slot), grouped by expert, tokens
+//   ascending | chunk[nchunks][E] per-chunk counts (scratch of the build).
+// Sized for the smallest m-tile (MM_BM pairs); launch_map0 cuts m-tiles of
+// `bm` >= MM_BM pairs.
+constexpr int MM_BM = 64;
+constexpr int BK_CHUNK = 64;    // tokens per bucket chunk
+struct MapLayout {
+    int64_t tpe, off, n_tiles, dup, tiles, list, chunk;  // word offsets
+    int64_t t_max, nchunks, words;
+    __host__ __device__ MapLayout(int n_expert, int t, int top_k) {
+        const int64_t pairs = (int64_t)t * top_k;
+        t_max = (pairs + MM_BM - 1) / MM_BM + n_expert;
+        nchunks = (t + BK_CHUNK - 1) / BK_CHUNK;
+        tpe = 0;
+        off = n_expert;
+        n_tiles = off + n_expert + 1;
+        dup = n_tiles + 1;
+        tiles = dup + 1;
+        list = tiles + t_max;
+        chunk = list + pairs;
+        words = chunk + nchunks * n_expert;
+    }
+};
 size_t map0_bytes(int n_expert, int t, int top_k);
 mx_status launch_map0(const uint32_t *ids, int t, int top_k, int n_expert, int32_t *scratch,
-                      hipStream_t s);
+                      hipStream_t s, int bm = MM_BM);
 struct MmArgs {
     const uint8_t *w;
     int64_t expert_bytes, row_bytes;
@@ -106,5 +133,37 @@ struct MmArgs {
     float *dst;              // [t, top_k, n_out]
 };
 mx_status launch_mul_mm_id(int dtype, const MmArgs &a, hipStream_t s);
+
+// mx_gemm.hip -- MFMA grouped GEMM of the fused prefill path.
+// A operand: f16 rows scaled by a power of two per row (x = a * a_scale).
+constexpr int GM_BM = 128;   // pairs per m-tile (launch_map0 with bm = GM_BM)
+struct GemmArgs {
+    const uint8_t *w[2];        // routed stacks (first block of expert 0): [0] = gate / the
+                                // only matrix, [1] = up (SwiGLU)
+    const uint8_t *w_sh[2];     // map expert n_expert: shared expert (n_expert == 1 stacks)
+    int64_t expert_bytes, row_bytes, sh_row_bytes;
+    int n_expert, n_out, k;     // k % 256 == 0
+    const _Float16 *a;          // [rows, k]
+    const float *a_scale;       // [rows]
+    int a_by_token;             // 1: A row = pair / top_k, 0: A row = bucket position
+    int t, top_k, n_map_expert; // map geometry
+    const int32_t *map;         // built with bm = GM_BM
+    float *out;                 // SwiGLU: act [position, n_out]; plain: rows
+                                // (pair / top_k) * out_stride + pair % top_k + out_add
+    int out_stride, out_add;
+};
+bool gemm_supported(int dtype, int k);
+mx_status launch_gemm(int dtype, bool swiglu, const GemmArgs &a, hipStream_t s);
+// rows of x (f32, [rows, k], k % 4 == 0) -> f16 times a per-row power of two;
+// rows at or beyond *count (when count != NULL) are skipped
+mx_status launch_to_f16_rows(const float *x, int64_t rows, int k, const int32_t *count, _Float16 *y,
+                             float *scale, hipStream_t s);
+// ids_aug[t, top_k + 1]: ids with a last slot = n_expert (the shared expert)
+mx_status launch_ids_with_shared(const uint32_t *ids, int t, int top_k, int n_expert, uint32_t *ids_aug,
+                                 hipStream_t s);
+// out[t, n] = residual + sum_s w[t, s] * down[t * kk + s] + (has_shared ? down[t * kk + top_k] : 0),
+// kk = top_k + has_shared
+mx_status launch_combine_prefill(const float *down, const float *w, const float *residual, int t, int top_k,
+                                 int has_shared, int n, float *out, hipStream_t s);
 
 }  // namespace mx

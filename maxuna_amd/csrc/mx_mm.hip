@@ -17,29 +17,9 @@
 
 namespace mx {
 
-constexpr int MM_BM = 64;       // pairs per m-tile
 constexpr int MM_BN = 64;       // weight rows per n-tile
 constexpr int MM_BK = 256;      // K per step (one K-quant super-block)
 constexpr int MM_LDK = MM_BK + 8;  // padded LDS row (halves)
-constexpr int BK_CHUNK = 64;    // tokens per bucket chunk
-
-struct MapLayout {
-    int64_t tpe, off, n_tiles, dup, tiles, list, chunk;  // word offsets
-    int64_t t_max, nchunks, words;
-    __host__ __device__ MapLayout(int n_expert, int t, int top_k) {
-        const int64_t pairs = (int64_t)t * top_k;
-        t_max = (pairs + MM_BM - 1) / MM_BM + n_expert;
-        nchunks = (t + BK_CHUNK - 1) / BK_CHUNK;
-        tpe = 0;
-        off = n_expert;
-        n_tiles = off + n_expert + 1;
-        dup = n_tiles + 1;
-        tiles = dup + 1;
-        list = tiles + t_max;
-        chunk = list + pairs;
-        words = chunk + nchunks * n_expert;
-    }
-};
 
 size_t map0_bytes(int n_expert, int t, int top_k) {
     return (size_t)MapLayout(n_expert, t, top_k).words * 4;
@@ -71,7 +51,7 @@ __global__ void __launch_bounds__(256) k_bucket_count(const uint32_t *__restrict
 }
 
 // per-expert scan over chunks, expert offsets, tile list.  One block of 1024.
-__global__ void __launch_bounds__(1024) k_bucket_scan(int t, int top_k, int n_expert,
+__global__ void __launch_bounds__(1024) k_bucket_scan(int t, int top_k, int n_expert, int bm,
                                                       int32_t *__restrict__ map) {
     __shared__ int32_t s_a[1024], s_b[1024];
     const MapLayout L(n_expert, t, top_k);
@@ -89,7 +69,7 @@ __global__ void __launch_bounds__(1024) k_bucket_scan(int t, int top_k, int n_ex
         }
         map[L.tpe + e] = run;
         sum_pairs += run;
-        sum_tiles += (run + MM_BM - 1) / MM_BM;
+        sum_tiles += (run + bm - 1) / bm;
     }
     // block exclusive scan of (pairs, tiles) over threads
     s_a[tid] = sum_pairs;
@@ -106,7 +86,7 @@ __global__ void __launch_bounds__(1024) k_bucket_scan(int t, int top_k, int n_ex
     for (int e = e0; e < e1; e++) {
         const int n = map[L.tpe + e];
         map[L.off + e] = po;
-        const int mt = (n + MM_BM - 1) / MM_BM;
+        const int mt = (n + bm - 1) / bm;
         for (int m = 0; m < mt; m++) map[L.tiles + to + m] = (e << 16) | m;
         po += n;
         to += mt;
@@ -149,7 +129,7 @@ __global__ void k_zero_words(int32_t *__restrict__ p, int64_t n) {
 }
 
 mx_status launch_map0(const uint32_t *ids, int t, int top_k, int n_expert, int32_t *map,
-                      hipStream_t s) {
+                      hipStream_t s, int bm) {
     const MapLayout L(n_expert, t, top_k);
     // header (tpe, off, n_tiles, dup) starts at zero; the passes below fill it
     hipLaunchKernelGGL(k_zero_words, dim3((unsigned)((L.tiles + 255) / 256)), dim3(256), 0, s, map,
@@ -159,7 +139,7 @@ mx_status launch_map0(const uint32_t *ids, int t, int top_k, int n_expert, int32
     hipLaunchKernelGGL(k_bucket_count, dim3((unsigned)L.nchunks), dim3(256), n_expert * 4, s, ids, t,
                        top_k, n_expert, map);
     MX_LAUNCH("k_bucket_count");
-    hipLaunchKernelGGL(k_bucket_scan, dim3(1), dim3(1024), 0, s, t, top_k, n_expert, map);
+    hipLaunchKernelGGL(k_bucket_scan, dim3(1), dim3(1024), 0, s, t, top_k, n_expert, bm, map);
     MX_LAUNCH("k_bucket_scan");
     hipLaunchKernelGGL(k_bucket_fill, dim3((unsigned)L.nchunks), dim3(256),
                        BK_CHUNK * top_k * 4, s, ids, t, top_k, n_expert, map);

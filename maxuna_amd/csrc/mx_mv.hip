@@ -33,37 +33,13 @@
 // geometry dispatch.rs:409-462), silu_mul.metal:57-72, combine.metal:70-97.
 #include "mx_launch.h"
 #include "mx_stage.h"
+#include "mx_dma.h"
 
 namespace mx {
 
 __device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }
-
-// ---- wave-private LDS weight staging ------------------------------------------------
-#define MX_AS_LDS __attribute__((address_space(3)))
-#define MX_AS_GLB __attribute__((address_space(1)))
-
-// one 16-byte global -> LDS copy per lane; `lds_dst` must be wave-uniform (the
-// hardware writes lane i's 16 bytes at lds_dst + 16 * i)
-__device__ __forceinline__ void dma16(const uint8_t *src, uint8_t *lds_dst) {
-    __builtin_amdgcn_global_load_lds((MX_AS_GLB void *)src, (MX_AS_LDS void *)lds_dst, 16, 0, 0);
-}
-
-// s_waitcnt vmcnt(n) for a wave-uniform n in 0..63 (expcnt / lgkmcnt not waited)
-#define MX_VMW(n) \
-    case n: __builtin_amdgcn_s_waitcnt(0x0F70 | ((n) & 15) | (((n) >> 4) << 14)); break;
-__device__ __forceinline__ void wait_vmcnt(int n) {
-    switch (n) {
-        MX_VMW(0) MX_VMW(1) MX_VMW(2) MX_VMW(3) MX_VMW(4) MX_VMW(5) MX_VMW(6) MX_VMW(7)
-        MX_VMW(8) MX_VMW(9) MX_VMW(10) MX_VMW(11) MX_VMW(12) MX_VMW(13) MX_VMW(14) MX_VMW(15)
-        MX_VMW(16) MX_VMW(17) MX_VMW(18) MX_VMW(19) MX_VMW(20) MX_VMW(21) MX_VMW(22) MX_VMW(23)
-        MX_VMW(24) MX_VMW(25) MX_VMW(26) MX_VMW(27) MX_VMW(28) MX_VMW(29) MX_VMW(30) MX_VMW(31)
-        default: __builtin_amdgcn_s_waitcnt(0x0F70); break;
-    }
-    asm volatile("" ::: "memory");
-}
-#undef MX_VMW
 
 // DMA instructions for a batch of `rows` rows of `row_bytes` of nm matrices
 // (worst-case alignment: one extra chunk per matrix span)

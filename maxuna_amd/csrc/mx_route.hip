@@ -231,9 +231,86 @@ __global__ void __launch_bounds__(256) k_route_logits(const float *__restrict__ 
     }
 }
 
+// MFMA variant (hidden % 16 == 0): v_mfma_f32_32x32x2_f32, f32 products and sums.
+// Block = 32 tokens x 64 experts; its 8 waves split K in 16-wide chunks
+// (chunk c goes to wave c % 8) and the 8 partial tiles are summed in LDS in
+// wave order.  Inside a chunk, lane half kh holds k = 8kh .. 8kh+7 and MFMA
+// step s contracts k = s and 8 + s (the same permutation for both operands).
+constexpr int RL_T = 32, RL_E = 64, RL_W = 8, RL_KC = 16;
+
+__global__ void __launch_bounds__(64 * RL_W) k_route_logits_mfma(const float *__restrict__ x,
+                                                                  const float *__restrict__ r, int t, int hidden,
+                                                                  int n_expert, float *__restrict__ logits) {
+    __shared__ float red[RL_W][RL_T * RL_E];
+    const int t0 = blockIdx.y * RL_T, e0 = blockIdx.x * RL_E;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, i = lane & 31, kh = lane >> 5;
+    const float *xr = x + (int64_t)min(t0 + i, t - 1) * hidden + 8 * kh;
+    const float *ra = r + (int64_t)min(e0 + i, n_expert - 1) * hidden + 8 * kh;
+    const float *rb = r + (int64_t)min(e0 + 32 + i, n_expert - 1) * hidden + 8 * kh;
+    float16_t acc0, acc1;
+#pragma unroll
+    for (int q = 0; q < 16; q++) acc0[q] = acc1[q] = 0.f;
+    const int nch = hidden / RL_KC;
+    struct Chunk {
+        float4 x0, x1, a0, a1, b0, b1;
+    };
+    auto load = [&](int c, Chunk &v) {
+        const int64_t k = (int64_t)c * RL_KC;
+        v.x0 = *reinterpret_cast<const float4 *>(xr + k);
+        v.x1 = *reinterpret_cast<const float4 *>(xr + k + 4);
+        v.a0 = *reinterpret_cast<const float4 *>(ra + k);
+        v.a1 = *reinterpret_cast<const float4 *>(ra + k + 4);
+        v.b0 = *reinterpret_cast<const float4 *>(rb + k);
+        v.b1 = *reinterpret_cast<const float4 *>(rb + k + 4);
+    };
+    auto mma = [&](const Chunk &v) {
+        const float xs[8] = {v.x0.x, v.x0.y, v.x0.z, v.x0.w, v.x1.x, v.x1.y, v.x1.z, v.x1.w};
+        const float as[8] = {v.a0.x, v.a0.y, v.a0.z, v.a0.w, v.a1.x, v.a1.y, v.a1.z, v.a1.w};
+        const float bs[8] = {v.b0.x, v.b0.y, v.b0.z, v.b0.w, v.b1.x, v.b1.y, v.b1.z, v.b1.w};
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(xs[q], as[q], acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(xs[q], bs[q], acc1, 0, 0, 0);
+        }
+    };
+    Chunk c0, c1;
+    int c = wave;
+    if (c < nch) load(c, c0);
+    while (c < nch) {
+        if (c + RL_W < nch) load(c + RL_W, c1);
+        mma(c0);
+        c += RL_W;
+        if (c >= nch) break;
+        if (c + RL_W < nch) load(c + RL_W, c0);
+        mma(c1);
+        c += RL_W;
+    }
+    // acc[q] = D[token 8 (q / 4) + 4 kh + q % 4][expert i (+ 32)]
+#pragma unroll
+    for (int q = 0; q < 16; q++) {
+        const int row = 8 * (q >> 2) + 4 * kh + (q & 3);
+        red[wave][row * RL_E + i] = acc0[q];
+        red[wave][row * RL_E + 32 + i] = acc1[q];
+    }
+    __syncthreads();
+    for (int o = threadIdx.x; o < RL_T * RL_E; o += 64 * RL_W) {
+        float v = red[0][o];
+#pragma unroll
+        for (int w2 = 1; w2 < RL_W; w2++) v += red[w2][o];
+        const int tok = t0 + o / RL_E, e = e0 + o % RL_E;
+        if (tok < t && e < n_expert) logits[(int64_t)tok * n_expert + e] = v;
+    }
+}
+
 mx_status launch_route_logits(const float *x, const float *router, int t, int hidden, int n_expert, float *logits,
                               hipStream_t s) {
     if (t == 0) return MX_OK;
+    if (hidden % RL_KC == 0 && t >= 8) {
+        const dim3 grid((unsigned)((n_expert + RL_E - 1) / RL_E), (unsigned)((t + RL_T - 1) / RL_T));
+        hipLaunchKernelGGL(k_route_logits_mfma, grid, dim3(64 * RL_W), 0, s, x, router, t, hidden, n_expert, logits);
+        MX_LAUNCH("k_route_logits_mfma");
+        return MX_OK;
+    }
     const dim3 grid((unsigned)((n_expert + LG_E - 1) / LG_E), (unsigned)((t + LG_T - 1) / LG_T));
     hipLaunchKernelGGL(k_route_logits, grid, dim3(256), 0, s, x, router, t, hidden, n_expert, logits);
     MX_LAUNCH("k_route_logits");
