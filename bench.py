@@ -115,23 +115,27 @@ def bench_decode(args):
     log(f"decode: {steps} steps, {ms * 1e3:.2f} us/layer, {gbs:.0f} GB/s (wall {wall * 1e3:.1f} ms)")
     # per-stage HIP-event timing (eager, rotating layers) for the roofline of the dominant kernel
     stages = []
-    for r in range(args.profile_iters):
+    for r in range(max(1, args.profile_iters)):
         i = r % L
         stages.append(profiled(layers[i].block, xs[i], outs[i], 1))
-    st = np.array(stages).mean(0)  # route, gate_up, down (ms)
+    st = np.array(stages).mean(0)  # router logits, top-k + shared gate/up, routed gate/up, down (ms)
     eb_gu = 2 * spec.ff * (spec.hidden // 256) * 144
     eb_dn = spec.hidden * (spec.ff // 256) * 210
     k = spec.top_k
-    gu_bytes = (k + 1) * eb_gu + spec.hidden * 4
+    sh_bytes = eb_gu + spec.hidden * 4
+    gu_bytes = k * eb_gu + spec.hidden * 4
     dn_bytes = (k + 1) * eb_dn + (k + 1) * spec.ff * 4 + spec.hidden * 4
-    kern = {"k_decode_gate_up": (st[1], gu_bytes), "k_decode_down": (st[2], dn_bytes)}
+    kern = {"k_decode_gate_up (shared + top-k)": (st[1], sh_bytes), "k_decode_gate_up (routed)": (st[2], gu_bytes),
+            "k_decode_down": (st[3], dn_bytes)}
     dom = max(kern, key=lambda n: kern[n][0])
     dms, dbytes = kern[dom]
     roof = {"bound": "hbm", "kernel": dom, "achieved": round(dbytes / (dms * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(dbytes / (dms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "traffic": None, "bytes_per_launch": dbytes, "launch_us": round(dms * 1e3, 2)}
+    stage_us = {"route_logits": st[0] * 1e3, "select_shared_gate_up": st[1] * 1e3, "gate_up": st[2] * 1e3,
+                "down": st[3] * 1e3}
     return dict(ms_per_step=ms, steps=steps, gbs=gbs, bytes_per_step=bytes_per_step, uniq=uniq,
-                stage_us={"route": st[0] * 1e3, "gate_up": st[1] * 1e3, "down": st[2] * 1e3}, roofline=roof,
+                stage_us=stage_us, roofline=roof,
                 layers=layers)
 
 
@@ -160,16 +164,20 @@ def bench_prefill(args):
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / args.prefill_steps
     st = np.array([profiled(layer.block, x, out, t) for _ in range(3)]).mean(0)
-    names = ["route", "map0", "gate", "up", "silu", "down", "combine", "shared", "add"]
+    names = ["route", "map0", "x_f16", "gate_up_gemm", "act_f16", "down_gemm", "combine"]
     stage_us = {n: round(v * 1e3, 1) for n, v in zip(names, st)}
-    pairs = t * spec.top_k
-    gate_flops = 2 * pairs * spec.ff * spec.hidden
-    tf = gate_flops / (st[2] * 1e-3) / 1e12
-    log(f"prefill: {ms:.3f} ms/layer, {flops / (ms * 1e-3) / 1e12:.1f} TFLOP/s, gate GEMM {tf:.1f} TFLOP/s")
+    kk = spec.top_k + (1 if spec.shared else 0)
+    gu_flops = 2 * 2 * t * kk * spec.ff * spec.hidden
+    dn_flops = 2 * t * kk * spec.hidden * spec.ff
+    gemms = {"k_gemm gate/up (SwiGLU)": (st[3], gu_flops), "k_gemm down": (st[5], dn_flops)}
+    dom = max(gemms, key=lambda n: gemms[n][0])
+    tf = gemms[dom][1] / (gemms[dom][0] * 1e-3) / 1e12
+    log(f"prefill: {ms:.3f} ms/layer, {flops / (ms * 1e-3) / 1e12:.1f} TFLOP/s, {dom} {tf:.1f} TFLOP/s")
     return dict(ms=ms, tflops=flops / (ms * 1e-3) / 1e12, gbs=nbytes / (ms * 1e-3) / 1e9, flops=flops,
                 bytes=nbytes, uniq=uniq, stage_us=stage_us,
-                gate_gemm={"kernel": "k_mul_mm_id<Q4_K>", "achieved": round(tf, 1), "peak": MFMA_F16_PEAK_TFLOPS,
-                           "unit": "TFLOP/s", "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4)},
+                gate_gemm={"bound": "mfma", "kernel": dom, "achieved": round(tf, 1), "peak": MFMA_F16_PEAK_TFLOPS,
+                           "unit": "TFLOP/s", "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
+                           "flops_per_launch": gemms[dom][1], "launch_us": round(gemms[dom][0] * 1e3, 1)},
                 tokens_per_s=t / (ms * 1e-3))
 
 

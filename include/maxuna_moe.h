@@ -214,8 +214,11 @@ mx_status mx_moe_forward(const mx_moe_layer *layer, const float *x, int64_t t,
 
 /* Same as mx_moe_forward, and additionally records a HIP event after each
  * stage on `stream`, waits for the last one and returns the stage durations
- * in milliseconds (decode: route, gate_up+SwiGLU, down+combine; grouped path:
- * route, map0, gate, up, silu, down, combine, shared, add).  For profiling
+ * in milliseconds.  Decode (t < mm_min_seq): router logits, top-k + shared
+ * gate/up (t <= 4; empty otherwise), routed gate/up + SwiGLU, down + combine.
+ * Grouped path: route, map0, x -> f16, then per bucket map gate/up GEMM +
+ * SwiGLU, act -> f16, down GEMM (one map when the shared expert has the
+ * routed quant types, else a second map for it), then combine.  For profiling
  * and the benchmark; no reference counterpart.  Not capturable. */
 mx_status mx_moe_forward_profiled(const mx_moe_layer *layer, const float *x, int64_t t,
                                   const float *residual, float *out, uint32_t *ids_out,

@@ -470,10 +470,11 @@ mx_status moe_forward_impl(const mx_moe_layer *L, const float *x, int64_t t, con
 
     // routing (+ the RMSNorm of the FFN half when requested)
     if (p.fused_router) {
-        // the router also stages the (normalised) rows for the decode expert kernels
+        // logits -> keys/probs; the router also stages the (normalised) rows for the
+        // decode expert kernels.  The top-k runs in the selection blocks of the next
+        // launch (below).
         MX_TRY(launch_route_fused(x, L->rms_alpha, L->rms_eps, o.x_normed, L->router, L->exp_probs_b, (int)t,
-                                  (int)H, (int)E, (int)K, scale, apply, L->weights_norm, ids, w, o.route_ws,
-                                  o.xstage, s));
+                                  (int)H, (int)E, o.route_ws, o.xstage, s));
         if (L->rms_alpha) xin = o.x_normed;
     } else {
         if (L->rms_alpha) {
@@ -504,7 +505,20 @@ mx_status moe_forward_impl(const mx_moe_layer *L, const float *x, int64_t t, con
         }
         DecodeGateUpArgs ga{gg.w, gu.w, gg.expert_bytes, gg.row_bytes, shf ? sg.w : nullptr, shf ? su.w : nullptr,
                             sg.row_bytes, (int)E, (int)FF, (int)H, o.xstage, ids, (int)t, (int)K, o.act};
-        MX_TRY(launch_decode_gate_up(L->gate.dtype, ga, s));
+        if (p.fused_router) {
+            // the top-k of every token, next to the shared expert's gate/up rows (which
+            // need no routing) -- then the routed slots, which read the selection
+            const uint8_t *keys = static_cast<const uint8_t *>(o.route_ws);
+            DecodeSelArgs sel{reinterpret_cast<const uint64_t *>(keys),
+                              reinterpret_cast<const float *>(keys + (size_t)t * E * sizeof(uint64_t)), (int)E,
+                              (int)t, scale, apply, L->weights_norm, ids, w};
+            MX_TRY(launch_decode_gate_up(L->gate.dtype, ga, (int)K, shf ? 1 : 0, &sel, s));
+            MX_STAGE();
+            MX_TRY(launch_decode_gate_up(L->gate.dtype, ga, 0, (int)K, nullptr, s));
+        } else {
+            MX_STAGE();
+            MX_TRY(launch_decode_gate_up(L->gate.dtype, ga, 0, (int)K + (shf ? 1 : 0), nullptr, s));
+        }
         MX_STAGE();
         DecodeDownArgs da{gd.w, gd.expert_bytes, gd.row_bytes, shf ? sd.w : nullptr, sd.row_bytes, shared_out,
                           (int)E, (int)FF, (int)H, o.act, ids, w, residual, (int)t, (int)K, out, o.part,
@@ -552,8 +566,10 @@ mx_status moe_forward_impl(const mx_moe_layer *L, const float *x, int64_t t, con
         ga.t = (int)t; ga.top_k = top_k; ga.n_map_expert = n_map_expert; ga.map = map;
         ga.out = o.act + act_row0 * FF;
         MX_TRY(launch_gemm(dt_gu, true, ga, s));
+        MX_STAGE();
         MX_TRY(launch_to_f16_rows(ga.out, t * top_k, (int)FF, map + LM.off + n_map_expert,
                                   o.act16 + act_row0 * FF, o.act16s + act_row0, s));
+        MX_STAGE();
         GemmArgs da = ga;
         da.w[0] = wd; da.w[1] = nullptr;
         da.w_sh[0] = shd; da.w_sh[1] = nullptr;
@@ -561,7 +577,9 @@ mx_status moe_forward_impl(const mx_moe_layer *L, const float *x, int64_t t, con
         da.n_out = (int)H; da.k = (int)FF;
         da.a = o.act16 + act_row0 * FF; da.a_scale = o.act16s + act_row0; da.a_by_token = 0;
         da.out = o.down; da.out_stride = KK; da.out_add = out_add;
-        return launch_gemm(dt_d, false, da, s);
+        MX_TRY(launch_gemm(dt_d, false, da, s));
+        MX_STAGE();
+        return MX_OK;
     };
     if (one_map) {
         MX_TRY(experts(o.map, EM, KM, (int)E, gg.w, gu.w, gd.w, sg.w, su.w, sd.w, 0, 0, L->gate.dtype,
@@ -573,7 +591,6 @@ mx_status moe_forward_impl(const mx_moe_layer *L, const float *x, int64_t t, con
             MX_TRY(experts(o.map_sh, 1, 1, 0, nullptr, nullptr, nullptr, sg.w, su.w, sd.w, t * K, (int)K,
                            L->shared_gate.dtype, L->shared_down.dtype, sg, sd, sg, sd));
     }
-    MX_STAGE();
     MX_TRY(launch_combine_prefill(o.down, w, residual, (int)t, (int)K, S, (int)H, out, s));
     MX_STAGE();
     return MX_OK;

@@ -38,8 +38,22 @@ struct DecodeGateUpArgs {
     int t, top_k;
     float *act;                          // [t, slots, ff], slots = top_k + (sh_gate != NULL)
 };
-// the shared expert (sh_gate/sh_up != NULL) must have the routed experts' quant type
-mx_status launch_decode_gate_up(int dtype, const DecodeGateUpArgs &a, hipStream_t s);
+// Optional top-k blocks in front of the gate/up blocks (decode router split):
+// block i < n_sel selects token i from keys/probs [n_sel, n_expert] (written by
+// launch_route_fused) into ids/w [n_sel, top_k].
+struct DecodeSelArgs {
+    const uint64_t *keys;
+    const float *probs;
+    int n_expert, n_sel;
+    float scale;
+    int apply_scale, norm;
+    uint32_t *ids;
+    float *w;
+};
+// Slots slot0 .. slot0 + nslot - 1 of every token (slot top_k = the shared
+// expert, which must have the routed experts' quant type); sel may be NULL.
+mx_status launch_decode_gate_up(int dtype, const DecodeGateUpArgs &a, int slot0, int nslot,
+                                const DecodeSelArgs *sel, hipStream_t s);
 
 struct DecodeDownArgs {
     const uint8_t *down;
@@ -67,17 +81,16 @@ mx_status launch_route_logits(const float *x, const float *router, int t, int hi
 mx_status launch_route_select(const float *logits, const float *bias, int t, int n_expert,
                               int top_k, float scale, int apply_scale, int norm, uint32_t *ids,
                               float *w, hipStream_t s);
-// Decode router: RMSNorm (optional) + logits + select for t tokens in one
-// launch using a last-block reduction; also stages the (normalised) rows into
-// `xstage` (mx_stage.h layout) and/or writes them to `x_normed` when non-NULL.
-// ws: logits + counter (zeroed once, self-resetting).
+// Decode router, first half: RMSNorm (optional) + logits -> sigmoid
+// probabilities and selection sort keys for t tokens (ws: keys u64 [t, E] |
+// probs f32 [t, E]); also stages the (normalised) rows into `xstage`
+// (mx_stage.h layout) and/or writes them to `x_normed` when non-NULL.  The
+// top-k runs in the selection blocks of launch_decode_gate_up.
 size_t route_fused_ws_bytes(int t, int hidden, int n_expert);
 int route_fused_max_t();
 mx_status launch_route_fused(const float *x, const float *rms_alpha, float rms_eps,
                              float *x_normed, const float *router, const float *bias, int t,
-                             int hidden, int n_expert, int top_k, float scale, int apply_scale,
-                             int norm, uint32_t *ids, float *w, void *ws, uint8_t *xstage,
-                             hipStream_t s);
+                             int hidden, int n_expert, void *ws, uint8_t *xstage, hipStream_t s);
 // Stages t rows of k values (mx_stage.h layout, xstage_bytes(k) per row).
 mx_status launch_stage_rows(const float *x, int t, int k, uint8_t *xstage, hipStream_t s);
 size_t stage_row_bytes(int k);

@@ -34,6 +34,7 @@
 #include "mx_launch.h"
 #include "mx_stage.h"
 #include "mx_dma.h"
+#include "mx_select.h"
 
 namespace mx {
 
@@ -429,7 +430,11 @@ __device__ __forceinline__ void load_xs(const uint8_t *staged, int k, const Geo<
 #ifndef MX_NIT2
 #define MX_NIT2 1
 #endif
+#ifndef MX_WAVES_DN
+#define MX_WAVES_DN 4
+#endif
 constexpr int WAVES = MX_WAVES;
+constexpr int WAVES_DN = MX_WAVES_DN;  // waves per block of the fused down kernel
 constexpr int RW_MV = 16, RW_GU = MX_RW_GU, RW_DN = MX_RW_DN;
 constexpr int RING_MV = 2, RING_GU = MX_RING_GU, RING_DN = MX_RING_DN;
 
@@ -522,18 +527,40 @@ mx_status launch_mul_mv_id(int dtype, const MvArgs &a, hipStream_t s) {
 }
 
 // ---- fused decode: gate/up + SwiGLU ---------------------------------------------------
-// grid (ff / (WAVES * RW_GU), slots, t); slot top_k (if present) is the shared
-// expert, which then has the routed experts' quant type and shape.
+// Flattened grid: sel.n_sel selection blocks, then (ff / (WAVES * RW_GU)) row
+// tiles x nslot slots x t tokens.  Slots slot0 .. slot0 + nslot - 1; slot
+// top_k (if present) is the shared expert, which then has the routed experts'
+// quant type and shape.
 // act[tok, slot, r] = silu(gate_r . x) * (up_r . x), silu(g) = g / (1 + exp(-g)),
 // the product rounded on its own (silu_mul.metal:57-72).  The token row comes
-// staged from the router kernel (global memory).  Waves are independent.
+// staged from the router kernel (global memory).  Expert waves are independent.
+// Selection block i (decode router split, mx_route.hip) runs the top-k of
+// token i from the router's keys and writes ids / weights; the routed slots
+// are launched in the next kernel, which reads them.  The shared expert's
+// blocks need no routing, so they fill the machine while the selection runs.
+#ifndef MX_GU_WPE
+#define MX_GU_WPE 6
+#endif
 template <int DT, int NG>
-__global__ void __launch_bounds__(64 * WAVES) k_decode_gate_up(DecodeGateUpArgs a, int ni) {
+__global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(MX_GU_WPE))) k_decode_gate_up(DecodeGateUpArgs a, int ni, int slot0, int nslot,
+                                                               DecodeSelArgs sel) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    const int slot = blockIdx.y, tok = blockIdx.z;
+    int bid = blockIdx.x;
+    if (bid < sel.n_sel) {
+        // the selection state lives in the dynamic LDS (a static __shared__ would be
+        // reserved by every block of the launch and cut the expert blocks' occupancy)
+        SelShared &sh = *reinterpret_cast<SelShared *>(lds);
+        const int64_t o = (int64_t)bid * sel.n_expert;
+        topk_from_keys(sel.keys + o, sel.probs + o, sel.n_expert, a.top_k, sel.scale, sel.apply_scale, sel.norm,
+                       sel.ids + (int64_t)bid * a.top_k, sel.w + (int64_t)bid * a.top_k, sh);
+        return;
+    }
+    bid -= sel.n_sel;
+    const int tiles = (a.ff + WAVES * RW_GU - 1) / (WAVES * RW_GU);
+    const int tile = bid % tiles, slot = slot0 + (bid / tiles) % nslot, tok = bid / (tiles * nslot);
     const int wave = threadIdx.x >> 6;
-    const int r0 = blockIdx.x * (WAVES * RW_GU) + wave * RW_GU;
-    if (r0 >= a.ff) return;  // wave-uniform; no block barrier in this kernel
+    const int r0 = tile * (WAVES * RW_GU) + wave * RW_GU;
+    if (r0 >= a.ff) return;  // wave-uniform; no block barrier below
     const int slots = a.top_k + (a.sh_gate ? 1 : 0);
     float *act = a.act + ((int64_t)tok * slots + slot) * a.ff;
     const uint8_t *gw, *uw;
@@ -564,54 +591,67 @@ __global__ void __launch_bounds__(64 * WAVES) k_decode_gate_up(DecodeGateUpArgs 
 }
 
 template <int DT, int NG>
-static mx_status launch_gu_ng(const DecodeGateUpArgs &a, dim3 grid, hipStream_t s) {
+static mx_status launch_gu_ng(const DecodeGateUpArgs &a, unsigned blocks, int slot0, int nslot,
+                              const DecodeSelArgs &sel, hipStream_t s) {
     const int ni = ring_insts<DT, NG>(2, a.hidden, a.gu_row_bytes);
     if (ni > DMA_MAX_INSTS) return fail(MX_ERR_SHAPE, "decode gate/up: rows too long for the LDS ring");
-    const size_t lds = (size_t)WAVES * RING_GU * ni * 1024;
+    size_t lds = (size_t)WAVES * RING_GU * ni * 1024;
+    if (sel.n_sel && lds < sizeof(SelShared)) lds = sizeof(SelShared);
     if (lds > 160 * 1024) return fail(MX_ERR_SHAPE, "decode gate/up: hidden = %d needs %zu bytes of LDS", a.hidden, lds);
-    hipLaunchKernelGGL((k_decode_gate_up<DT, NG>), grid, dim3(64 * WAVES), lds, s, a, ni);
+    hipLaunchKernelGGL((k_decode_gate_up<DT, NG>), dim3(blocks), dim3(64 * WAVES), lds, s, a, ni, slot0, nslot, sel);
     return MX_OK;
 }
 
 template <int DT>
-static mx_status launch_gu_dt(const DecodeGateUpArgs &a, dim3 grid, hipStream_t s) {
+static mx_status launch_gu_dt(const DecodeGateUpArgs &a, unsigned blocks, int slot0, int nslot,
+                              const DecodeSelArgs &sel, hipStream_t s) {
     const int ng = ng_variant(Geo<DT>(a.hidden).NG);
-#define MX_L(N) return launch_gu_ng<DT, N>(a, grid, s)
+#define MX_L(N) return launch_gu_ng<DT, N>(a, blocks, slot0, nslot, sel, s)
     MX_NG_SWITCH(ng, MX_L)
 #undef MX_L
     return MX_OK;
 }
 
-mx_status launch_decode_gate_up(int dtype, const DecodeGateUpArgs &a, hipStream_t s) {
-    const dim3 grid((unsigned)((a.ff + WAVES * RW_GU - 1) / (WAVES * RW_GU)),
-                    (unsigned)(a.top_k + (a.sh_gate ? 1 : 0)), (unsigned)a.t);
-    if (grid.x == 0 || a.t == 0) return MX_OK;
+mx_status launch_decode_gate_up(int dtype, const DecodeGateUpArgs &a, int slot0, int nslot,
+                                const DecodeSelArgs *sel, hipStream_t s) {
+    DecodeSelArgs none{};
+    const DecodeSelArgs &sa = sel ? *sel : none;
+    if (a.t == 0) return MX_OK;
+    if (sa.n_sel && (sa.n_expert > SEL_MAX_E || a.top_k > SEL_MAX_K || 64 * WAVES != SEL_THREADS))
+        return fail(MX_ERR_SHAPE, "decode select: n_expert <= %d and top_k <= %d", SEL_MAX_E, SEL_MAX_K);
+    const int64_t tiles = (a.ff + WAVES * RW_GU - 1) / (WAVES * RW_GU);
+    const int64_t blocks = sa.n_sel + tiles * nslot * a.t;
+    if (blocks == 0) return MX_OK;
+    if (blocks > INT32_MAX) return fail(MX_ERR_OVERFLOW, "decode gate/up: grid too large");
     if (a.hidden % 32) return fail(MX_ERR_BLOCK, "decode gate/up: hidden must be a multiple of 32");
     if (a.sh_gate && a.sh_row_bytes != a.gu_row_bytes)
         return fail(MX_ERR_SHAPE, "decode gate/up: shared expert rows must match the routed rows");
     switch (dtype) {
-    case kQ4_K: MX_TRY(launch_gu_dt<kQ4_K>(a, grid, s)); break;
-    case kQ6_K: MX_TRY(launch_gu_dt<kQ6_K>(a, grid, s)); break;
-    default: MX_TRY(launch_gu_dt<kQ8_0>(a, grid, s)); break;
+    case kQ4_K: MX_TRY(launch_gu_dt<kQ4_K>(a, (unsigned)blocks, slot0, nslot, sa, s)); break;
+    case kQ6_K: MX_TRY(launch_gu_dt<kQ6_K>(a, (unsigned)blocks, slot0, nslot, sa, s)); break;
+    default: MX_TRY(launch_gu_dt<kQ8_0>(a, (unsigned)blocks, slot0, nslot, sa, s)); break;
     }
     MX_LAUNCH("k_decode_gate_up");
     return MX_OK;
 }
 
 // ---- fused decode: down (one slot per block) + last-block weighted combine ---------------
-// grid (hidden / (WAVES * RW_DN), n_slot_blocks, t).  Each block writes its slot's
+// grid (hidden / (WAVES_DN * RW_DN), n_slot_blocks, t).  Each block writes its slot's
 // down rows to part[tok, slot, :]; the last of the n_slot_blocks blocks of a
 // (tok, row tile) to finish (device-scope counter) combines them in slot order:
 //   out[c] = residual[c] + ( sum_k w[k] * part[k][c] + part[shared][c] )
 // (combine.metal:70-97, moe.rs:73-78, model.rs:351) and resets the counter.  When
 // the shared expert has another quant type than the routed experts, the host
 // computes it separately and passes it as a.shared_out (a.sh_down == NULL).
+#ifndef MX_DN_WPE
+#define MX_DN_WPE 1
+#endif
 template <int DT, int NG>
-__global__ void __launch_bounds__(64 * WAVES) k_decode_down(DecodeDownArgs a, int ni) {
+__global__ void __launch_bounds__(64 * WAVES_DN) __attribute__((amdgpu_waves_per_eu(MX_DN_WPE))) k_decode_down(DecodeDownArgs a, int ni) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     __shared__ int s_last;
     const int slot = blockIdx.y, tok = blockIdx.z;
-    constexpr int ROWS_PER_WG = WAVES * RW_DN;
+    constexpr int ROWS_PER_WG = WAVES_DN * RW_DN;
     const int tile0 = blockIdx.x * ROWS_PER_WG;
     const int wave = threadIdx.x >> 6;
     const int r0 = tile0 + wave * RW_DN;
@@ -673,9 +713,9 @@ template <int DT, int NG>
 static mx_status launch_dn_ng(const DecodeDownArgs &a, dim3 grid, hipStream_t s) {
     const int ni = ring_insts<DT, NG>(1, a.ff, a.d_row_bytes);
     if (ni > DMA_MAX_INSTS) return fail(MX_ERR_SHAPE, "decode down: rows too long for the LDS ring");
-    const size_t lds = align16(xstage_bytes(a.ff)) + (size_t)WAVES * RING_DN * ni * 1024;
+    const size_t lds = align16(xstage_bytes(a.ff)) + (size_t)WAVES_DN * RING_DN * ni * 1024;
     if (lds > 160 * 1024) return fail(MX_ERR_SHAPE, "decode down: expert_ff = %d needs %zu bytes of LDS", a.ff, lds);
-    hipLaunchKernelGGL((k_decode_down<DT, NG>), grid, dim3(64 * WAVES), lds, s, a, ni);
+    hipLaunchKernelGGL((k_decode_down<DT, NG>), grid, dim3(64 * WAVES_DN), lds, s, a, ni);
     return MX_OK;
 }
 
@@ -689,11 +729,11 @@ static mx_status launch_dn_dt(const DecodeDownArgs &a, dim3 grid, hipStream_t s)
 }
 
 size_t decode_down_counter_words(int t, int hidden) {
-    return (size_t)t * (size_t)((hidden + WAVES * RW_DN - 1) / (WAVES * RW_DN));
+    return (size_t)t * (size_t)((hidden + WAVES_DN * RW_DN - 1) / (WAVES_DN * RW_DN));
 }
 
 mx_status launch_decode_down(int dtype, const DecodeDownArgs &a, hipStream_t s) {
-    const dim3 grid((unsigned)((a.hidden + WAVES * RW_DN - 1) / (WAVES * RW_DN)),
+    const dim3 grid((unsigned)((a.hidden + WAVES_DN * RW_DN - 1) / (WAVES_DN * RW_DN)),
                     (unsigned)(a.top_k + (a.sh_down ? 1 : 0)), (unsigned)a.t);
     if (grid.x == 0 || a.t == 0) return MX_OK;
     if (a.ff % 32) return fail(MX_ERR_BLOCK, "decode down: expert_ff must be a multiple of 32");

@@ -14,151 +14,33 @@
 // its matmul (moe.rs:43), which this layout makes unnecessary.
 #include "mx_launch.h"
 #include "mx_stage.h"
+#include "mx_select.h"
 
 namespace mx {
 
-constexpr int RT_THREADS = 256;
-constexpr int RT_MAX_E = 1024;
-constexpr int RT_MAX_K = 32;
+constexpr int RT_THREADS = SEL_THREADS;
+static_assert(SEL_MAX_E == 1024 && SEL_MAX_K == 32, "route limits: n_expert <= 1024, top_k <= 32");
 
-// Sort key of a stable descending sort on the selection score: the score's
-// bits mapped to an unsigned order (-0 folded to +0 first, so equal floats get
-// equal keys) in the high word, the complemented expert id in the low word
-// (equal scores -> the lower id ranks first).  Larger key = earlier position.
-__device__ __forceinline__ uint64_t sel_key(float v, int e) {
-    v = v + 0.0f;  // -0 -> +0
-    const uint32_t b = __float_as_uint(v);
-    const uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-    return ((uint64_t)o << 32) | (uint32_t)(~(uint32_t)e);
-}
-
-// Block-wide stable top-k for one token.  Each expert's position in the stable
-// descending order is its rank: the number of experts with a larger key.  The
-// keys sit in LDS and every thread counts against all of them with 16-byte
-// broadcast reads (independent, so they pipeline).  `logits` may be in shared
-// or global memory; all RT_THREADS threads must call.
+// Block-wide stable top-k for one token from its logits (mx_select.h).
+// `logits` may be in shared or global memory; all RT_THREADS threads must call.
 __device__ void select_token(const float *logits, const float *__restrict__ bias, int n_expert, int top_k,
                              float scale, int apply_scale, int norm, uint32_t *__restrict__ ids_out,
                              float *__restrict__ w_out) {
-    constexpr int PER = RT_MAX_E / RT_THREADS;
-    __shared__ __attribute__((aligned(16))) uint64_t s_key[RT_MAX_E];
-    __shared__ float s_prob[RT_MAX_K];
-    __shared__ int s_pick[RT_MAX_K];
-    const int tid = threadIdx.x;
-    float prob[PER];
-    uint64_t key[PER];
+    __shared__ SelShared sh;
+    uint64_t key[SEL_PER];
+    float prob[SEL_PER];
 #pragma unroll
-    for (int j = 0; j < PER; j++) {
-        const int e = tid + RT_THREADS * j;
+    for (int j = 0; j < SEL_PER; j++) {
+        const int e = threadIdx.x + SEL_THREADS * j;
         prob[j] = 0.f;
         key[j] = 0;
         if (e < n_expert) {
             const float ex = expf(-logits[e]);
-            prob[j] = 1.0f / (ex + 1.0f);
+            prob[j] = 1.0f / (ex + 1.0f);  // sigmoid (moe.rs:101)
             key[j] = sel_key(prob[j] + bias[e], e);
-            s_key[e] = key[j];
         }
     }
-    // pad to a multiple of 2 keys with key 0 (no real key is smaller)
-    if (tid == 0 && (n_expert & 1)) s_key[n_expert] = 0;
-    __syncthreads();
-    const int npair = (n_expert + 1) >> 1;
-    const ulonglong2 *kp = reinterpret_cast<const ulonglong2 *>(s_key);
-#pragma unroll
-    for (int j = 0; j < PER; j++) {
-        const int e = tid + RT_THREADS * j;
-        if (j * RT_THREADS < n_expert) {  // block-uniform skip of empty rounds
-            int rank = 0;
-            const uint64_t mine = key[j];
-#pragma unroll 8
-            for (int i = 0; i < npair; i++) {
-                const ulonglong2 v = kp[i];
-                rank += (v.x > mine) + (v.y > mine);
-            }
-            if (e < n_expert && rank < top_k) {
-                s_pick[rank] = e;
-                s_prob[rank] = prob[j];
-            }
-        }
-    }
-    __syncthreads();
-    if (tid == 0) {
-        float sum = 0.f;
-        for (int k = 0; k < top_k; k++) sum = sum + s_prob[k];
-        if (sum < 6.103515625e-5f) sum = 6.103515625e-5f;
-        for (int k = 0; k < top_k; k++) {
-            float wk = s_prob[k];
-            if (norm) wk = wk / sum;
-            if (apply_scale) wk = wk * scale;
-            ids_out[k] = (uint32_t)s_pick[k];
-            w_out[k] = wk;
-        }
-    }
-    __syncthreads();
-}
-
-// Top-k from published sort keys and probabilities (device-scope coherent
-// loads): rank = number of larger keys, in LDS with 16-byte broadcast reads.
-// The weight sum runs in slot order on one thread, the divisions one slot per
-// thread.  All RT_THREADS threads must call.
-__device__ void select_from_keys(const uint64_t *keys, const float *probs, int n_expert, int top_k, float scale,
-                                 int apply_scale, int norm, uint32_t *__restrict__ ids_out,
-                                 float *__restrict__ w_out) {
-    constexpr int PER = RT_MAX_E / RT_THREADS;
-    __shared__ __attribute__((aligned(16))) uint64_t s_key[RT_MAX_E];
-    __shared__ float s_prob[RT_MAX_K];
-    __shared__ int s_pick[RT_MAX_K];
-    __shared__ float s_sum;
-    const int tid = threadIdx.x;
-    uint64_t key[PER];
-    float prob[PER];
-#pragma unroll
-    for (int j = 0; j < PER; j++) {
-        const int e = tid + RT_THREADS * j;
-        key[j] = 0;
-        prob[j] = 0.f;
-        if (e < n_expert) {
-            key[j] = __hip_atomic_load(const_cast<uint64_t *>(keys) + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            prob[j] = ld_agent(probs + e);
-            s_key[e] = key[j];
-        }
-    }
-    if (tid == 0 && (n_expert & 1)) s_key[n_expert] = 0;  // pad with key 0 (no real key is smaller)
-    __syncthreads();
-    const int npair = (n_expert + 1) >> 1;
-    const ulonglong2 *kp = reinterpret_cast<const ulonglong2 *>(s_key);
-#pragma unroll
-    for (int j = 0; j < PER; j++) {
-        const int e = tid + RT_THREADS * j;
-        if (j * RT_THREADS < n_expert) {  // block-uniform skip of empty rounds
-            int rank = 0;
-            const uint64_t mine = key[j];
-#pragma unroll 8
-            for (int i = 0; i < npair; i++) {
-                const ulonglong2 v = kp[i];
-                rank += (v.x > mine) + (v.y > mine);
-            }
-            if (e < n_expert && rank < top_k) {
-                s_pick[rank] = e;
-                s_prob[rank] = prob[j];
-            }
-        }
-    }
-    __syncthreads();
-    if (tid == 0) {
-        float sum = 0.f;
-        for (int k = 0; k < top_k; k++) sum = sum + s_prob[k];
-        s_sum = sum < 6.103515625e-5f ? 6.103515625e-5f : sum;
-    }
-    __syncthreads();
-    if (tid < top_k) {
-        float wk = s_prob[tid];
-        if (norm) wk = wk / s_sum;
-        if (apply_scale) wk = wk * scale;
-        ids_out[tid] = (uint32_t)s_pick[tid];
-        w_out[tid] = wk;
-    }
-    __syncthreads();
+    topk_select(key, prob, n_expert, top_k, scale, apply_scale, norm, ids_out, w_out, sh);
 }
 
 __global__ void __launch_bounds__(RT_THREADS) k_route_select(const float *__restrict__ logits,
@@ -317,29 +199,29 @@ mx_status launch_route_logits(const float *x, const float *router, int t, int hi
     return MX_OK;
 }
 
-// ---- fused decode router (t <= RF_MAX_T) ------------------------------------------------
+// ---- decode router, logits half (t <= RF_MAX_T) ------------------------------------------
 // Blocks [0, n_expert): one expert each.  Its 256 threads split the expert's
 // router row (contiguous in the GGUF layout) and the token rows, so every
 // logit costs one memory round trip.  Optional RMSNorm is folded in: the block
 // reduces sum(x^2) alongside the dot product and forms
 //   logit = sum(x * alpha * r) / sqrt(mean(x^2) + eps).
-// The block then turns the logit into the expert's sigmoid probability and
-// its stable-sort key (bias added for selection only) and publishes both.  The
-// last of these blocks to finish (two-level device-scope counter in `ws`,
-// self-resetting) ranks the keys and writes ids and weights.
+// The block turns the logit into the expert's sigmoid probability and its
+// stable-sort key (bias added for selection only) and stores both in `ws`;
+// the top-k runs in the next kernel on the stream (k_decode_select in
+// mx_mv.hip), which sees these stores at the kernel boundary.  Selecting in a
+// last-arriving block instead costs a device-scope publish + atomic round trip
+// per block (measured: 3.5 us more than a kernel boundary on MI355X).
 // Blocks [n_expert, n_expert + n_stage): stage the (normalised) token rows for
 // the expert kernels (mx_stage.h layout, one row of xstage_bytes(hidden) per
-// token in `xstage`) and, if requested, write them as f32 to `x_normed`; they
-// run alongside the expert blocks and take no part in the count.
+// token in `xstage`) and, if requested, write them as f32 to `x_normed`.
 constexpr int RF_MAX_T = 4;
 constexpr int RF_THREADS = 256;
 constexpr int RF_UNROLL = 4;  // float4 loads per thread per pass
-constexpr int RF_SUB = 16;    // arrival sub-counters (ws words 1..RF_SUB; word 0 is the top counter)
 
-// ws: counters (256 B) | keys u64 [t][E] | probs f32 [t][E]
+// ws: keys u64 [t][E] | probs f32 [t][E]
 size_t route_fused_ws_bytes(int t, int hidden, int n_expert) {
     (void)hidden;
-    return 256 + (size_t)t * (size_t)n_expert * (sizeof(uint64_t) + sizeof(float));
+    return (size_t)t * (size_t)n_expert * (sizeof(uint64_t) + sizeof(float));
 }
 
 // Normalised token value block: x / m * alpha (alpha == NULL: x as is).
@@ -370,13 +252,10 @@ __device__ __forceinline__ void block_sums(float (&v)[RF_MAX_T], int t, float (*
 
 __global__ void __launch_bounds__(RF_THREADS) k_route_fused(
     const float *__restrict__ x, const float *__restrict__ rms_alpha, float rms_eps, float *__restrict__ x_normed,
-    const float *__restrict__ router, const float *__restrict__ bias, int t, int hidden, int n_expert, int top_k,
-    float scale, int apply_scale, int norm, uint32_t *__restrict__ ids, float *__restrict__ w,
+    const float *__restrict__ router, const float *__restrict__ bias, int t, int hidden, int n_expert,
     uint8_t *__restrict__ ws, uint8_t *__restrict__ xstage) {
     __shared__ float s_red[RF_MAX_T][RF_THREADS / 64];
-    __shared__ int s_last;
-    unsigned *counter = reinterpret_cast<unsigned *>(ws);
-    uint64_t *keys = reinterpret_cast<uint64_t *>(ws + 256);
+    uint64_t *keys = reinterpret_cast<uint64_t *>(ws);
     float *probs = reinterpret_cast<float *>(keys + (int64_t)t * n_expert);
     const int tid = threadIdx.x;
     if (blockIdx.x >= n_expert) {
@@ -452,34 +331,15 @@ __global__ void __launch_bounds__(RF_THREADS) k_route_fused(
         const float lg = rms_alpha ? dot[tid] / sqrtf(ss[tid] / (float)hidden + rms_eps) : dot[tid];
         const float p = 1.0f / (expf(-lg) + 1.0f);  // sigmoid (moe.rs:101)
         const int64_t o = (int64_t)tid * n_expert + e;
-        __hip_atomic_store(keys + o, sel_key(p + be, e), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        st_agent(probs + o, p);
+        keys[o] = sel_key(p + be, e);
+        probs[o] = p;
     }
-    // publish (completed agent-coherent stores), then count this block in: blocks
-    // arrive on one of RF_SUB sub-counters, the last of each group on the top
-    // counter (bounded contention per address); the block that completes the top
-    // counter has seen every block's arrival.
-    drain_vmem();
-    __syncthreads();
-    if (tid == 0) {
-        const int grp = blockIdx.x % RF_SUB;
-        const unsigned in_grp = (n_expert - grp + RF_SUB - 1) / RF_SUB;
-        const unsigned groups = min(RF_SUB, n_expert);
-        s_last = arrive_last(counter + 1 + grp, in_grp) && arrive_last(counter, groups);
-    }
-    __syncthreads();
-    if (!s_last) return;  // block-uniform
-    for (int tok = 0; tok < t; tok++)
-        select_from_keys(keys + (int64_t)tok * n_expert, probs + (int64_t)tok * n_expert, n_expert, top_k, scale,
-                         apply_scale, norm, ids + (int64_t)tok * top_k, w + (int64_t)tok * top_k);
-    if (tid <= RF_SUB) reset_counter(counter + tid);
 }
 
 int route_fused_max_t() { return RF_MAX_T; }
 
 mx_status launch_route_fused(const float *x, const float *rms_alpha, float rms_eps, float *x_normed,
-                             const float *router, const float *bias, int t, int hidden, int n_expert, int top_k,
-                             float scale, int apply_scale, int norm, uint32_t *ids, float *w, void *ws,
+                             const float *router, const float *bias, int t, int hidden, int n_expert, void *ws,
                              uint8_t *xstage, hipStream_t s) {
     if (t == 0) return MX_OK;
     if (t > RF_MAX_T) return fail(MX_ERR_SHAPE, "fused router handles at most %d tokens", RF_MAX_T);
@@ -487,8 +347,8 @@ mx_status launch_route_fused(const float *x, const float *rms_alpha, float rms_e
     const int nq = t * (hidden / 8);
     const int n_stage = (xstage || x_normed) ? (nq + RF_THREADS - 1) / RF_THREADS : 0;
     hipLaunchKernelGGL(k_route_fused, dim3((unsigned)(n_expert + n_stage)), dim3(RF_THREADS), 0, s, x, rms_alpha,
-                       rms_eps, x_normed, router, bias, t, hidden, n_expert, top_k, scale, apply_scale, norm, ids, w,
-                       reinterpret_cast<uint8_t *>(ws), xstage);
+                       rms_eps, x_normed, router, bias, t, hidden, n_expert, reinterpret_cast<uint8_t *>(ws),
+                       xstage);
     MX_LAUNCH("k_route_fused");
     return MX_OK;
 }
