@@ -34,6 +34,18 @@ MFMA_F16_PEAK_TFLOPS = 2500.0
 METRIC = "batch-1 MoE layer µs + achieved HBM GB/s; prefill-2048 MoE TFLOP/s (1 GPU)"
 
 
+def measured_traffic():
+    """Calibrated HBM bytes per launch of the decode kernels, from the committed
+    rocprofv3 PMC summary (FETCH_SIZE / WRITE_SIZE passes); {} when absent."""
+    path = ROOT / "profiles" / "decode_c1_hbm_traffic.md"
+    try:
+        text = path.read_text()
+        block = text.split("```json", 1)[1].split("```", 1)[0]
+        return json.loads(block)["traffic_bytes"]
+    except (OSError, IndexError, KeyError, ValueError):
+        return {}
+
+
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -131,7 +143,7 @@ def bench_decode(args):
     dms, dbytes = kern[dom]
     roof = {"bound": "hbm", "kernel": dom, "achieved": round(dbytes / (dms * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(dbytes / (dms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "traffic": None, "bytes_per_launch": dbytes, "launch_us": round(dms * 1e3, 2)}
+            "traffic": measured_traffic().get(dom), "bytes_per_launch": dbytes, "launch_us": round(dms * 1e3, 2)}
     stage_us = {"route_logits": st[0] * 1e3, "select_shared_gate_up": st[1] * 1e3, "gate_up": st[2] * 1e3,
                 "down": st[3] * 1e3}
     return dict(ms_per_step=ms, steps=steps, gbs=gbs, bytes_per_step=bytes_per_step, uniq=uniq,
@@ -237,6 +249,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--copy-probe-mb", type=int, default=0,
+                    help="only run N device-to-device copies of this many MB (HBM counter calibration) and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (expert-parallel sharding is "
@@ -244,6 +258,17 @@ def main():
         sys.exit(2)
     import torch
     torch.cuda.set_device(0)
+    if args.copy_probe_mb:
+        # a plain copy of known size: FETCH_SIZE / WRITE_SIZE of its dispatches calibrate
+        # the counters that give the decode kernels' HBM traffic
+        n = args.copy_probe_mb * (1 << 20)
+        src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(4):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy probe: 4 x {n} bytes")
+        return
     dec = bench_decode(args)
     pre = None if args.no_prefill else bench_prefill(args)
     cpu = None if args.no_cpu_baseline else cpu_baseline(args, dec)

@@ -101,6 +101,40 @@ __global__ void __launch_bounds__(1024) k_bucket_scan(int t, int top_k, int n_ex
 __global__ void __launch_bounds__(256) k_bucket_fill(const uint32_t *__restrict__ ids, int t,
                                                      int top_k, int n_expert,
                                                      int32_t *__restrict__ map) {
+    // s_slot[tt * n_expert + e]: the first slot of token tt that picked expert e
+    // (0xFF: none), so each expert's thread walks the chunk's tokens in order
+    // with one LDS byte per token
+    extern __shared__ uint8_t s_slot[];
+    const MapLayout L(n_expert, t, top_k);
+    const int c = blockIdx.x, tid = threadIdx.x;
+    const int tok0 = c * BK_CHUNK;
+    const int ntok = min(BK_CHUNK, t - tok0);
+    uint32_t *w32 = reinterpret_cast<uint32_t *>(s_slot);
+    for (int i = tid; i < BK_CHUNK * n_expert / 4; i += 256) w32[i] = 0xFFFFFFFFu;
+    __syncthreads();
+    for (int i = tid; i < ntok * top_k; i += 256) {
+        const uint32_t *row = ids + (int64_t)(tok0 + i / top_k) * top_k;
+        const int slot = i % top_k;
+        const uint32_t id = row[slot];
+        bool first = id < (uint32_t)n_expert;  // out-of-range ids are dropped (flagged by the count pass)
+        for (int s2 = 0; s2 < slot; s2++) first = first && (row[s2] != id);
+        if (first) s_slot[(i / top_k) * n_expert + id] = (uint8_t)slot;  // one writer per (token, expert)
+    }
+    __syncthreads();
+    for (int e = tid; e < n_expert; e += 256) {
+        int pos = map[L.off + e] + map[L.chunk + (int64_t)c * n_expert + e];
+        for (int tt = 0; tt < ntok; tt++) {
+            const int sl = s_slot[tt * n_expert + e];
+            if (sl != 0xFF) map[L.list + pos++] = (tok0 + tt) * top_k + sl;
+        }
+    }
+}
+
+// The same list for expert counts whose slot table does not fit in LDS: each
+// expert's thread scans the chunk's ids directly.
+__global__ void __launch_bounds__(256) k_bucket_fill_scan(const uint32_t *__restrict__ ids, int t,
+                                                          int top_k, int n_expert,
+                                                          int32_t *__restrict__ map) {
     extern __shared__ uint32_t s_ids[];
     const MapLayout L(n_expert, t, top_k);
     const int c = blockIdx.x, tid = threadIdx.x;
@@ -141,9 +175,16 @@ mx_status launch_map0(const uint32_t *ids, int t, int top_k, int n_expert, int32
     MX_LAUNCH("k_bucket_count");
     hipLaunchKernelGGL(k_bucket_scan, dim3(1), dim3(1024), 0, s, t, top_k, n_expert, bm, map);
     MX_LAUNCH("k_bucket_scan");
-    hipLaunchKernelGGL(k_bucket_fill, dim3((unsigned)L.nchunks), dim3(256),
-                       BK_CHUNK * top_k * 4, s, ids, t, top_k, n_expert, map);
-    MX_LAUNCH("k_bucket_fill");
+    const size_t slot_lds = (size_t)BK_CHUNK * ((n_expert + 3) & ~3);
+    if (slot_lds <= 96 * 1024) {
+        hipLaunchKernelGGL(k_bucket_fill, dim3((unsigned)L.nchunks), dim3(256), slot_lds, s, ids, t, top_k,
+                           n_expert, map);
+        MX_LAUNCH("k_bucket_fill");
+    } else {
+        hipLaunchKernelGGL(k_bucket_fill_scan, dim3((unsigned)L.nchunks), dim3(256), BK_CHUNK * top_k * 4, s, ids,
+                           t, top_k, n_expert, map);
+        MX_LAUNCH("k_bucket_fill_scan");
+    }
     return MX_OK;
 }
 
