@@ -249,6 +249,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-decode", action="store_true", help="prefill only (profiling); prints no JSON line")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="only run N device-to-device copies of this many MB (HBM counter calibration) and exit")
     args = ap.parse_args()
@@ -268,6 +269,9 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         log(f"copy probe: 4 x {n} bytes")
+        return
+    if args.no_decode:
+        bench_prefill(args)
         return
     dec = bench_decode(args)
     pre = None if args.no_prefill else bench_prefill(args)

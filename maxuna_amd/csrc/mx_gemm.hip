@@ -138,40 +138,47 @@ template <> struct WB<kQ4_K> {
 // step p takes the 4-bit part from the low (p even) / high (p odd) ql piece,
 // nibble p / 2, and bits 2p of qh; scale 8n + 2p + kh (mm_id.metal:115-135).
 template <> struct WB<kQ6_K> {
-    Raw16 lo, hi, qh;
-    uint2 sc;
-    uint16_t dh;
+    // raw bytes, realigned in place by prep(): ql low piece, ql high piece, qh
+    uint4 lo, hi, qh;
+    uint32_t lo_t, hi_t, qh_t;  // the dword after each piece (2-byte aligned blocks)
+    uint32_t sc0, sc1, dsh;     // scale dwords covering scales[8n .. 8n+7]; d and the shift
     __device__ __forceinline__ void load(const uint8_t *row, int ks, int kh) {
         const uint8_t *blk = row + (int64_t)(ks >> 1) * 210;
         const int n = ks & 1;
-        lo = ld16_a2(blk + 64 * n + 16 * kh);
-        hi = ld16_a2(blk + 64 * n + 32 + 16 * kh);
-        qh = ld16_a2(blk + 128 + 32 * n + 16 * kh);
-        sc = load8_a2(blk + 192 + 8 * n);
-        dh = ld_u16(blk + 208);
+        const Raw16 a = ld16_a2(blk + 64 * n + 16 * kh);
+        const Raw16 b = ld16_a2(blk + 64 * n + 32 + 16 * kh);
+        const Raw16 c = ld16_a2(blk + 128 + 32 * n + 16 * kh);
+        lo = a.v; lo_t = a.tail;
+        hi = b.v; hi_t = b.tail;
+        qh = c.v; qh_t = c.tail;
+        const uint2 sc = load8_a2(blk + 192 + 8 * n);
+        sc0 = sc.x;
+        sc1 = sc.y;
+        // every field of a block shares its 4-byte phase: the shift is a.sh
+        dsh = (uint32_t)ld_u16(blk + 208) | (a.sh << 16);
     }
     float ds[4];
-    uint4 l4, h4, q4;
     template <int PAR> __device__ __forceinline__ void prep(int kh) {
-        const float d = h2f(dh);
+        const float d = h2f((uint16_t)(dsh & 0xFFFFu));
+        const uint32_t sh = dsh >> 16;
 #pragma unroll
         for (int p = 0; p < 4; p++) {
             const int j = 2 * p + kh;  // byte j of the stage's 8 scales
-            const uint32_t word = j < 4 ? sc.x : sc.y;
+            const uint32_t word = j < 4 ? sc0 : sc1;
             const int8_t s8 = (int8_t)((word >> (8 * (j & 3))) & 0xFFu);
             ds[p] = d * (float)s8;
         }
-        l4 = fix16(lo);
-        h4 = fix16(hi);
-        q4 = fix16(qh);
+        lo = fix16(Raw16{lo, lo_t, sh});
+        hi = fix16(Raw16{hi, hi_t, sh});
+        qh = fix16(Raw16{qh, qh_t, sh});
     }
     __device__ __forceinline__ half8_t step(int p, int hh) const {
-        const uint4 &ql = (p & 1) ? h4 : l4;
+        const uint4 &ql = (p & 1) ? hi : lo;
         const int shl = 4 * (p >> 1), shh = 2 * p;
         const uint32_t a0 = ((hh ? ql.z : ql.x) >> shl) & 0x0F0F0F0Fu;
         const uint32_t a1 = ((hh ? ql.w : ql.y) >> shl) & 0x0F0F0F0Fu;
-        const uint32_t b0 = (((hh ? q4.z : q4.x) >> shh) & 0x03030303u) << 4;
-        const uint32_t b1 = (((hh ? q4.w : q4.y) >> shh) & 0x03030303u) << 4;
+        const uint32_t b0 = (((hh ? qh.z : qh.x) >> shh) & 0x03030303u) << 4;
+        const uint32_t b1 = (((hh ? qh.w : qh.y) >> shh) & 0x03030303u) << 4;
         float f[8];
         ubytes(a0 | b0, f);
         ubytes(a1 | b1, f + 4);
@@ -242,8 +249,17 @@ __device__ __forceinline__ bool tile_of(const GemmArgs &a, int nt_count, Tile &t
     return true;
 }
 
+// waves per SIMD the register allocation must allow, per weight type
+#ifndef MX_GEMM_WPE_Q4K
+#define MX_GEMM_WPE_Q4K 2
+#endif
+#ifndef MX_GEMM_WPE_Q6K
+#define MX_GEMM_WPE_Q6K 1
+#endif
+template <int DT> struct GemmWpe { static constexpr int v = DT == kQ4_K ? MX_GEMM_WPE_Q4K : DT == kQ6_K ? MX_GEMM_WPE_Q6K : 1; };
+
 template <int DT, bool SWIGLU>
-__global__ void __launch_bounds__(64 * NWAVE) k_gemm(GemmArgs a) {
+__global__ void __launch_bounds__(64 * NWAVE) __attribute__((amdgpu_waves_per_eu(GemmWpe<DT>::v))) k_gemm(GemmArgs a) {
     __shared__ __attribute__((aligned(1024))) uint8_t sA[2][STAGE_BYTES];
     __shared__ int64_t s_src[GM_BM];  // byte offset of the A row
     __shared__ float s_scale[GM_BM];
