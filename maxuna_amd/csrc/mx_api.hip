@@ -523,6 +523,15 @@ mx_status moe_forward_impl(const mx_moe_layer *L, const float *x, int64_t t, con
         DecodeDownArgs da{gd.w, gd.expert_bytes, gd.row_bytes, shf ? sd.w : nullptr, sd.row_bytes, shared_out,
                           (int)E, (int)FF, (int)H, o.act, ids, w, residual, (int)t, (int)K, out, o.part,
                           o.counters};
+#ifdef MX_SEPARATE_COMBINE
+        if (shf) {
+            da.counters = nullptr;
+            MX_TRY(launch_decode_down(L->down.dtype, da, s));
+            MX_TRY(launch_combine_prefill(o.part, w, residual, (int)t, (int)K, 1, (int)H, out, s));
+            MX_STAGE();
+            return MX_OK;
+        }
+#endif
         MX_TRY(launch_decode_down(L->down.dtype, da, s));
         MX_STAGE();
         return MX_OK;

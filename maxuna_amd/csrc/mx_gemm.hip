@@ -43,8 +43,20 @@ namespace {
 constexpr int KS = 128;                // K per stage
 constexpr int ROWB = KS * 2;           // LDS bytes per A row and stage
 constexpr int STAGE_BYTES = GM_BM * ROWB;
-constexpr int NWAVE = 4;
-constexpr int DMA_PER_WAVE = STAGE_BYTES / 1024 / NWAVE;
+constexpr int BN = 256;  // weight rows (output columns) per block
+
+// Weight rows per wave = 32 * NB.  NB = 2 (4 waves per block) reuses every A
+// fragment read from LDS for two MFMAs and is what the SwiGLU epilogue needs
+// (32 gate + the same 32 up rows in one wave); NB = 1 (8 waves) halves the
+// accumulators and weight registers per wave, which lets the Q6_K plain GEMM
+// run two waves per SIMD without spilling.
+#ifndef MX_GEMM_NB_PLAIN
+#define MX_GEMM_NB_PLAIN 1
+#endif
+template <int DT, bool SWIGLU> struct GemmNb {
+    static constexpr int nb = (SWIGLU || DT == kQ4_K) ? 2 : MX_GEMM_NB_PLAIN;
+    static constexpr int waves = BN / (32 * nb);
+};
 
 typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
 typedef float float2_t __attribute__((ext_vector_type(2)));
@@ -259,12 +271,15 @@ __device__ __forceinline__ bool tile_of(const GemmArgs &a, int nt_count, Tile &t
 template <int DT> struct GemmWpe { static constexpr int v = DT == kQ4_K ? MX_GEMM_WPE_Q4K : DT == kQ6_K ? MX_GEMM_WPE_Q6K : 1; };
 
 template <int DT, bool SWIGLU>
-__global__ void __launch_bounds__(64 * NWAVE) __attribute__((amdgpu_waves_per_eu(GemmWpe<DT>::v))) k_gemm(GemmArgs a) {
+__global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
+    __attribute__((amdgpu_waves_per_eu(GemmWpe<DT>::v))) k_gemm(GemmArgs a) {
+    constexpr int NB = GemmNb<DT, SWIGLU>::nb;
+    constexpr int NWAVE = GemmNb<DT, SWIGLU>::waves;
+    constexpr int DMA_PER_WAVE = STAGE_BYTES / 1024 / NWAVE;
     __shared__ __attribute__((aligned(1024))) uint8_t sA[2][STAGE_BYTES];
     __shared__ int64_t s_src[GM_BM];  // byte offset of the A row
     __shared__ float s_scale[GM_BM];
     __shared__ int s_out[GM_BM];      // output row
-    constexpr int BN = 256;           // columns per block (SwiGLU: 128 gate + 128 up)
     constexpr int NCOL = SWIGLU ? BN / 2 : BN;
     const int nt_count = (a.n_out + NCOL - 1) / NCOL;
     Tile tl;
@@ -288,13 +303,13 @@ __global__ void __launch_bounds__(64 * NWAVE) __attribute__((amdgpu_waves_per_eu
     // this lane's two weight rows (one per 32-column MFMA block)
     const bool shared = tl.e >= a.n_expert;
     const int64_t rb = shared ? a.sh_row_bytes : a.row_bytes;
-    const uint8_t *wrow[2];
-    int col[2];
+    const uint8_t *wrow[NB];
+    int col[NB];
 #pragma unroll
-    for (int nb = 0; nb < 2; nb++) {
+    for (int nb = 0; nb < NB; nb++) {
         const int m = SWIGLU ? nb : 0;
         const uint8_t *base = shared ? a.w_sh[m] : a.w[m] + (int64_t)tl.e * a.expert_bytes;
-        col[nb] = SWIGLU ? tl.nt * NCOL + wave * 32 + j : tl.nt * NCOL + wave * 64 + nb * 32 + j;
+        col[nb] = SWIGLU ? tl.nt * NCOL + wave * 32 + j : tl.nt * NCOL + wave * 32 * NB + nb * 32 + j;
         wrow[nb] = base + (int64_t)min(col[nb], a.n_out - 1) * rb;
     }
 
@@ -318,54 +333,54 @@ __global__ void __launch_bounds__(64 * NWAVE) __attribute__((amdgpu_waves_per_eu
         aoff[s] = j * ROWB + ((c ^ (j & 15)) << 4);
     }
 
-    float16_t acc[4][2];
+    float16_t acc[4][NB];
 #pragma unroll
     for (int mb = 0; mb < 4; mb++)
 #pragma unroll
-        for (int nb = 0; nb < 2; nb++)
+        for (int nb = 0; nb < NB; nb++)
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[mb][nb][r] = 0.f;
 
-    auto compute = [&](const uint8_t *buf, WB<DT>(&wb)[2]) {
+    auto compute = [&](const uint8_t *buf, WB<DT>(&wb)[NB]) {
 #pragma unroll
         for (int s = 0; s < 8; s++) {
             const int p = s >> 1, hh = s & 1;
-            half8_t bf[2];
+            half8_t bf[NB];
 #pragma unroll
-            for (int nb = 0; nb < 2; nb++) bf[nb] = wb[nb].step(p, hh);
+            for (int nb = 0; nb < NB; nb++) bf[nb] = wb[nb].step(p, hh);
 #pragma unroll
             for (int mb = 0; mb < 4; mb++) {
                 const half8_t af = *reinterpret_cast<const half8_t *>(buf + mb * 32 * ROWB + aoff[s]);
 #pragma unroll
-                for (int nb = 0; nb < 2; nb++)
+                for (int nb = 0; nb < NB; nb++)
                     acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[nb], acc[mb][nb], 0, 0, 0);
             }
         }
     };
 
-    WB<DT> w0[2], w1[2];
+    WB<DT> w0[NB], w1[NB];
     const int nks = a.k / KS;  // even
     issue_a(0, sA[0]);
 #pragma unroll
-    for (int nb = 0; nb < 2; nb++) w0[nb].load(wrow[nb], 0, kh);
+    for (int nb = 0; nb < NB; nb++) w0[nb].load(wrow[nb], 0, kh);
     wait_vmcnt(0);
     __syncthreads();
     for (int ks = 0; ks < nks; ks += 2) {
         issue_a(ks + 1, sA[1]);
 #pragma unroll
-        for (int nb = 0; nb < 2; nb++) w1[nb].load(wrow[nb], ks + 1, kh);
+        for (int nb = 0; nb < NB; nb++) w1[nb].load(wrow[nb], ks + 1, kh);
 #pragma unroll
-        for (int nb = 0; nb < 2; nb++) w0[nb].template prep<0>(kh);
+        for (int nb = 0; nb < NB; nb++) w0[nb].template prep<0>(kh);
         compute(sA[0], w0);
         wait_vmcnt(0);
         __syncthreads();
         if (ks + 2 < nks) {
             issue_a(ks + 2, sA[0]);
 #pragma unroll
-            for (int nb = 0; nb < 2; nb++) w0[nb].load(wrow[nb], ks + 2, kh);
+            for (int nb = 0; nb < NB; nb++) w0[nb].load(wrow[nb], ks + 2, kh);
         }
 #pragma unroll
-        for (int nb = 0; nb < 2; nb++) w1[nb].template prep<1>(kh);
+        for (int nb = 0; nb < NB; nb++) w1[nb].template prep<1>(kh);
         compute(sA[1], w1);
         wait_vmcnt(0);
         __syncthreads();
@@ -387,7 +402,7 @@ __global__ void __launch_bounds__(64 * NWAVE) __attribute__((amdgpu_waves_per_eu
                 }
             } else {
 #pragma unroll
-                for (int nb = 0; nb < 2; nb++)
+                for (int nb = 0; nb < NB; nb++)
                     if (col[nb] < a.n_out) orow[col[nb]] = acc[mb][nb][r] * sc;
             }
         }
@@ -479,8 +494,8 @@ mx_status launch_gemm(int dtype, bool swiglu, const GemmArgs &a, hipStream_t s) 
     const int64_t t_max = ((int64_t)a.t * a.top_k + GM_BM - 1) / GM_BM + a.n_map_expert;  // m-tiles of GM_BM
     const int64_t blocks = (t_max * nt + 7) / 8 * 8;
     if (blocks > INT32_MAX) return fail(MX_ERR_OVERFLOW, "gemm: too many tiles");
-    const dim3 grid((unsigned)blocks), block(64 * NWAVE);
-#define MX_G(DT, SW) hipLaunchKernelGGL((k_gemm<DT, SW>), grid, block, 0, s, a)
+    const dim3 grid((unsigned)blocks);
+#define MX_G(DT, SW) hipLaunchKernelGGL((k_gemm<DT, SW>), grid, dim3((64 * GemmNb<DT, SW>::waves)), 0, s, a)
     switch (dtype) {
     case kQ4_K: if (swiglu) MX_G(kQ4_K, true); else MX_G(kQ4_K, false); break;
     case kQ6_K: if (swiglu) MX_G(kQ6_K, true); else MX_G(kQ6_K, false); break;
