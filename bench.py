@@ -80,6 +80,33 @@ def profiled(block, x, out, t, n_max=16):
     return [stage[i] for i in range(n.value)]
 
 
+def forward_repeat(block, x, out, stage, times):
+    """One layer forward with decode stage `stage` launched `times` times (0: skipped; capturable)."""
+    from maxuna_amd._lib import check, lib
+    from maxuna_amd import ops
+    ws = block.workspace(1, x.device)
+    check(lib().mx_moe_forward_repeat(C.byref(block._c), x.data_ptr(), 1, None, out.data_ptr(), None, None,
+                                      ws.data_ptr(), ws.numel(), ops._stream(), stage, times))
+
+
+def graph_us(fn, replays):
+    """Average time of one replay of the graph captured from fn(), us."""
+    import torch
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    for _ in range(3):
+        g.replay()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(replays):
+        g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) * 1e3 / replays
+
+
 def bench_decode(args):
     import numpy as np
     import torch
@@ -125,12 +152,20 @@ def bench_decode(args):
     ms = start.elapsed_time(end) / steps
     gbs = bytes_per_step / (ms * 1e-3) / 1e9
     log(f"decode: {steps} steps, {ms * 1e3:.2f} us/layer, {gbs:.0f} GB/s (wall {wall * 1e3:.1f} ms)")
-    # per-stage HIP-event timing (eager, rotating layers) for the roofline of the dominant kernel
-    stages = []
-    for r in range(max(1, args.profile_iters)):
-        i = r % L
-        stages.append(profiled(layers[i].block, xs[i], outs[i], 1))
-    st = np.array(stages).mean(0)  # router logits, top-k + shared gate/up, routed gate/up, down (ms)
+    # per-kernel time inside the replayed pipeline: the plain rotation minus the
+    # rotation with one stage's kernel left out (HIP events on the stream).  Leaving
+    # a launch out, unlike launching it twice, keeps every weight byte an HBM read.
+    reps = max(4, replays // 4)
+    base_us = graph_us(lambda: [forward_repeat(layers[i].block, xs[i], outs[i], -1, 1) for i in range(L)], reps)
+    st = []
+    for stage in range(4):
+        skip = graph_us(lambda: [forward_repeat(layers[i].block, xs[i], outs[i], stage, 0) for i in range(L)], reps)
+        st.append((base_us - skip) / L * 1e-3)  # ms per launch
+    # eager per-stage HIP events (include the dispatch gap before each kernel)
+    eager = np.array([profiled(layers[r % L].block, xs[r % L], outs[r % L], 1)
+                      for r in range(max(1, args.profile_iters))]).mean(0)
+    log("decode stage us (graph, differential): " + ", ".join(f"{v * 1e3:.2f}" for v in st)
+        + "; eager events: " + ", ".join(f"{v * 1e3:.2f}" for v in eager))
     eb_gu = 2 * spec.ff * (spec.hidden // 256) * 144
     eb_dn = spec.hidden * (spec.ff // 256) * 210
     k = spec.top_k
@@ -145,7 +180,7 @@ def bench_decode(args):
             "unit": "GB/s", "frac": round(dbytes / (dms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "traffic": measured_traffic().get(dom), "bytes_per_launch": dbytes, "launch_us": round(dms * 1e3, 2)}
     stage_us = {"route_logits": st[0] * 1e3, "select_shared_gate_up": st[1] * 1e3, "gate_up": st[2] * 1e3,
-                "down": st[3] * 1e3}
+                "down": st[3] * 1e3, "eager_events": [round(v * 1e3, 2) for v in eager]}
     return dict(ms_per_step=ms, steps=steps, gbs=gbs, bytes_per_step=bytes_per_step, uniq=uniq,
                 stage_us=stage_us, roofline=roof,
                 layers=layers)
@@ -296,7 +331,7 @@ def main():
         "tokens_per_s": round(1e3 / dec["ms_per_step"], 1),
         "bytes_per_step": int(dec["bytes_per_step"]),
         "hbm_frac": round(dec["gbs"] / HBM_PEAK_GBS, 4),
-        "decode_stage_us": {k: round(v, 2) for k, v in dec["stage_us"].items()},
+        "decode_stage_us": {k: (round(v, 2) if isinstance(v, float) else v) for k, v in dec["stage_us"].items()},
         "roofline": dec["roofline"],
     }
     if pre:

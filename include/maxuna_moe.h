@@ -226,6 +226,21 @@ mx_status mx_moe_forward_profiled(const mx_moe_layer *layer, const float *x, int
                                   mx_stream_t stream, float *stage_ms, int32_t max_stages,
                                   int32_t *n_stages);
 
+/* Same as mx_moe_forward, with the kernels of decode stage `stage` (0 router
+ * logits, 1 top-k + shared gate/up, 2 routed gate/up, 3 down + combine; the
+ * fused decode path, t <= 4) launched `times` times (0..16).  times = 0 skips
+ * the stage: the later stages then read what the workspace holds from the
+ * previous forward of the same layer (valid inputs, stale results) -- a graph
+ * of layers with one stage skipped, subtracted from the full graph, gives that
+ * stage's time inside the replayed pipeline.  Every stage recomputes its
+ * outputs from its inputs, so times > 1 leaves the result unchanged; `residual`
+ * must not alias `out` then.  Capturable.  For profiling and the benchmark; no
+ * reference counterpart. */
+mx_status mx_moe_forward_repeat(const mx_moe_layer *layer, const float *x, int64_t t,
+                                const float *residual, float *out, uint32_t *ids_out, float *w_out,
+                                void *workspace, size_t workspace_bytes, mx_stream_t stream,
+                                int32_t stage, int32_t times);
+
 /* ---- synthetic weights (bench/test utility, no reference counterpart) ----------
  * Fills nbytes of a tensor of raw blocks with the library's seeded generator:
  * byte j = byte (j&7) of splitmix64-mix(key + (j/8+1)*0x9E3779B97F4A7C15); the

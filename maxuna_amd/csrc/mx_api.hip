@@ -446,9 +446,16 @@ struct StageTimer {
         if (tm) MX_TRY(tm->mark(s)); \
     } while (0)
 
+// Launch count of decode stage `stage` (profiling: one stage skipped or
+// repeated, see mx_moe_forward_repeat; 1 otherwise).
+struct Repeat {
+    int stage = -1, times = 1;
+    int operator()(int st) const { return st == stage ? times : 1; }
+};
+
 mx_status moe_forward_impl(const mx_moe_layer *L, const float *x, int64_t t, const float *residual, float *out,
                            uint32_t *ids_out, float *w_out, void *workspace, size_t workspace_bytes,
-                           hipStream_t s, StageTimer *tm) {
+                           hipStream_t s, StageTimer *tm, Repeat rep = Repeat()) {
     StackGeom gg, gu, gd, sg{}, su{}, sd{};
     MX_TRY(check_layer(L, t, gg, gu, gd, sg, su, sd));
     if (t == 0) return MX_OK;
@@ -473,8 +480,9 @@ mx_status moe_forward_impl(const mx_moe_layer *L, const float *x, int64_t t, con
         // logits -> keys/probs; the router also stages the (normalised) rows for the
         // decode expert kernels.  The top-k runs in the selection blocks of the next
         // launch (below).
-        MX_TRY(launch_route_fused(x, L->rms_alpha, L->rms_eps, o.x_normed, L->router, L->exp_probs_b, (int)t,
-                                  (int)H, (int)E, o.route_ws, o.xstage, s));
+        for (int r = 0; r < rep(0); r++)
+            MX_TRY(launch_route_fused(x, L->rms_alpha, L->rms_eps, o.x_normed, L->router, L->exp_probs_b, (int)t,
+                                      (int)H, (int)E, o.route_ws, o.xstage, s));
         if (L->rms_alpha) xin = o.x_normed;
     } else {
         if (L->rms_alpha) {
@@ -512,9 +520,10 @@ mx_status moe_forward_impl(const mx_moe_layer *L, const float *x, int64_t t, con
             DecodeSelArgs sel{reinterpret_cast<const uint64_t *>(keys),
                               reinterpret_cast<const float *>(keys + (size_t)t * E * sizeof(uint64_t)), (int)E,
                               (int)t, scale, apply, L->weights_norm, ids, w};
-            MX_TRY(launch_decode_gate_up(L->gate.dtype, ga, (int)K, shf ? 1 : 0, &sel, s));
+            for (int r = 0; r < rep(1); r++)
+                MX_TRY(launch_decode_gate_up(L->gate.dtype, ga, (int)K, shf ? 1 : 0, &sel, s));
             MX_STAGE();
-            MX_TRY(launch_decode_gate_up(L->gate.dtype, ga, 0, (int)K, nullptr, s));
+            for (int r = 0; r < rep(2); r++) MX_TRY(launch_decode_gate_up(L->gate.dtype, ga, 0, (int)K, nullptr, s));
         } else {
             MX_STAGE();
             MX_TRY(launch_decode_gate_up(L->gate.dtype, ga, 0, (int)K + (shf ? 1 : 0), nullptr, s));
@@ -523,16 +532,7 @@ mx_status moe_forward_impl(const mx_moe_layer *L, const float *x, int64_t t, con
         DecodeDownArgs da{gd.w, gd.expert_bytes, gd.row_bytes, shf ? sd.w : nullptr, sd.row_bytes, shared_out,
                           (int)E, (int)FF, (int)H, o.act, ids, w, residual, (int)t, (int)K, out, o.part,
                           o.counters};
-#ifdef MX_SEPARATE_COMBINE
-        if (shf) {
-            da.counters = nullptr;
-            MX_TRY(launch_decode_down(L->down.dtype, da, s));
-            MX_TRY(launch_combine_prefill(o.part, w, residual, (int)t, (int)K, 1, (int)H, out, s));
-            MX_STAGE();
-            return MX_OK;
-        }
-#endif
-        MX_TRY(launch_decode_down(L->down.dtype, da, s));
+        for (int r = 0; r < (p.fused_router ? rep(3) : 1); r++) MX_TRY(launch_decode_down(L->down.dtype, da, s));
         MX_STAGE();
         return MX_OK;
     }
@@ -633,6 +633,19 @@ mx_status mx_moe_forward_profiled(const mx_moe_layer *L, const float *x, int64_t
         MX_HIP(hipEventElapsedTime(&stage_ms[k], tm.ev[i - 1], tm.ev[i]));
     *n_stages = k;
     return MX_OK;
+}
+
+mx_status mx_moe_forward_repeat(const mx_moe_layer *L, const float *x, int64_t t, const float *residual, float *out,
+                                uint32_t *ids_out, float *w_out, void *workspace, size_t workspace_bytes,
+                                mx_stream_t stream, int32_t stage, int32_t times) {
+    if (times < 0 || times > 16) return fail(MX_ERR_SHAPE, "moe_forward_repeat: times must be in 0..16");
+    if (times > 1 && residual && residual == out)
+        return fail(MX_ERR_SHAPE, "moe_forward_repeat: an in-place residual would be added once per repeat");
+    Repeat rep;
+    rep.stage = stage;
+    rep.times = times;
+    return moe_forward_impl(L, x, t, residual, out, ids_out, w_out, workspace, workspace_bytes, (hipStream_t)stream,
+                            nullptr, rep);
 }
 
 uint64_t mx_tensor_key(uint64_t seed, uint32_t layer, uint32_t tensor_id) {

@@ -686,7 +686,6 @@ __global__ void __launch_bounds__(64 * WAVES_DN) __attribute__((amdgpu_waves_per
         stage_pre(xrow, a.ff, xp);
         stage_post(xrow, a.ff, xp, lds);
     }
-    if (!a.counters) return;  // the caller combines the partial rows in a kernel of its own
     // publish this block's partial rows (completed agent-coherent stores), then count in
     drain_vmem();
     __syncthreads();
