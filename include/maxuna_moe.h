@@ -43,6 +43,9 @@ typedef int32_t mx_status;
 #define MX_ERR_TOPK           8  /* top_k out of range (0 < top_k <= min(E, 32))    */
 #define MX_ERR_ALIGN          9  /* pointer misaligned for its element type         */
 #define MX_ERR_HIP           10  /* the HIP runtime reported an error               */
+#define MX_ERR_IO            11  /* a file could not be opened or read              */
+#define MX_ERR_FORMAT        12  /* a GGUF file is malformed or unsupported         */
+#define MX_ERR_NOT_FOUND     13  /* no tensor / metadata key of that name           */
 
 /* GGML type ids (GgmlDType). */
 #define MX_Q8_0  8
@@ -240,6 +243,49 @@ mx_status mx_moe_forward_repeat(const mx_moe_layer *layer, const float *x, int64
                                 const float *residual, float *out, uint32_t *ids_out, float *w_out,
                                 void *workspace, size_t workspace_bytes, mx_stream_t stream,
                                 int32_t stage, int32_t times);
+
+/* ---- GGUF ingestion --------------------------------------------------------------
+ * A GGUF v2/v3 file: header, typed metadata, tensor table and data section
+ * (public GGUF layout).  Replaces what the reference host gets from candle's
+ * gguf_file::Content plus its loaders (src/gguf.rs:554-658 expert stacks,
+ * gguf.rs:676-687 bias-suffixed f32 tensors, config.rs:115-130 metadata).
+ * The handle keeps the file open; tensor bytes are read on request.  Not
+ * thread-safe per handle. */
+typedef struct mx_gguf mx_gguf;
+typedef struct mx_gguf_tensor {
+    const char *name;     /* owned by the handle (valid until mx_gguf_close)     */
+    int32_t ggml_type;
+    int32_t n_dims;
+    int64_t ne[4];        /* ggml order: ne[0] is the contiguous (row) dimension;
+                             an expert stack [n_expert, n_out, k] has ne = {k, n_out, n_expert} */
+    uint64_t offset;      /* absolute file offset of the first byte             */
+    uint64_t nbytes;      /* 0 if the ggml type's size is unknown here           */
+} mx_gguf_tensor;
+
+mx_status mx_gguf_open(const char *path, mx_gguf **out);
+void mx_gguf_close(mx_gguf *g);
+uint32_t mx_gguf_version(const mx_gguf *g);
+uint64_t mx_gguf_alignment(const mx_gguf *g);
+uint64_t mx_gguf_data_offset(const mx_gguf *g);
+int64_t mx_gguf_tensor_count(const mx_gguf *g);
+mx_status mx_gguf_tensor_at(const mx_gguf *g, int64_t index, mx_gguf_tensor *out);
+mx_status mx_gguf_find_tensor(const mx_gguf *g, const char *name, mx_gguf_tensor *out);
+/* Metadata: the GGUF value type of `key` (-1 if absent); integers of any width
+ * and bool as int64; f32/f64 (or an integer) as double; strings (owned by the
+ * handle); arrays as (element type, count). */
+int32_t mx_gguf_kv_type(const mx_gguf *g, const char *key);
+mx_status mx_gguf_get_int(const mx_gguf *g, const char *key, int64_t *out);
+mx_status mx_gguf_get_float(const mx_gguf *g, const char *key, double *out);
+mx_status mx_gguf_get_string(const mx_gguf *g, const char *key, const char **out);
+mx_status mx_gguf_get_array(const mx_gguf *g, const char *key, int32_t *elem_type, uint64_t *count);
+/* Copies a tensor's bytes into host memory (dst_bytes >= t->nbytes). */
+mx_status mx_gguf_read_host(const mx_gguf *g, const mx_gguf_tensor *t, void *dst, uint64_t dst_bytes);
+/* Copies a tensor's raw bytes into device memory: the file is read in chunks
+ * into two pinned host buffers while the previous chunk's DMA runs on
+ * `stream`.  Returns after the copy has completed.  The zero-copy mmap view of
+ * the reference (gguf.rs:616-658) becomes one upload into HBM. */
+mx_status mx_gguf_read(mx_gguf *g, const mx_gguf_tensor *t, void *dst, uint64_t dst_bytes,
+                       mx_stream_t stream);
 
 /* ---- synthetic weights (bench/test utility, no reference counterpart) ----------
  * Fills nbytes of a tensor of raw blocks with the library's seeded generator:

@@ -17,6 +17,7 @@ MX_OK = 0
 STATUS_NAMES = {
     1: "MX_ERR_NULL", 2: "MX_ERR_SHAPE", 3: "MX_ERR_DTYPE", 4: "MX_ERR_BLOCK", 5: "MX_ERR_XPR",
     6: "MX_ERR_SCRATCH", 7: "MX_ERR_OVERFLOW", 8: "MX_ERR_TOPK", 9: "MX_ERR_ALIGN", 10: "MX_ERR_HIP",
+    11: "MX_ERR_IO", 12: "MX_ERR_FORMAT", 13: "MX_ERR_NOT_FOUND",
 }
 
 
@@ -73,6 +74,17 @@ class MoeLayerC(C.Structure):
     ]
 
 
+class GgufTensorC(C.Structure):
+    _fields_ = [
+        ("name", C.c_char_p),
+        ("ggml_type", C.c_int32),
+        ("n_dims", C.c_int32),
+        ("ne", C.c_int64 * 4),
+        ("offset", C.c_uint64),
+        ("nbytes", C.c_uint64),
+    ]
+
+
 P, I32, I64, U32, U64, F32, F64, SZ = (C.c_void_p, C.c_int32, C.c_int64, C.c_uint32, C.c_uint64,
                                        C.c_float, C.c_double, C.c_size_t)
 SIGNATURES = {
@@ -99,6 +111,21 @@ SIGNATURES = {
     "mx_moe_forward_profiled": (I32, [C.POINTER(MoeLayerC), P, I64, P, P, P, P, P, SZ, P, P, I32, P]),
     "mx_moe_forward_repeat": (I32, [C.POINTER(MoeLayerC), P, I64, P, P, P, P, P, SZ, P, I32, I32]),
     "mx_tensor_key": (U64, [U64, U32, U32]),
+    "mx_gguf_open": (I32, [C.c_char_p, C.POINTER(P)]),
+    "mx_gguf_close": (None, [P]),
+    "mx_gguf_version": (U32, [P]),
+    "mx_gguf_alignment": (U64, [P]),
+    "mx_gguf_data_offset": (U64, [P]),
+    "mx_gguf_tensor_count": (I64, [P]),
+    "mx_gguf_tensor_at": (I32, [P, I64, C.POINTER(GgufTensorC)]),
+    "mx_gguf_find_tensor": (I32, [P, C.c_char_p, C.POINTER(GgufTensorC)]),
+    "mx_gguf_kv_type": (I32, [P, C.c_char_p]),
+    "mx_gguf_get_int": (I32, [P, C.c_char_p, C.POINTER(I64)]),
+    "mx_gguf_get_float": (I32, [P, C.c_char_p, C.POINTER(F64)]),
+    "mx_gguf_get_string": (I32, [P, C.c_char_p, C.POINTER(C.c_char_p)]),
+    "mx_gguf_get_array": (I32, [P, C.c_char_p, C.POINTER(I32), C.POINTER(U64)]),
+    "mx_gguf_read_host": (I32, [P, C.POINTER(GgufTensorC), P, U64]),
+    "mx_gguf_read": (I32, [P, C.POINTER(GgufTensorC), P, U64, P]),
     "mx_synth_blocks": (I32, [I32, U64, P, I64, P]),
 }
 

@@ -130,6 +130,32 @@ def test_route_from_logits_bit_exact(dev, orc):
         assert np.allclose(host(w), ow, rtol=2e-6, atol=0)
 
 
+def test_route_pruned_topk_edge_cases(dev, orc):
+    """The pruned top-k (group maxima -> threshold -> candidate ranks) against a
+    full stable sort: expert counts that are not multiples of the 8-expert
+    group, fewer groups than top_k, top_k = 32, heavy ties, -0.0 / +0.0."""
+    rng = np.random.default_rng(44)
+    for E, K in [(20, 7), (37, 17), (8, 8), (1000, 32), (1024, 1), (256, 10), (64, 32)]:
+        _log(f"pruned top-k E={E} K={K}")
+        t = 24
+        logits = rng.standard_normal((t, E)).astype(np.float32)
+        logits[:6] = np.round(logits[:6] * 2) / 2  # many exact ties
+        logits[6:9] = 0.25  # every score tied
+        logits[9, : E // 2] = -0.0
+        logits[9, E // 2:] = 0.0
+        bias = np.zeros(E, np.float32)
+        if E > 16:
+            bias[: E // 3] = (rng.standard_normal(E // 3) * 0.1).astype(np.float32)
+        ids, w = ops.route_from_logits(dev_f32(logits), dev_f32(bias), K, 1.0, True)
+        oid, ow = orc.route_from_logits(logits, bias, K, 1.0, True)
+        assert np.array_equal(host(ids), oid), (E, K)
+        assert np.allclose(host(w), ow, rtol=2e-6, atol=0)
+        # all scores tied: the order is the bias order, ties -> lower id
+        p = np.float32(1.0) / (np.float32(1.0) + np.exp(np.float32(-0.25)))
+        want6 = np.argsort(-(p + bias), kind="stable")[:K]
+        assert host(ids)[6].tolist() == want6.tolist()
+
+
 def test_route_kats_on_device(dev, orc):
     """The reference's routing known-answer tests (moe.rs:405-484) on the GPU."""
     row = np.array([[2.0, -2.0, 0.0, 1.0, -1.0, 3.0, 0.5, -0.5]], np.float32)
