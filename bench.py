@@ -228,6 +228,87 @@ def bench_prefill(args):
                 tokens_per_s=t / (ms * 1e-3))
 
 
+def bench_verify(args, dec):
+    """C2: the speculative-verify block (t = 16) on the decode layers' rotation.
+    Bytes count each expert touched by any of the 16 tokens once."""
+    import torch
+    from maxuna_amd.synth import CONFIGS, make_x
+
+    spec = CONFIGS["C2"]["spec"]
+    t = CONFIGS["C2"]["t"]
+    layers = dec["layers"]
+    L = len(layers)
+    xs = [torch.from_numpy(make_x(spec, 99, t, layer=i)).cuda() for i in range(L)]
+    outs = [torch.empty_like(x) for x in xs]
+    tot, uniq = 0, []
+    for i in range(L):
+        _, ids, _ = layers[i].block.forward(xs[i], return_routing=True)
+        b, u = layer_bytes(spec, ids.view(torch.int32).cpu().numpy(), t)
+        tot += b
+        uniq.append(u)
+    us = graph_us(lambda: [layers[i].block.forward(xs[i], out=outs[i]) for i in range(L)],
+                  max(4, args.steps // (4 * L))) / L
+    gbs = tot / L / (us * 1e-6) / 1e9
+    log(f"verify C2 (t={t}): {us:.1f} us/block, {gbs:.0f} GB/s, {sum(uniq) / L:.0f} unique experts")
+    return {"workload": "C2 verify block, t=16, top-10 of 256 + shared", "us_per_block": round(us, 2),
+            "tokens_per_s": round(t / (us * 1e-6), 1), "hbm_gbs": round(gbs, 1),
+            "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_block": int(tot / L),
+            "unique_experts": round(sum(uniq) / L, 1)}
+
+
+def bench_chain(args):
+    """C4: one decode step through 48 MoE layers, x <- x + MoE(RMSNorm(x)),
+    every layer with its own weights (about 150 GB resident in HBM)."""
+    import torch
+    from maxuna_amd.synth import CONFIGS, build_layer, make_x
+
+    spec = CONFIGS["C4"]["spec"]
+    n = CONFIGS["C4"]["layers"]
+    log(f"chain: building {n} C1 layers ({n * spec.n_expert * spec.expert_bytes() / 1e9:.0f} GB of experts)")
+    layers = [build_layer(spec, seed=4848, layer=i, rms=True) for i in range(n)]
+    x0 = torch.from_numpy(make_x(spec, 48, 1)).cuda()
+    x = x0.clone()
+    tot = 0
+    for lay in layers:  # routing of one pass, for the byte count (RMSNorm weights included)
+        xin = x.clone()
+        _, ids, _ = lay.block.forward(xin, residual=x, out=x, return_routing=True)
+        tot += layer_bytes(spec, ids.view(torch.int32).cpu().numpy(), 1)[0] + spec.hidden * 4
+    x.copy_(x0)
+
+    def step():
+        for lay in layers:
+            lay.block.forward(x, residual=x, out=x)
+
+    us = graph_us(step, max(3, args.steps // 100))
+    gbs = tot / (us * 1e-6) / 1e9
+    log(f"chain C4: {us / 1e3:.3f} ms/step over {n} layers, {gbs:.0f} GB/s")
+    del layers
+    torch.cuda.empty_cache()
+    return {"workload": "C4 48-layer MoE-only decode step (RMSNorm eps 1e-6, weight 1; residual)",
+            "ms_per_step": round(us / 1e3, 4), "tokens_per_s": round(1e6 / us, 1), "hbm_gbs": round(gbs, 1),
+            "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_step": int(tot)}
+
+
+def bench_lm_head(args):
+    """Plain quantised mat-vec at the lm_head shape: Q6_K [100352 x 3072], t = 1,
+    over 4 distinct weight copies (1 GB, so the Infinity Cache cannot serve repeats)."""
+    import torch
+    from maxuna_amd import ops
+    from maxuna_amd.gguf import GgmlDType
+    from maxuna_amd.synth import synth_stack
+
+    n_out, k, copies = 100352, 3072, 4
+    ws = [synth_stack(GgmlDType.Q6_K, 1, n_out, k, key=9000 + i) for i in range(copies)]
+    x = torch.randn(1, k, device="cuda")
+    us = graph_us(lambda: [ops.mul_mv(w.buffer, GgmlDType.Q6_K, n_out, k, x) for w in ws],
+                  max(4, args.steps // 16)) / copies
+    nbytes = ws[0].nbytes + k * 4 + n_out * 4
+    gbs = nbytes / (us * 1e-6) / 1e9
+    log(f"lm_head Q6_K [{n_out} x {k}]: {us:.1f} us, {gbs:.0f} GB/s")
+    return {"workload": "plain mat-vec Q6_K [100352 x 3072], t=1 (mul_mv, lm_head shape)", "us": round(us, 2),
+            "hbm_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": int(nbytes)}
+
+
 def cpu_baseline(args, dec):
     """The CPU oracle (C restatement of the reference expert path, OpenMP) on a
     bounded sample of the decode workload: C1 layers, t = 1."""
@@ -285,6 +366,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-decode", action="store_true", help="prefill only (profiling); prints no JSON line")
+    ap.add_argument("--no-extra", action="store_true", help="skip the C2 verify, C4 chain and lm_head figures")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="only run N device-to-device copies of this many MB (HBM counter calibration) and exit")
     args = ap.parse_args()
@@ -309,8 +391,15 @@ def main():
         bench_prefill(args)
         return
     dec = bench_decode(args)
+    ver = None if args.no_extra else bench_verify(args, dec)
     pre = None if args.no_prefill else bench_prefill(args)
     cpu = None if args.no_cpu_baseline else cpu_baseline(args, dec)
+    extra = {}
+    if not args.no_extra:
+        extra["lm_head"] = bench_lm_head(args)
+        del dec["layers"]
+        torch.cuda.empty_cache()
+        extra["chain"] = bench_chain(args)
     line = {
         "metric": METRIC,
         "value": round(dec["gbs"], 1),
@@ -340,6 +429,9 @@ def main():
                            "hbm_gbs": round(pre["gbs"], 1), "tokens_per_s": round(pre["tokens_per_s"], 1),
                            "flops": pre["flops"], "bytes": pre["bytes"], "experts_touched": pre["uniq"],
                            "stage_us": pre["stage_us"], "roofline": pre["gate_gemm"]}
+    if ver:
+        line["verify"] = ver
+    line.update(extra)
     if cpu:
         line["cpu_baseline"] = cpu
     print(json.dumps(line), flush=True)
