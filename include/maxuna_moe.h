@@ -13,6 +13,7 @@
  *
  * Quantised weights are raw GGUF/ggml blocks, read in place (no repacking):
  *   Q4_K (type 12): 144-byte super-blocks of 256 weights
+ *   Q5_K (type 13): 176-byte super-blocks of 256 weights
  *   Q6_K (type 14): 210-byte super-blocks of 256 weights
  *   Q8_0 (type  8):  34-byte blocks of 32 weights
  * An expert stack is [n_expert, n_out, k] expert-major: row stride
@@ -50,6 +51,7 @@ typedef int32_t mx_status;
 /* GGML type ids (GgmlDType). */
 #define MX_Q8_0  8
 #define MX_Q4_K 12
+#define MX_Q5_K 13
 #define MX_Q6_K 14
 
 /* Thread-local text for the last non-zero status returned on this thread. */

@@ -24,10 +24,10 @@ mx_status hip_check(hipError_t e, const char *what) {
     return fail(MX_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
 }
 
-static bool supported(int dt) { return dt == kQ4_K || dt == kQ6_K || dt == kQ8_0; }
+static bool supported(int dt) { return dt == kQ4_K || dt == kQ5_K || dt == kQ6_K || dt == kQ8_0; }
 static bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 static const char *dt_name(int dt) {
-    return dt == kQ4_K ? "Q4_K" : dt == kQ6_K ? "Q6_K" : dt == kQ8_0 ? "Q8_0" : "unsupported";
+    return dt == kQ4_K ? "Q4_K" : dt == kQ5_K ? "Q5_K" : dt == kQ6_K ? "Q6_K" : dt == kQ8_0 ? "Q8_0" : "unsupported";
 }
 
 // Validates a stack and returns its geometry.
@@ -53,11 +53,11 @@ static mx_status check_stack(const mx_expert_stack *st, const char *what, StackG
     g.w = static_cast<const uint8_t *>(st->data) + st->base_off;
     g.row_bytes = st->k / bs * type_size(st->dtype);
     g.expert_bytes = st->n_out * g.row_bytes;
-    // Q4_K rows are read with 16-byte loads.  Q6_K/Q8_0 blocks are 2-byte aligned
+    // Q4_K / Q5_K rows are read with 16-byte loads (144 and 176 are multiples of 16).  Q6_K/Q8_0 blocks are 2-byte aligned
     // inside a row; they are read with 16-bit loads or with 4-byte-aligned dwords
     // that each contain at least one byte of the block (never a byte of an
     // unmapped page), so 2-byte alignment suffices.
-    const size_t need = st->dtype == kQ4_K ? 16 : 2;
+    const size_t need = (st->dtype == kQ4_K || st->dtype == kQ5_K) ? 16 : 2;
     if (!aligned(g.w, need))
         return fail(MX_ERR_ALIGN, "%s: first block (data + base_off) must be %zu-byte aligned", what, need);
     return MX_OK;
@@ -113,7 +113,7 @@ mx_status mx_dequantize(int32_t dtype, const void *blocks, int64_t n, float *out
     if (n == 0) return MX_OK;
     if (!blocks) return fail(MX_ERR_NULL, "dequantize: blocks is NULL");
     MX_TRY(check_f32(out, "dequantize: out"));
-    if (!aligned(blocks, dtype == kQ4_K ? 16 : 2))
+    if (!aligned(blocks, (dtype == kQ4_K || dtype == kQ5_K) ? 16 : 2))
         return fail(MX_ERR_ALIGN, "dequantize: blocks misaligned");
     return launch_dequantize(dtype, static_cast<const uint8_t *>(blocks), n, out, (hipStream_t)stream);
 }
@@ -286,6 +286,7 @@ struct Ws {
 struct Plan {
     bool mm, fused_router, has_shared;
     bool shared_in_decode;  // shared expert rides in the fused decode kernels (same quant types)
+    bool expert_order;      // decode kernels walk (token, slot) pairs in expert order (t > 4)
     int64_t min_seq;
 };
 
@@ -303,6 +304,7 @@ Plan plan_for(const mx_moe_layer *L, int64_t t) {
     p.has_shared = L->shared_gate.data != nullptr;
     p.shared_in_decode = p.has_shared && L->shared_gate.dtype == L->gate.dtype &&
                          L->shared_down.dtype == L->down.dtype;
+    p.expert_order = !p.mm && !p.fused_router && t * (L->top_k + (p.shared_in_decode ? 1 : 0)) <= SORT_PAIRS_MAX;
     return p;
 }
 
@@ -314,7 +316,7 @@ struct Layout {
     uint8_t *xstage = nullptr;
     float *part = nullptr;
     unsigned *counters = nullptr;
-    int32_t *map = nullptr, *map_sh = nullptr;
+    int32_t *map = nullptr, *map_sh = nullptr, *order = nullptr;
     uint32_t *ids_aug = nullptr;
     _Float16 *x16 = nullptr, *act16 = nullptr;
     float *x16s = nullptr, *act16s = nullptr, *down = nullptr;
@@ -340,6 +342,7 @@ Layout carve(const mx_moe_layer *L, int64_t t, const Plan &p, void *base) {
         o.act = ws.take<float>(t * slots * FF);
         o.part = ws.take<float>(t * slots * H);
         o.counters = ws.take<unsigned>(decode_down_counter_words((int)t, (int)H));
+        if (p.expert_order) o.order = ws.take<int32_t>(t * slots);
         if (p.has_shared && !p.shared_in_decode) {
             o.sh_g = ws.take<float>(t * FF);
             o.sh_u = ws.take<float>(t * FF);
@@ -493,6 +496,8 @@ mx_status moe_forward_impl(const mx_moe_layer *L, const float *x, int64_t t, con
         MX_TRY(launch_route_select(o.logits, L->exp_probs_b, (int)t, (int)E, (int)K, scale, apply,
                                    L->weights_norm, ids, w, s));
         if (!p.mm) MX_TRY(launch_stage_rows(xin, (int)t, (int)H, o.xstage, s));
+        if (p.expert_order)
+            MX_TRY(launch_sort_pairs(ids, (int)t, (int)K, p.shared_in_decode ? 1 : 0, (int)E, o.order, s));
     }
     MX_STAGE();
 
@@ -512,7 +517,7 @@ mx_status moe_forward_impl(const mx_moe_layer *L, const float *x, int64_t t, con
             shared_out = o.sh_out;
         }
         DecodeGateUpArgs ga{gg.w, gu.w, gg.expert_bytes, gg.row_bytes, shf ? sg.w : nullptr, shf ? su.w : nullptr,
-                            sg.row_bytes, (int)E, (int)FF, (int)H, o.xstage, ids, (int)t, (int)K, o.act};
+                            sg.row_bytes, (int)E, (int)FF, (int)H, o.xstage, ids, (int)t, (int)K, o.act, o.order};
         if (p.fused_router) {
             // the top-k of every token, next to the shared expert's gate/up rows (which
             // need no routing) -- then the routed slots, which read the selection
@@ -531,7 +536,7 @@ mx_status moe_forward_impl(const mx_moe_layer *L, const float *x, int64_t t, con
         MX_STAGE();
         DecodeDownArgs da{gd.w, gd.expert_bytes, gd.row_bytes, shf ? sd.w : nullptr, sd.row_bytes, shared_out,
                           (int)E, (int)FF, (int)H, o.act, ids, w, residual, (int)t, (int)K, out, o.part,
-                          o.counters};
+                          o.counters, o.order};
         for (int r = 0; r < (p.fused_router ? rep(3) : 1); r++) MX_TRY(launch_decode_down(L->down.dtype, da, s));
         MX_STAGE();
         return MX_OK;

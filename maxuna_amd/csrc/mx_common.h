@@ -2,6 +2,7 @@
 //
 // Block layouts are the public GGUF/ggml formats (reference: mv.metal:55-80):
 //   Q4_K 144 B: f16 d | f16 dmin | u8 scales[12] | u8 qs[128]
+//   Q5_K 176 B: f16 d | f16 dmin | u8 scales[12] | u8 qh[32] | u8 qs[128]
 //   Q6_K 210 B: u8 ql[128] | u8 qh[64] | i8 scales[16] | f16 d
 //   Q8_0  34 B: f16 d | i8 qs[32]
 // Q6_K and Q8_0 blocks are only 2-byte aligned inside a row, so every load of
@@ -19,6 +20,7 @@ namespace mx {
 
 constexpr int kQ8_0 = MX_Q8_0;
 constexpr int kQ4_K = MX_Q4_K;
+constexpr int kQ5_K = MX_Q5_K;
 constexpr int kQ6_K = MX_Q6_K;
 constexpr int QK_K = 256;
 
@@ -29,10 +31,10 @@ typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef float float16_t __attribute__((ext_vector_type(16)));
 
 __host__ __device__ constexpr int block_size(int dt) {
-    return dt == kQ8_0 ? 32 : (dt == kQ4_K || dt == kQ6_K) ? 256 : -1;
+    return dt == kQ8_0 ? 32 : (dt == kQ4_K || dt == kQ5_K || dt == kQ6_K) ? 256 : -1;
 }
 __host__ __device__ constexpr int type_size(int dt) {
-    return dt == kQ8_0 ? 34 : dt == kQ4_K ? 144 : dt == kQ6_K ? 210 : -1;
+    return dt == kQ8_0 ? 34 : dt == kQ4_K ? 144 : dt == kQ5_K ? 176 : dt == kQ6_K ? 210 : -1;
 }
 
 __device__ __forceinline__ float h2f(uint16_t h) {

@@ -4,6 +4,7 @@
 // Dequantisation restates the GGUF formulas the reference dequantises with
 // (candle QTensor::dequantize, moe.rs:173-175; block math mm_id.metal:75-167):
 //   Q4_K  y = fl(fl(d*sc) * q) - fl(dmin*m)      (one rounding per op)
+//   Q5_K  the same, q = low nibble + 16 * high bit (bit 2i + h of qh[l])
 //   Q6_K  y = fl(fl(d*sc) * (q - 32))
 //   Q8_0  y = fl(q * d)
 // This file is compiled with -ffp-contract=off, so no product/difference pair
@@ -24,7 +25,7 @@ __global__ void __launch_bounds__(256) k_dequantize(const uint8_t *__restrict__ 
     const int part = (int)(c % CPB);
     const uint8_t *blk = blocks + b * type_size(DT);
     float y[32];
-    if constexpr (DT == kQ4_K) {
+    if constexpr (DT == kQ4_K || DT == kQ5_K) {
         const int i = part >> 1, hi = part & 1;
         const float d = h2f(ld_u16(blk)), dmin = h2f(ld_u16(blk + 2));
         const uint32_t s0 = ld_u32(blk + 4), s1 = ld_u32(blk + 8), s2 = ld_u32(blk + 12);
@@ -32,14 +33,16 @@ __global__ void __launch_bounds__(256) k_dequantize(const uint8_t *__restrict__ 
         q4k_scale_min(2 * i + hi, s0, s1, s2, sc, m);
         const float d1 = d * (float)sc;
         const float m1 = dmin * (float)m;
-        const uint8_t *q = blk + 16 + 32 * i;
+        constexpr int QS = DT == kQ5_K ? 48 : 16;  // Q5_K: qh[32] sits before qs
+        const uint8_t *q = blk + QS + 32 * i;
 #pragma unroll
         for (int w = 0; w < 8; w++) {
             const uint32_t v = ld_u32(q + 4 * w);
+            const uint32_t hb = DT == kQ5_K ? ld_u32(blk + 16 + 4 * w) >> (2 * i + hi) : 0u;
 #pragma unroll
             for (int bb = 0; bb < 4; bb++) {
                 const uint32_t byte = (v >> (8 * bb)) & 0xFFu;
-                const uint32_t qq = hi ? (byte >> 4) : (byte & 0xFu);
+                const uint32_t qq = (hi ? (byte >> 4) : (byte & 0xFu)) | (((hb >> (8 * bb)) & 1u) << 4);
                 const float p = d1 * (float)qq;
                 y[4 * w + bb] = p - m1;
             }
@@ -85,6 +88,7 @@ mx_status launch_dequantize(int dtype, const uint8_t *blocks, int64_t n, float *
     const dim3 grid((unsigned)((chunks + 255) / 256));
     switch (dtype) {
     case kQ4_K: hipLaunchKernelGGL(k_dequantize<kQ4_K>, grid, dim3(256), 0, s, blocks, chunks, out); break;
+    case kQ5_K: hipLaunchKernelGGL(k_dequantize<kQ5_K>, grid, dim3(256), 0, s, blocks, chunks, out); break;
     case kQ6_K: hipLaunchKernelGGL(k_dequantize<kQ6_K>, grid, dim3(256), 0, s, blocks, chunks, out); break;
     default: hipLaunchKernelGGL(k_dequantize<kQ8_0>, grid, dim3(256), 0, s, blocks, chunks, out); break;
     }
@@ -139,7 +143,7 @@ __global__ void __launch_bounds__(256) k_synth_fix(uint64_t key, uint8_t *__rest
     if (b >= n_blocks) return;
     const uint64_t h = mix64((key ^ 0xA0761D6478BD642Full) + ((uint64_t)b + 1) * GAMMA);
     uint8_t *blk = dst + b * type_size(DT);
-    if constexpr (DT == kQ4_K) {
+    if constexpr (DT == kQ4_K || DT == kQ5_K) {
         *reinterpret_cast<uint16_t *>(blk) = synth_scale(h, 0);
         *reinterpret_cast<uint16_t *>(blk + 2) = synth_scale(h, 1);
     } else if constexpr (DT == kQ6_K) {
@@ -160,6 +164,7 @@ mx_status launch_synth(int dtype, uint64_t key, uint8_t *dst, int64_t nbytes, hi
     const dim3 grid((unsigned)((nb + 255) / 256));
     switch (dtype) {
     case kQ4_K: hipLaunchKernelGGL(k_synth_fix<kQ4_K>, grid, dim3(256), 0, s, key, dst, nb); break;
+    case kQ5_K: hipLaunchKernelGGL(k_synth_fix<kQ5_K>, grid, dim3(256), 0, s, key, dst, nb); break;
     case kQ6_K: hipLaunchKernelGGL(k_synth_fix<kQ6_K>, grid, dim3(256), 0, s, key, dst, nb); break;
     default: hipLaunchKernelGGL(k_synth_fix<kQ8_0>, grid, dim3(256), 0, s, key, dst, nb); break;
     }

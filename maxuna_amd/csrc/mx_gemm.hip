@@ -145,6 +145,47 @@ template <> struct WB<kQ4_K> {
     }
 };
 
+// Q5_K: Q4_K's stage layout (qs at byte 48) plus lane half kh's 16 bytes of qh;
+// step p of half `par` adds bit 4 par + p of qh[l] as the fifth bit (mm_id.metal:113-134).
+template <> struct WB<kQ5_K> {
+    uint4 h, q[2], qh;
+    __device__ __forceinline__ void load(const uint8_t *row, int ks, int kh) {
+        const uint8_t *blk = row + (ks >> 1) * 176;
+        h = ld16(blk);
+        qh = ld16(blk + 16 + 16 * kh);
+        const uint8_t *qs = blk + 48 + 64 * (ks & 1) + 16 * kh;
+        q[0] = ld16(qs);
+        q[1] = ld16(qs + 32);
+    }
+    float d[4], m[4];
+    int hsh;
+    template <int PAR> __device__ __forceinline__ void prep(int kh) {
+        (void)kh;
+        const float dd = h2f((uint16_t)(h.x & 0xFFFFu)), dmin = h2f((uint16_t)(h.x >> 16));
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            uint32_t sc, mn;
+            q4k_scale_min(4 * PAR + p, h.y, h.z, h.w, sc, mn);
+            d[p] = dd * (float)sc;
+            m[p] = dmin * (float)mn;
+        }
+        hsh = 4 * PAR;
+    }
+    __device__ __forceinline__ half8_t step(int p, int hh) const {
+        const uint4 &v = q[p >> 1];
+        const int sh = 4 * (p & 1);
+        const uint32_t hb = hsh + p;
+        const uint32_t w0 = (((hh ? v.z : v.x) >> sh) & 0x0F0F0F0Fu) | ((((hh ? qh.z : qh.x) >> hb) & 0x01010101u) << 4);
+        const uint32_t w1 = (((hh ? v.w : v.y) >> sh) & 0x0F0F0F0Fu) | ((((hh ? qh.w : qh.y) >> hb) & 0x01010101u) << 4);
+        float f[8];
+        ubytes(w0, f);
+        ubytes(w1, f + 4);
+#pragma unroll
+        for (int i = 0; i < 8; i++) f[i] = __builtin_fmaf(d[p], f[i], -m[p]);
+        return pack8(f);
+    }
+};
+
 // Q6_K: stage = half n = par of super-block ks / 2 (128 values).  Lane half kh
 // holds ql[64n + 16kh, +16), ql[64n + 32 + 16kh, +16), qh[32n + 16kh, +16);
 // step p takes the 4-bit part from the low (p even) / high (p odd) ql piece,
@@ -268,7 +309,9 @@ __device__ __forceinline__ bool tile_of(const GemmArgs &a, int nt_count, Tile &t
 #ifndef MX_GEMM_WPE_Q6K
 #define MX_GEMM_WPE_Q6K 1
 #endif
-template <int DT> struct GemmWpe { static constexpr int v = DT == kQ4_K ? MX_GEMM_WPE_Q4K : DT == kQ6_K ? MX_GEMM_WPE_Q6K : 1; };
+template <int DT> struct GemmWpe {
+    static constexpr int v = (DT == kQ4_K || DT == kQ5_K) ? MX_GEMM_WPE_Q4K : DT == kQ6_K ? MX_GEMM_WPE_Q6K : 1;
+};
 
 template <int DT, bool SWIGLU>
 __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
@@ -483,7 +526,7 @@ __global__ void __launch_bounds__(256) k_combine_prefill(const float *__restrict
 }  // namespace
 
 bool gemm_supported(int dtype, int k) {
-    return (dtype == kQ4_K || dtype == kQ6_K || dtype == kQ8_0) && k > 0 && k % 256 == 0;
+    return (dtype == kQ4_K || dtype == kQ5_K || dtype == kQ6_K || dtype == kQ8_0) && k > 0 && k % 256 == 0;
 }
 
 mx_status launch_gemm(int dtype, bool swiglu, const GemmArgs &a, hipStream_t s) {
@@ -498,6 +541,7 @@ mx_status launch_gemm(int dtype, bool swiglu, const GemmArgs &a, hipStream_t s) 
 #define MX_G(DT, SW) hipLaunchKernelGGL((k_gemm<DT, SW>), grid, dim3((64 * GemmNb<DT, SW>::waves)), 0, s, a)
     switch (dtype) {
     case kQ4_K: if (swiglu) MX_G(kQ4_K, true); else MX_G(kQ4_K, false); break;
+    case kQ5_K: if (swiglu) MX_G(kQ5_K, true); else MX_G(kQ5_K, false); break;
     case kQ6_K: if (swiglu) MX_G(kQ6_K, true); else MX_G(kQ6_K, false); break;
     default: if (swiglu) MX_G(kQ8_0, true); else MX_G(kQ8_0, false); break;
     }

@@ -193,8 +193,9 @@ mx_status launch_map0(const uint32_t *ids, int t, int top_k, int n_expert, int32
 template <int DT>
 __device__ __forceinline__ void deq_quarter(const uint8_t *__restrict__ row, int kstep, int q,
                                             int k, _Float16 *__restrict__ out) {
-    if constexpr (DT == kQ4_K) {
-        const uint8_t *blk = row + (int64_t)kstep * 144;
+    if constexpr (DT == kQ4_K || DT == kQ5_K) {
+        constexpr int TS = DT == kQ5_K ? 176 : 144, QS = DT == kQ5_K ? 48 : 16;
+        const uint8_t *blk = row + (int64_t)kstep * TS;
         const uint4 h = *reinterpret_cast<const uint4 *>(blk);
         uint32_t sc0, m0, sc1, m1;
         q4k_scale_min(2 * q, h.y, h.z, h.w, sc0, m0);
@@ -202,17 +203,20 @@ __device__ __forceinline__ void deq_quarter(const uint8_t *__restrict__ row, int
         const float d = h2f((uint16_t)(h.x & 0xFFFFu)), dmin = h2f((uint16_t)(h.x >> 16));
         const float d1 = d * (float)sc0, mm1 = dmin * (float)m0;
         const float d2 = d * (float)sc1, mm2 = dmin * (float)m1;
-        const uint4 qa = *reinterpret_cast<const uint4 *>(blk + 16 + 32 * q);
-        const uint4 qb = *reinterpret_cast<const uint4 *>(blk + 32 + 32 * q);
+        const uint4 qa = *reinterpret_cast<const uint4 *>(blk + QS + 32 * q);
+        const uint4 qb = *reinterpret_cast<const uint4 *>(blk + QS + 16 + 32 * q);
         const uint32_t qw[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
 #pragma unroll
         for (int w = 0; w < 8; w++) {
             half4_t lo, hi;
+            // Q5_K: the fifth bits of weights 32*half + 4w .. +3 of this pair (bits 2q, 2q+1)
+            const uint32_t hb = DT == kQ5_K ? *reinterpret_cast<const uint32_t *>(blk + 16 + 4 * w) >> (2 * q) : 0u;
 #pragma unroll
             for (int bb = 0; bb < 4; bb++) {
                 const uint32_t byte = (qw[w] >> (8 * bb)) & 0xFFu;
-                lo[bb] = (_Float16)(d1 * (float)(byte & 0xFu) - mm1);
-                hi[bb] = (_Float16)(d2 * (float)(byte >> 4) - mm2);
+                const uint32_t h5 = (hb >> (8 * bb)) & 3u;
+                lo[bb] = (_Float16)(d1 * (float)((byte & 0xFu) | ((h5 & 1u) << 4)) - mm1);
+                hi[bb] = (_Float16)(d2 * (float)((byte >> 4) | ((h5 >> 1) << 4)) - mm2);
             }
             *reinterpret_cast<half4_t *>(out + 4 * w) = lo;
             *reinterpret_cast<half4_t *>(out + 32 + 4 * w) = hi;
@@ -380,6 +384,7 @@ mx_status launch_mul_mm_id(int dtype, const MmArgs &a, hipStream_t s) {
     const dim3 grid((unsigned)L.t_max, (unsigned)((a.n_out + MM_BN - 1) / MM_BN));
     switch (dtype) {
     case kQ4_K: hipLaunchKernelGGL(k_mul_mm_id<kQ4_K>, grid, dim3(256), 0, s, a); break;
+    case kQ5_K: hipLaunchKernelGGL(k_mul_mm_id<kQ5_K>, grid, dim3(256), 0, s, a); break;
     case kQ6_K: hipLaunchKernelGGL(k_mul_mm_id<kQ6_K>, grid, dim3(256), 0, s, a); break;
     default: hipLaunchKernelGGL(k_mul_mm_id<kQ8_0>, grid, dim3(256), 0, s, a); break;
     }

@@ -14,6 +14,7 @@
 //
 // Work layout (gfx950, wave64).  A row of k weights is cut into "groups":
 //   Q4_K  group = one 64-weight sub-block pair (2i, 2i+1) of a super-block (4 per block)
+//   Q5_K  as Q4_K, with the pair's fifth bits from qh
 //   Q6_K  group = 32 weights: half n, 8-wide l-slice j of all 4 parts        (8 per block)
 //   Q8_0  group = one 34-byte block of 32 weights                            (1 per block)
 // P lanes share a row; lane `sub` owns groups sub, sub+P, ... (NG of them, the
@@ -104,6 +105,52 @@ template <> struct Q<kQ4_K> {
         const int A = (ah << 8) + al, B = (bh << 8) + bl;
         uint32_t sc0, m0, sc1, m1;
         const int i = g & 3;
+        q4k_scale_min(2 * i, r.hd.y, r.hd.z, r.hd.w, sc0, m0);
+        q4k_scale_min(2 * i + 1, r.hd.y, r.hd.z, r.hd.w, sc1, m1);
+        const float d = h2f((uint16_t)(r.hd.x & 0xFFFFu));
+        const float dmin = h2f((uint16_t)(r.hd.x >> 16));
+        const float p = __builtin_fmaf((float)sc0 * x.sa, (float)A, (float)sc1 * x.sb * (float)B);
+        const float m = __builtin_fmaf((float)m0, x.ssa, (float)m1 * x.ssb);
+        return __builtin_fmaf(d, p, -dmin * m);
+    }
+};
+
+// ---- Q5_K -------------------------------------------------------------------------
+// Q4_K's group layout (one 64-weight sub-block pair per group) plus the fifth
+// bit: weight 32h + l of pair i takes bit 2i + h of qh[l] (mm_id.metal:113-134).
+template <> struct Q<kQ5_K> {
+    static constexpr int GPB = 4;
+    using X = Q<kQ4_K>::X;
+    struct Raw { uint4 hd, qa, qb, ha, hb; };
+    __device__ static void load_x(const XView &xv, int g, X &x) { Q<kQ4_K>::load_x(xv, g, x); }
+    __device__ static Raw load(const uint8_t *__restrict__ row, int g) {
+        const uint8_t *blk = row + (g >> 2) * 176;
+        const int i = g & 3;
+        Raw r;
+        r.hd = *reinterpret_cast<const uint4 *>(blk);
+        r.ha = *reinterpret_cast<const uint4 *>(blk + 16);
+        r.hb = *reinterpret_cast<const uint4 *>(blk + 32);
+        r.qa = *reinterpret_cast<const uint4 *>(blk + 48 + 32 * i);
+        r.qb = *reinterpret_cast<const uint4 *>(blk + 64 + 32 * i);
+        return r;
+    }
+    __device__ static float dot(const Raw &r, int g, const X &x) {
+        const uint32_t q[8] = {r.qa.x, r.qa.y, r.qa.z, r.qa.w, r.qb.x, r.qb.y, r.qb.z, r.qb.w};
+        const uint32_t h[8] = {r.ha.x, r.ha.y, r.ha.z, r.ha.w, r.hb.x, r.hb.y, r.hb.z, r.hb.w};
+        const int i = g & 3;
+        int ah = 0, al = 0, bh = 0, bl = 0;
+#pragma unroll
+        for (int w = 0; w < 8; w++) {
+            const uint32_t hs = h[w] >> (2 * i);
+            const uint32_t lo = (q[w] & 0x0F0F0F0Fu) | ((hs & 0x01010101u) << 4);
+            const uint32_t hi = ((q[w] >> 4) & 0x0F0F0F0Fu) | (((hs >> 1) & 0x01010101u) << 4);
+            ah = dot4(lo, x.h[w], ah);
+            al = dot4(lo, x.l[w], al);
+            bh = dot4(hi, x.h[8 + w], bh);
+            bl = dot4(hi, x.l[8 + w], bl);
+        }
+        const int A = (ah << 8) + al, B = (bh << 8) + bl;
+        uint32_t sc0, m0, sc1, m1;
         q4k_scale_min(2 * i, r.hd.y, r.hd.z, r.hd.w, sc0, m0);
         q4k_scale_min(2 * i + 1, r.hd.y, r.hd.z, r.hd.w, sc1, m1);
         const float d = h2f((uint16_t)(r.hd.x & 0xFFFFu));
@@ -519,6 +566,7 @@ mx_status launch_mul_mv_id(int dtype, const MvArgs &a, hipStream_t s) {
     if (a.k % 32) return fail(MX_ERR_BLOCK, "mul_mv_id: k must be a multiple of 32");
     switch (dtype) {
     case kQ4_K: MX_TRY(launch_mv_dt<kQ4_K>(a, grid, s)); break;
+    case kQ5_K: MX_TRY(launch_mv_dt<kQ5_K>(a, grid, s)); break;
     case kQ6_K: MX_TRY(launch_mv_dt<kQ6_K>(a, grid, s)); break;
     default: MX_TRY(launch_mv_dt<kQ8_0>(a, grid, s)); break;
     }
@@ -557,11 +605,22 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
     }
     bid -= sel.n_sel;
     const int tiles = (a.ff + WAVES * RW_GU - 1) / (WAVES * RW_GU);
-    const int tile = bid % tiles, slot = slot0 + (bid / tiles) % nslot, tok = bid / (tiles * nslot);
+    const int slots = a.top_k + (a.sh_gate ? 1 : 0);
+    int tile, slot, tok;
+    if (a.order) {  // every slot of every token, pairs in expert order, pair index fastest
+        const int npair = a.t * slots;
+        const int pair = a.order[bid % npair];
+        tile = bid / npair;
+        tok = pair / slots;
+        slot = pair % slots;
+    } else {
+        tile = bid % tiles;
+        slot = slot0 + (bid / tiles) % nslot;
+        tok = bid / (tiles * nslot);
+    }
     const int wave = threadIdx.x >> 6;
     const int r0 = tile * (WAVES * RW_GU) + wave * RW_GU;
     if (r0 >= a.ff) return;  // wave-uniform; no block barrier below
-    const int slots = a.top_k + (a.sh_gate ? 1 : 0);
     float *act = a.act + ((int64_t)tok * slots + slot) * a.ff;
     const uint8_t *gw, *uw;
     int64_t rb;
@@ -619,6 +678,8 @@ mx_status launch_decode_gate_up(int dtype, const DecodeGateUpArgs &a, int slot0,
     if (a.t == 0) return MX_OK;
     if (sa.n_sel && (sa.n_expert > SEL_MAX_E || a.top_k > SEL_MAX_K || 64 * WAVES != SEL_THREADS))
         return fail(MX_ERR_SHAPE, "decode select: n_expert <= %d and top_k <= %d", SEL_MAX_E, SEL_MAX_K);
+    if (a.order && (sa.n_sel || slot0 != 0 || nslot != a.top_k + (a.sh_gate ? 1 : 0)))
+        return fail(MX_ERR_SHAPE, "decode gate/up: an expert-ordered launch covers every slot");
     const int64_t tiles = (a.ff + WAVES * RW_GU - 1) / (WAVES * RW_GU);
     const int64_t blocks = sa.n_sel + tiles * nslot * a.t;
     if (blocks == 0) return MX_OK;
@@ -628,6 +689,7 @@ mx_status launch_decode_gate_up(int dtype, const DecodeGateUpArgs &a, int slot0,
         return fail(MX_ERR_SHAPE, "decode gate/up: shared expert rows must match the routed rows");
     switch (dtype) {
     case kQ4_K: MX_TRY(launch_gu_dt<kQ4_K>(a, (unsigned)blocks, slot0, nslot, sa, s)); break;
+    case kQ5_K: MX_TRY(launch_gu_dt<kQ5_K>(a, (unsigned)blocks, slot0, nslot, sa, s)); break;
     case kQ6_K: MX_TRY(launch_gu_dt<kQ6_K>(a, (unsigned)blocks, slot0, nslot, sa, s)); break;
     default: MX_TRY(launch_gu_dt<kQ8_0>(a, (unsigned)blocks, slot0, nslot, sa, s)); break;
     }
@@ -650,12 +712,24 @@ template <int DT, int NG>
 __global__ void __launch_bounds__(64 * WAVES_DN) __attribute__((amdgpu_waves_per_eu(MX_DN_WPE))) k_decode_down(DecodeDownArgs a, int ni) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     __shared__ int s_last;
-    const int slot = blockIdx.y, tok = blockIdx.z;
+    const int slots = a.top_k + (a.sh_down ? 1 : 0);
+    int slot, tok, tile, n_tiles;
+    if (a.order) {  // grid (t * slots pairs in expert order, row tiles)
+        const int pair = a.order[blockIdx.x];
+        tok = pair / slots;
+        slot = pair % slots;
+        tile = blockIdx.y;
+        n_tiles = gridDim.y;
+    } else {  // grid (row tiles, slots, t)
+        slot = blockIdx.y;
+        tok = blockIdx.z;
+        tile = blockIdx.x;
+        n_tiles = gridDim.x;
+    }
     constexpr int ROWS_PER_WG = WAVES_DN * RW_DN;
-    const int tile0 = blockIdx.x * ROWS_PER_WG;
+    const int tile0 = tile * ROWS_PER_WG;
     const int wave = threadIdx.x >> 6;
     const int r0 = tile0 + wave * RW_DN;
-    const int slots = a.top_k + (a.sh_down ? 1 : 0);
     const float *xrow = a.act + ((int64_t)tok * slots + slot) * a.ff;
     uint8_t *ring = lds + align16(xstage_bytes(a.ff)) + wave * (RING_DN * ni * 1024);
     XPre xp;
@@ -689,8 +763,8 @@ __global__ void __launch_bounds__(64 * WAVES_DN) __attribute__((amdgpu_waves_per
     // publish this block's partial rows (completed agent-coherent stores), then count in
     drain_vmem();
     __syncthreads();
-    unsigned *counter = a.counters + (int64_t)tok * gridDim.x + blockIdx.x;
-    if (threadIdx.x == 0) s_last = arrive_last(counter, gridDim.y);
+    unsigned *counter = a.counters + (int64_t)tok * n_tiles + tile;
+    if (threadIdx.x == 0) s_last = arrive_last(counter, (unsigned)slots);
     __syncthreads();
     if (!s_last) return;
     const float *wt = a.w + tok * a.top_k;
@@ -733,18 +807,53 @@ size_t decode_down_counter_words(int t, int hidden) {
 }
 
 mx_status launch_decode_down(int dtype, const DecodeDownArgs &a, hipStream_t s) {
-    const dim3 grid((unsigned)((a.hidden + WAVES_DN * RW_DN - 1) / (WAVES_DN * RW_DN)),
-                    (unsigned)(a.top_k + (a.sh_down ? 1 : 0)), (unsigned)a.t);
+    const unsigned tiles = (unsigned)((a.hidden + WAVES_DN * RW_DN - 1) / (WAVES_DN * RW_DN));
+    const unsigned slots = (unsigned)(a.top_k + (a.sh_down ? 1 : 0));
+    const dim3 grid = a.order ? dim3(slots * (unsigned)a.t, tiles) : dim3(tiles, slots, (unsigned)a.t);
     if (grid.x == 0 || a.t == 0) return MX_OK;
     if (a.ff % 32) return fail(MX_ERR_BLOCK, "decode down: expert_ff must be a multiple of 32");
     if (a.sh_down && a.sh_row_bytes != a.d_row_bytes)
         return fail(MX_ERR_SHAPE, "decode down: shared expert rows must match the routed rows");
     switch (dtype) {
     case kQ4_K: MX_TRY(launch_dn_dt<kQ4_K>(a, grid, s)); break;
+    case kQ5_K: MX_TRY(launch_dn_dt<kQ5_K>(a, grid, s)); break;
     case kQ6_K: MX_TRY(launch_dn_dt<kQ6_K>(a, grid, s)); break;
     default: MX_TRY(launch_dn_dt<kQ8_0>(a, grid, s)); break;
     }
     MX_LAUNCH("k_decode_down");
+    return MX_OK;
+}
+
+// ---- (token, slot) pairs in expert order (small-batch verify) --------------------------
+__global__ void __launch_bounds__(SORT_PAIRS_MAX) k_sort_pairs(const uint32_t *__restrict__ ids, int t, int top_k,
+                                                               int has_shared, int n_expert,
+                                                               int32_t *__restrict__ order) {
+    __shared__ uint32_t s_key[SORT_PAIRS_MAX];
+    const int slots = top_k + has_shared;
+    const int n = t * slots;
+    const int p = threadIdx.x;
+    uint32_t key = 0xFFFFFFFFu;
+    if (p < n) {
+        const int tok = p / slots, slot = p % slots;
+        uint32_t e = slot < top_k ? ids[tok * top_k + slot] : (uint32_t)n_expert;
+        if (e > (uint32_t)n_expert) e = (uint32_t)n_expert;  // out-of-range ids sort with the shared expert
+        key = (e << 10) | (uint32_t)p;                      // n_expert <= 32767, p < 1024: distinct keys
+    }
+    s_key[p] = key;
+    __syncthreads();
+    if (p >= n) return;
+    int rank = 0;
+    for (int i = 0; i < n; i++) rank += s_key[i] < key;
+    order[rank] = p;
+}
+
+mx_status launch_sort_pairs(const uint32_t *ids, int t, int top_k, int has_shared, int n_expert, int32_t *order,
+                            hipStream_t s) {
+    if ((int64_t)t * (top_k + has_shared) > SORT_PAIRS_MAX) return fail(MX_ERR_SHAPE, "sort_pairs: too many pairs");
+    if (t == 0) return MX_OK;
+    hipLaunchKernelGGL(k_sort_pairs, dim3(1), dim3(SORT_PAIRS_MAX), 0, s, ids, t, top_k, has_shared, n_expert,
+                       order);
+    MX_LAUNCH("k_sort_pairs");
     return MX_OK;
 }
 

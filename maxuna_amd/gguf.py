@@ -24,6 +24,7 @@ class GgmlDType(IntEnum):
 
     Q8_0 = 8
     Q4_K = 12
+    Q5_K = 13
     Q6_K = 14
 
     @property
@@ -32,7 +33,7 @@ class GgmlDType(IntEnum):
 
     @property
     def type_size(self) -> int:
-        return {GgmlDType.Q8_0: 34, GgmlDType.Q4_K: 144, GgmlDType.Q6_K: 210}[self]
+        return {GgmlDType.Q8_0: 34, GgmlDType.Q4_K: 144, GgmlDType.Q5_K: 176, GgmlDType.Q6_K: 210}[self]
 
 
 def row_bytes(dtype: GgmlDType, k: int) -> int:

@@ -30,6 +30,7 @@ int or_block_size(int dtype) {
     switch (dtype) {
     case OR_Q8_0: return 32;
     case OR_Q4_K: return 256;
+    case OR_Q5_K: return 256;
     case OR_Q6_K: return 256;
     default: return -1;
     }
@@ -39,6 +40,7 @@ int or_type_size(int dtype) {
     switch (dtype) {
     case OR_Q8_0: return 34;  /* f16 d; i8 qs[32] */
     case OR_Q4_K: return 144; /* f16 d, dmin; u8 scales[12]; u8 qs[128] */
+    case OR_Q5_K: return 176; /* f16 d, dmin; u8 scales[12]; u8 qh[32]; u8 qs[128] */
     case OR_Q6_K: return 210; /* u8 ql[128]; u8 qh[64]; i8 scales[16]; f16 d */
     default: return -1;
     }
@@ -99,7 +101,8 @@ static inline uint16_t rd16(const uint8_t *p) { return (uint16_t)(p[0] | (p[1] <
 
 /* ---- dequantisation (mm_id.metal:75-167; candle QTensor::dequantize,
  *      moe.rs:173-175).  Rounding order: d1=fl(d*sc), m1=fl(dmin*m),
- *      y=fl(fl(d1*q)-m1) for Q4_K; y=fl(fl(d*sc)*q) for Q6_K; y=fl(d*q) Q8_0. */
+ *      y=fl(fl(d1*q)-m1) for Q4_K and Q5_K (q = 4 low bits + 16 * high bit);
+ *      y=fl(fl(d*sc)*q) for Q6_K; y=fl(d*q) Q8_0. */
 static void get_scale_min_k4(int j, const uint8_t *s, uint8_t *sc, uint8_t *m) {
     /* mm_id.metal:89-92 */
     if (j < 4) {
@@ -126,6 +129,34 @@ static void deq_q4_K(const uint8_t *b, float *y) {
             float p1 = d1 * (float)(q[32 * i + l] & 0xF);
             y[64 * i + l] = p1 - m1;
             float p2 = d2 * (float)(q[32 * i + l] >> 4);
+            y[64 * i + 32 + l] = p2 - m2;
+        }
+    }
+}
+
+/* Q5_K (mm_id.metal:113-134 per 16-value piece; the public ggml formula per
+ * block): the Q4_K header, then qh[32] and qs[128].  Pair i (weights 64i ..
+ * 64i+63) uses sub-blocks 2i / 2i+1: the low / high nibble of qs[32i + l] plus
+ * 16 times bit 2i / 2i+1 of qh[l].  (The reference's d/16 with the nibble left
+ * in the high half is the same value: every product is exact in f32.) */
+static void deq_q5_K(const uint8_t *b, float *y) {
+    const float d = or_f16_to_f32(rd16(b));
+    const float dmin = or_f16_to_f32(rd16(b + 2));
+    const uint8_t *scales = b + 4;
+    const uint8_t *qh = b + 16;
+    const uint8_t *q = b + 48;
+    for (int i = 0; i < 4; i++) {
+        uint8_t sc, m;
+        get_scale_min_k4(2 * i, scales, &sc, &m);
+        const float d1 = d * (float)sc, m1 = dmin * (float)m;
+        get_scale_min_k4(2 * i + 1, scales, &sc, &m);
+        const float d2 = d * (float)sc, m2 = dmin * (float)m;
+        for (int l = 0; l < 32; l++) {
+            const int v1 = (q[32 * i + l] & 0xF) + (((qh[l] >> (2 * i)) & 1) << 4);
+            const int v2 = (q[32 * i + l] >> 4) + (((qh[l] >> (2 * i + 1)) & 1) << 4);
+            float p1 = d1 * (float)v1;
+            y[64 * i + l] = p1 - m1;
+            float p2 = d2 * (float)v2;
             y[64 * i + 32 + l] = p2 - m2;
         }
     }
@@ -168,6 +199,7 @@ int or_dequantize(int dtype, const uint8_t *blocks, int64_t n, float *out) {
         const uint8_t *b = blocks + i * ts;
         float *y = out + i * bs;
         if (dtype == OR_Q4_K) deq_q4_K(b, y);
+        else if (dtype == OR_Q5_K) deq_q5_K(b, y);
         else if (dtype == OR_Q6_K) deq_q6_K(b, y);
         else deq_q8_0(b, y);
     }
@@ -178,7 +210,7 @@ int or_dequantize(int dtype, const uint8_t *blocks, int64_t n, float *out) {
  * Counter-based splitmix64 stream: byte j of a tensor is byte (j & 7) of
  * mix64(key + (j/8 + 1) * GAMMA).  The f16 super-block scales are then
  * overwritten with d = f16(0.001 + 0.009 u), u uniform on [0,1) in 2^-24 steps
- * (and dmin likewise for Q4_K), f32 ops rounded separately, f16 by RNE.
+ * (and dmin likewise for Q4_K / Q5_K), f32 ops rounded separately, f16 by RNE.
  * The device generator in the library implements the same definition. */
 #define OR_GAMMA 0x9E3779B97F4A7C15ull
 
@@ -218,7 +250,9 @@ int or_synth_blocks(int dtype, uint64_t key, int64_t byte_off, int64_t nbytes, u
         const uint64_t h = or_mix64((key ^ 0xA0761D6478BD642Full) + ((uint64_t)b + 1) * OR_GAMMA);
         uint16_t f[2];
         int off[2], nf = 0;
-        if (dtype == OR_Q4_K) { f[0] = synth_scale(h, 0); off[0] = 0; f[1] = synth_scale(h, 1); off[1] = 2; nf = 2; }
+        if (dtype == OR_Q4_K || dtype == OR_Q5_K) {
+            f[0] = synth_scale(h, 0); off[0] = 0; f[1] = synth_scale(h, 1); off[1] = 2; nf = 2;
+        }
         else if (dtype == OR_Q6_K) { f[0] = synth_scale(h, 0); off[0] = 208; nf = 1; }
         else { f[0] = synth_scale(h, 0); off[0] = 0; nf = 1; }
         for (int i = 0; i < nf; i++) {

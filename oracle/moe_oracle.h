@@ -23,7 +23,7 @@ extern "C" {
 #endif
 
 /* GGML type codes (GgmlDType ids in GGUF). */
-enum { OR_Q8_0 = 8, OR_Q4_K = 12, OR_Q6_K = 14 };
+enum { OR_Q8_0 = 8, OR_Q4_K = 12, OR_Q5_K = 13, OR_Q6_K = 14 };
 
 int    or_block_size(int dtype);   /* weights per block (-1 if unsupported) */
 int    or_type_size(int dtype);    /* bytes per block   (-1 if unsupported) */

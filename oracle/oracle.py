@@ -16,9 +16,9 @@ import numpy as np
 HERE = Path(__file__).resolve().parent
 LIB = HERE / "lib" / "libmoe_oracle.so"
 
-Q8_0, Q4_K, Q6_K = 8, 12, 14
-BLOCK = {Q8_0: 32, Q4_K: 256, Q6_K: 256}
-TSIZE = {Q8_0: 34, Q4_K: 144, Q6_K: 210}
+Q8_0, Q4_K, Q5_K, Q6_K = 8, 12, 13, 14
+BLOCK = {Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256}
+TSIZE = {Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210}
 
 _lib = None
 

@@ -1,4 +1,4 @@
-"""Block ENCODERS for the three GGUF formats, written from the published layout
+"""Block ENCODERS for the GGUF formats, written from the published layout
 (the inverse direction of every decoder under test).  Used to build blocks
 whose dequantised values are known in closed form, so a decoder that reads a
 nibble, a scale bit or a byte from the wrong place fails."""
@@ -35,6 +35,24 @@ def q4_k_values(d, dmin, sc, m, q) -> np.ndarray:
     """Exact real values d*sc_j*q - dmin*m_j (j = weight // 32), float64."""
     j = np.arange(256) // 32
     return d * np.array(sc, np.float64)[j] * q - dmin * np.array(m, np.float64)[j]
+
+
+def pack_q5_k(d: float, dmin: float, sc: list[int], m: list[int], q: np.ndarray) -> np.ndarray:
+    """Q5_K (176 B): the Q4_K header (d, dmin, 12 scale bytes), qh[32], qs[128].
+    q: 256 values 0..31; weight 64i + 32h + l keeps its low 4 bits in nibble h of
+    qs[32i + l] and its fifth bit in bit 2i + h of qh[l]."""
+    assert q.shape == (256,) and int(q.max()) < 32
+    hdr = pack_q4_k(d, dmin, sc, m, q & 0xF)
+    b = np.zeros(176, np.uint8)
+    b[0:16] = hdr[0:16]
+    b[48:176] = hdr[16:144]
+    qh = np.zeros(32, np.uint8)
+    for i in range(4):
+        for h in range(2):
+            for l in range(32):
+                qh[l] |= ((int(q[64 * i + 32 * h + l]) >> 4) & 1) << (2 * i + h)
+    b[16:48] = qh
+    return b
 
 
 def pack_q6_k(d: float, sc: list[int], q: np.ndarray) -> np.ndarray:

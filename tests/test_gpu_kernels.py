@@ -16,7 +16,7 @@ from tests.gpu_util import (assert_close, dev_f32, dev_u32, host, rel_l2, upload
 
 pytestmark = pytest.mark.gpu
 
-DTYPES = [GgmlDType.Q4_K, GgmlDType.Q6_K, GgmlDType.Q8_0]
+DTYPES = [GgmlDType.Q4_K, GgmlDType.Q5_K, GgmlDType.Q6_K, GgmlDType.Q8_0]
 
 
 def _log(msg):
@@ -90,7 +90,7 @@ def test_mul_mv_id_repeated_ids_ragged_rows(dev, orc, dt):
     # n_out = 100 (ragged tail), k = 512 (two super-blocks), nonzero base_off
     rng = np.random.default_rng(2)
     ids = rng.integers(0, 3, (2, 2)).astype(np.uint32)
-    got, want, *_ = _mv_case(orc, dt, 3, 100, 512, 2, 2, 2, ids, 0x400, base_off=16 if dt == GgmlDType.Q4_K else 2)
+    got, want, *_ = _mv_case(orc, dt, 3, 100, 512, 2, 2, 2, ids, 0x400, base_off=16 if dt in (GgmlDType.Q4_K, GgmlDType.Q5_K) else 2)
     assert_close(got, want, what="ragged")
 
 

@@ -58,14 +58,26 @@ def test_decode_layer(dev, orc, name):
         oracle_check(orc, layer, x, out, ids, w, f"{name} seed={seed}", max_flips=0)
 
 
-def test_verify_block_t16(dev, orc):
-    """C2: 16-token speculative verify block (below MM_ID_MIN_SEQ: fused decode kernels)."""
+@pytest.mark.parametrize("t", [5, 16, 31])
+def test_verify_block(dev, orc, t):
+    """C2: speculative verify blocks below MM_ID_MIN_SEQ (decode kernels, (token,
+    slot) pairs walked in expert order)."""
     cfg = CONFIGS["C2"]
-    _log("C2 t=16")
+    _log(f"C2 t={t}")
     layer = build_layer(cfg["spec"], seed=1002)
-    x = make_x(cfg["spec"], 11, 16)
+    x = make_x(cfg["spec"], 11, t)
     out, ids, w = run_block(layer, x)
-    oracle_check(orc, layer, x, out, ids, w, "C2", max_flips=1)
+    oracle_check(orc, layer, x, out, ids, w, f"C2 t={t}", max_flips=1)
+
+
+def test_verify_block_no_shared(dev, orc):
+    """Expert-ordered verify without a shared expert (C0 shape, t = 20)."""
+    cfg = CONFIGS["C0"]
+    _log("C0 t=20")
+    layer = build_layer(cfg["spec"], seed=1010)
+    x = make_x(cfg["spec"], 12, 20)
+    out, ids, w = run_block(layer, x)
+    oracle_check(orc, layer, x, out, ids, w, "C0 t=20", max_flips=1)
 
 
 def test_prefill_grouped_gemm_small(dev, orc):
@@ -110,6 +122,20 @@ def test_prefill_full_size_mm_vs_decode_and_sample(dev, orc):
     mv = host(routed + layer.block.shared.forward(xd))
     assert_close(mv[rows], want, what="C3 decode path sample vs oracle")
     assert_close(out, mv, rel=2e-3, max_of_rms=np.inf, what="C3 mm vs mv (all rows)")
+
+
+@pytest.mark.parametrize("gate_dt,down_dt", [(GgmlDType.Q5_K, GgmlDType.Q5_K), (GgmlDType.Q5_K, GgmlDType.Q6_K),
+                                             (GgmlDType.Q4_K, GgmlDType.Q5_K)], ids=["q5q5", "q5q6", "q4q5"])
+def test_q5_k_layers(dev, orc, gate_dt, down_dt):
+    """Q5_K experts (the UD-Q4_K_XL mixes): decode (t = 1), expert-ordered verify
+    (t = 12) and the grouped GEMM (t = 64), shared expert included."""
+    spec = LayerSpec(1024, 512, 64, 6, gate_dt, down_dt, shared=True)
+    layer = build_layer(spec, seed=1020 + int(gate_dt) + int(down_dt))
+    for t in (1, 12, 64):
+        _log(f"q5 {gate_dt.name}/{down_dt.name} t={t}")
+        x = make_x(spec, 31 + t, t)
+        out, ids, w = run_block(layer, x)
+        oracle_check(orc, layer, x, out, ids, w, f"{gate_dt.name}/{down_dt.name} t={t}", max_flips=1)
 
 
 def test_fused_experts_ops_match_block(dev, orc):

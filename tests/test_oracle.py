@@ -10,9 +10,9 @@ import math
 import numpy as np
 import pytest
 
-from tests._pack import (pack_q4_k, pack_q6_k, pack_q8_0, q4_k_values, q6_k_values, f16_bits)
+from tests._pack import (pack_q4_k, pack_q5_k, pack_q6_k, pack_q8_0, q4_k_values, q6_k_values, f16_bits)
 
-Q8_0, Q4_K, Q6_K = 8, 12, 14
+Q8_0, Q4_K, Q5_K, Q6_K = 8, 12, 13, 14
 
 # sigmoid of the reference's fixed logit row [2,-2,0,1,-1,3,0.5,-0.5] (moe.rs:384-387)
 S2, S1, S3, S05 = 0.8807970779778823, 0.7310585786300049, 0.9525741268224334, 0.6224593312018546
@@ -90,6 +90,45 @@ def test_q4_k_rounding_order(orc):
     assert np.array_equal(got.view(np.uint32), exp.astype(f).view(np.uint32))
     # sanity: the exact value is within 1 ulp-ish of both
     assert np.allclose(got, q4_k_values(d, dmin, sc, m, q), rtol=1e-6, atol=1e-6)
+
+
+def test_q5_k_integer_grid_exact(orc):
+    """d*sc_j*q - dmin*m_j with q in 0..31 (the fifth bit from qh)."""
+    rng = np.random.default_rng(20)
+    for trial in range(20):
+        d = [1.0, 0.5, 2.0, 0.25][trial % 4]
+        dmin = [0.5, 1.0, 0.125, 0.0][trial % 4]
+        sc = [int(v) for v in rng.integers(0, 64, 8)]
+        m = [int(v) for v in rng.integers(0, 64, 8)]
+        q = rng.integers(0, 32, 256)
+        got = orc.dequantize(Q5_K, pack_q5_k(d, dmin, sc, m, q), 256)
+        assert np.array_equal(got.astype(np.float64), q4_k_values(d, dmin, sc, m, q)), trial
+
+
+def test_q5_k_each_high_bit_moves_only_its_weight(orc):
+    q = np.full(256, 5)
+    base = orc.dequantize(Q5_K, pack_q5_k(1.0, 0.0, [3] * 8, [0] * 8, q), 256)
+    for w in [0, 31, 32, 63, 64, 100, 159, 200, 255]:
+        q2 = q.copy()
+        q2[w] += 16
+        got = orc.dequantize(Q5_K, pack_q5_k(1.0, 0.0, [3] * 8, [0] * 8, q2), 256)
+        changed = np.nonzero(got != base)[0]
+        assert changed.tolist() == [w], w
+        assert got[w] - base[w] == 48.0  # 16 * d * sc
+
+
+def test_q5_k_special_cases_and_rounding(orc):
+    assert np.all(orc.dequantize(Q5_K, np.zeros(176, np.uint8), 256) == 0)
+    rng = np.random.default_rng(21)
+    d, dmin = float(np.float16(0.0047)), float(np.float16(0.0061))
+    sc = [int(v) for v in rng.integers(1, 64, 8)]
+    m = [int(v) for v in rng.integers(1, 64, 8)]
+    q = rng.integers(0, 32, 256)
+    got = orc.dequantize(Q5_K, pack_q5_k(d, dmin, sc, m, q), 256)
+    j = np.arange(256) // 32
+    f = np.float32
+    exp = (f(d) * np.array(sc, f)[j] * q.astype(f)) - f(dmin) * np.array(m, f)[j]
+    assert np.array_equal(got.view(np.uint32), exp.astype(f).view(np.uint32))
 
 
 def test_q6_k_integer_grid_exact(orc):
@@ -194,7 +233,7 @@ def test_tensor_key_matches_python(orc):
         assert orc.lib().or_mix64(seed) == mix64(seed)
 
 
-@pytest.mark.parametrize("dt", [Q4_K, Q6_K, Q8_0])
+@pytest.mark.parametrize("dt", [Q4_K, Q5_K, Q6_K, Q8_0])
 def test_synth_ranges_are_consistent(orc, dt):
     key = 0xDEADBEEF
     ts = orc.TSIZE[dt]
@@ -203,7 +242,7 @@ def test_synth_ranges_are_consistent(orc, dt):
         assert np.array_equal(orc.synth_bytes(dt, key, a, b - a), whole[a:b])
     # scale fields decode to f16 values in [0.001, 0.01]
     blocks = whole.reshape(40, ts)
-    offs = {Q4_K: [0, 2], Q6_K: [208], Q8_0: [0]}[dt]
+    offs = {Q4_K: [0, 2], Q5_K: [0, 2], Q6_K: [208], Q8_0: [0]}[dt]
     for o in offs:
         v = blocks[:, o:o + 2].copy().view(np.float16).astype(np.float32).ravel()
         assert np.all(v >= np.float16(0.001)) and np.all(v <= np.float16(0.01))
@@ -229,7 +268,7 @@ def orc_expert(dt, key, e, n_out, k):
     return o.expert_blocks(dt, key, e, n_out, k)
 
 
-@pytest.mark.parametrize("dt", [Q4_K, Q6_K, Q8_0])
+@pytest.mark.parametrize("dt", [Q4_K, Q5_K, Q6_K, Q8_0])
 def test_mul_mv_id_brute_force(orc, dt):
     rng = np.random.default_rng(7)
     n_expert, n_out, k, t, top_k = 4, 8, 256, 3, 2
@@ -300,7 +339,7 @@ def test_rmsnorm_closed_form(orc):
 
 
 # ---- ReferenceExperts wiring (structure of moe.rs:522-609) ----------------------------------
-@pytest.mark.parametrize("dt", [Q4_K, Q6_K, Q8_0])
+@pytest.mark.parametrize("dt", [Q4_K, Q5_K, Q6_K, Q8_0])
 def test_reference_experts_matches_per_token_oracle(orc, dt):
     rng = np.random.default_rng(12)
     n_expert, ff, hidden, seq, top_k = 4, 256, 256, 3, 2
