@@ -286,7 +286,7 @@ struct Ws {
 struct Plan {
     bool mm, fused_router, has_shared;
     bool shared_in_decode;  // shared expert rides in the fused decode kernels (same quant types)
-    bool expert_order;      // decode kernels walk (token, slot) pairs in expert order (t > 4)
+    bool expert_order;      // decode kernels walk (token, slot) pairs in expert order (unfused router)
     int64_t min_seq;
 };
 

@@ -199,7 +199,7 @@ mx_status launch_route_logits(const float *x, const float *router, int t, int hi
     return MX_OK;
 }
 
-// ---- decode router, logits half (t <= RF_MAX_T) ------------------------------------------
+// ---- decode router, logits half (t <= RF_TOKENS) ----------------------------------------
 // Blocks [0, n_expert): one expert each.  Its 256 threads split the expert's
 // router row (contiguous in the GGUF layout) and the token rows, so every
 // logit costs one memory round trip.  Optional RMSNorm is folded in: the block
@@ -214,7 +214,8 @@ mx_status launch_route_logits(const float *x, const float *router, int t, int hi
 // Blocks [n_expert, n_expert + n_stage): stage the (normalised) token rows for
 // the expert kernels (mx_stage.h layout, one row of xstage_bytes(hidden) per
 // token in `xstage`) and, if requested, write them as f32 to `x_normed`.
-constexpr int RF_MAX_T = 4;
+constexpr int RF_MAX_T = 4;     // tokens per register pass
+constexpr int RF_TOKENS = 32;   // tokens per launch
 constexpr int RF_THREADS = 256;
 constexpr int RF_UNROLL = 4;  // float4 loads per thread per pass
 
@@ -259,28 +260,36 @@ __global__ void __launch_bounds__(RF_THREADS) k_route_fused(
     float *probs = reinterpret_cast<float *>(keys + (int64_t)t * n_expert);
     const int tid = threadIdx.x;
     if (blockIdx.x >= n_expert) {
-        // ---- staging blocks
-        float ss[RF_MAX_T] = {};
-        if (rms_alpha) {
-            for (int h = 4 * tid; h < hidden; h += 4 * RF_THREADS) {
-                for (int tok = 0; tok < t; tok++) {
-                    const float4 v = *reinterpret_cast<const float4 *>(x + (int64_t)tok * hidden + h);
-                    ss[tok] = __builtin_fmaf(v.x, v.x, ss[tok]);
-                    ss[tok] = __builtin_fmaf(v.y, v.y, ss[tok]);
-                    ss[tok] = __builtin_fmaf(v.z, v.z, ss[tok]);
-                    ss[tok] = __builtin_fmaf(v.w, v.w, ss[tok]);
-                }
-            }
-            block_sums(ss, t, s_red);
-        }
+        // ---- staging blocks: quarter qi = 8 values of token qi / nq
+        __shared__ float s_m[RF_TOKENS];
         const int nq = hidden / 8;
-        const int qi = (blockIdx.x - n_expert) * RF_THREADS + tid;
+        const int qi0 = (blockIdx.x - n_expert) * RF_THREADS;
+        const int qi = qi0 + tid;
         const int tok = qi / nq, q = qi % nq;
         const bool valid = tok < t;
+        const int ta = qi0 / nq, tb = min(t - 1, (qi0 + RF_THREADS - 1) / nq);
+        if (rms_alpha) {  // RMS of the tokens this block touches, RF_MAX_T at a time (block-uniform loop)
+            for (int t0 = ta; t0 <= tb; t0 += RF_MAX_T) {
+                const int tc = min(RF_MAX_T, tb - t0 + 1);
+                float ss[RF_MAX_T] = {};
+                for (int h = 4 * tid; h < hidden; h += 4 * RF_THREADS) {
+                    for (int k = 0; k < tc; k++) {
+                        const float4 v = *reinterpret_cast<const float4 *>(x + (int64_t)(t0 + k) * hidden + h);
+                        ss[k] = __builtin_fmaf(v.x, v.x, ss[k]);
+                        ss[k] = __builtin_fmaf(v.y, v.y, ss[k]);
+                        ss[k] = __builtin_fmaf(v.z, v.z, ss[k]);
+                        ss[k] = __builtin_fmaf(v.w, v.w, ss[k]);
+                    }
+                }
+                block_sums(ss, tc, s_red);
+                if (tid < tc) s_m[t0 - ta + tid] = sqrtf(ss[tid] / (float)hidden + rms_eps);
+            }
+            __syncthreads();
+        }
         float v[8] = {};
         if (valid) {
             load8f(x + (int64_t)tok * hidden + 8 * q, v);
-            if (rms_alpha) norm8(v, rms_alpha, 8 * q, sqrtf(ss[tok] / (float)hidden + rms_eps));
+            if (rms_alpha) norm8(v, rms_alpha, 8 * q, s_m[tok - ta]);
             if (x_normed) {
                 float4 *o = reinterpret_cast<float4 *>(x_normed + (int64_t)tok * hidden + 8 * q);
                 o[0] = make_float4(v[0], v[1], v[2], v[3]);
@@ -290,59 +299,65 @@ __global__ void __launch_bounds__(RF_THREADS) k_route_fused(
         if (xstage) stage_quarter(v, q, valid, xstage + (int64_t)(valid ? tok : 0) * xstage_stride(hidden), hidden);
         return;
     }
-    // ---- expert blocks
+    // ---- expert blocks: the expert's router row against every token, RF_MAX_T
+    // tokens per pass (the row stays in L1/L2 after the first pass)
     const int e = blockIdx.x;
     const float be = bias[e];  // issued early: needed only after the reduction
     const float *rr = router + (int64_t)e * hidden;
-    float dot[RF_MAX_T] = {}, ss[RF_MAX_T] = {};
-    for (int c0 = 4 * tid; c0 < hidden; c0 += 4 * RF_THREADS * RF_UNROLL) {
-        float4 rv[RF_UNROLL], av[RF_UNROLL], xv[RF_MAX_T][RF_UNROLL];
-#pragma unroll
-        for (int i = 0; i < RF_UNROLL; i++) {
-            const int h = c0 + 4 * RF_THREADS * i;
-            const bool ok = h < hidden;
-            const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-            rv[i] = ok ? *reinterpret_cast<const float4 *>(rr + h) : z;
-            av[i] = (ok && rms_alpha) ? *reinterpret_cast<const float4 *>(rms_alpha + h) : make_float4(1.f, 1.f, 1.f, 1.f);
-#pragma unroll
-            for (int tok = 0; tok < RF_MAX_T; tok++)
-                xv[tok][i] = (ok && tok < t) ? *reinterpret_cast<const float4 *>(x + (int64_t)tok * hidden + h) : z;
-        }
-#pragma unroll
-        for (int tok = 0; tok < RF_MAX_T; tok++) {
-            if (tok >= t) break;
+    for (int t0 = 0; t0 < t; t0 += RF_MAX_T) {
+        const int tc = min(RF_MAX_T, t - t0);
+        const float *xt = x + (int64_t)t0 * hidden;
+        float dot[RF_MAX_T] = {}, ss[RF_MAX_T] = {};
+        for (int c0 = 4 * tid; c0 < hidden; c0 += 4 * RF_THREADS * RF_UNROLL) {
+            float4 rv[RF_UNROLL], av[RF_UNROLL], xv[RF_MAX_T][RF_UNROLL];
 #pragma unroll
             for (int i = 0; i < RF_UNROLL; i++) {
-                const float4 v = xv[tok][i];
-                ss[tok] = __builtin_fmaf(v.x, v.x, ss[tok]);
-                ss[tok] = __builtin_fmaf(v.y, v.y, ss[tok]);
-                ss[tok] = __builtin_fmaf(v.z, v.z, ss[tok]);
-                ss[tok] = __builtin_fmaf(v.w, v.w, ss[tok]);
-                dot[tok] = __builtin_fmaf(v.x * av[i].x, rv[i].x, dot[tok]);
-                dot[tok] = __builtin_fmaf(v.y * av[i].y, rv[i].y, dot[tok]);
-                dot[tok] = __builtin_fmaf(v.z * av[i].z, rv[i].z, dot[tok]);
-                dot[tok] = __builtin_fmaf(v.w * av[i].w, rv[i].w, dot[tok]);
+                const int h = c0 + 4 * RF_THREADS * i;
+                const bool ok = h < hidden;
+                const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+                rv[i] = ok ? *reinterpret_cast<const float4 *>(rr + h) : z;
+                av[i] = (ok && rms_alpha) ? *reinterpret_cast<const float4 *>(rms_alpha + h)
+                                          : make_float4(1.f, 1.f, 1.f, 1.f);
+#pragma unroll
+                for (int k = 0; k < RF_MAX_T; k++)
+                    xv[k][i] = (ok && k < tc) ? *reinterpret_cast<const float4 *>(xt + (int64_t)k * hidden + h) : z;
+            }
+#pragma unroll
+            for (int k = 0; k < RF_MAX_T; k++) {
+                if (k >= tc) break;
+#pragma unroll
+                for (int i = 0; i < RF_UNROLL; i++) {
+                    const float4 v = xv[k][i];
+                    ss[k] = __builtin_fmaf(v.x, v.x, ss[k]);
+                    ss[k] = __builtin_fmaf(v.y, v.y, ss[k]);
+                    ss[k] = __builtin_fmaf(v.z, v.z, ss[k]);
+                    ss[k] = __builtin_fmaf(v.w, v.w, ss[k]);
+                    dot[k] = __builtin_fmaf(v.x * av[i].x, rv[i].x, dot[k]);
+                    dot[k] = __builtin_fmaf(v.y * av[i].y, rv[i].y, dot[k]);
+                    dot[k] = __builtin_fmaf(v.z * av[i].z, rv[i].z, dot[k]);
+                    dot[k] = __builtin_fmaf(v.w * av[i].w, rv[i].w, dot[k]);
+                }
             }
         }
-    }
-    block_sums(dot, t, s_red);
-    if (rms_alpha) block_sums(ss, t, s_red);
-    if (tid < t) {
-        const float lg = rms_alpha ? dot[tid] / sqrtf(ss[tid] / (float)hidden + rms_eps) : dot[tid];
-        const float p = 1.0f / (expf(-lg) + 1.0f);  // sigmoid (moe.rs:101)
-        const int64_t o = (int64_t)tid * n_expert + e;
-        keys[o] = sel_key(p + be, e);
-        probs[o] = p;
+        block_sums(dot, tc, s_red);
+        if (rms_alpha) block_sums(ss, tc, s_red);
+        if (tid < tc) {
+            const float lg = rms_alpha ? dot[tid] / sqrtf(ss[tid] / (float)hidden + rms_eps) : dot[tid];
+            const float p = 1.0f / (expf(-lg) + 1.0f);  // sigmoid (moe.rs:101)
+            const int64_t o = (int64_t)(t0 + tid) * n_expert + e;
+            keys[o] = sel_key(p + be, e);
+            probs[o] = p;
+        }
     }
 }
 
-int route_fused_max_t() { return RF_MAX_T; }
+int route_fused_max_t() { return RF_TOKENS; }
 
 mx_status launch_route_fused(const float *x, const float *rms_alpha, float rms_eps, float *x_normed,
                              const float *router, const float *bias, int t, int hidden, int n_expert, void *ws,
                              uint8_t *xstage, hipStream_t s) {
     if (t == 0) return MX_OK;
-    if (t > RF_MAX_T) return fail(MX_ERR_SHAPE, "fused router handles at most %d tokens", RF_MAX_T);
+    if (t > RF_TOKENS) return fail(MX_ERR_SHAPE, "fused router handles at most %d tokens", RF_TOKENS);
     if (hidden % 32) return fail(MX_ERR_SHAPE, "fused router needs hidden %% 32 == 0");
     const int nq = t * (hidden / 8);
     const int n_stage = (xstage || x_normed) ? (nq + RF_THREADS - 1) / RF_THREADS : 0;
