@@ -58,7 +58,7 @@ def test_decode_layer(dev, orc, name):
         oracle_check(orc, layer, x, out, ids, w, f"{name} seed={seed}", max_flips=0)
 
 
-@pytest.mark.parametrize("t", [5, 16, 31])
+@pytest.mark.parametrize("t", [2, 5, 16, 31])
 def test_verify_block(dev, orc, t):
     """C2: speculative verify blocks below MM_ID_MIN_SEQ (decode kernels, (token,
     slot) pairs walked in expert order)."""
