@@ -6,6 +6,7 @@
 #include <cstring>
 
 #include "mx_launch.h"
+#include "mx_stage.h"
 
 namespace mx {
 
@@ -313,7 +314,7 @@ struct Layout {
     uint8_t *route_ws = nullptr;
     float *x_normed = nullptr, *logits = nullptr, *w = nullptr, *act = nullptr;
     uint32_t *ids = nullptr, *zero_ids = nullptr;
-    uint8_t *xstage = nullptr;
+    uint8_t *xstage = nullptr, *xstage_gm = nullptr;
     float *part = nullptr;
     unsigned *counters = nullptr;
     int32_t *map = nullptr, *map_sh = nullptr, *order = nullptr;
@@ -339,6 +340,7 @@ Layout carve(const mx_moe_layer *L, int64_t t, const Plan &p, void *base) {
     if (!p.mm) {
         const int64_t slots = K + (p.shared_in_decode ? 1 : 0);
         o.xstage = ws.take<uint8_t>(t * stage_row_bytes((int)H));
+        if (H % 64 == 0) o.xstage_gm = ws.take<uint8_t>(t * xstage_gm_stride((int)H));
         o.act = ws.take<float>(t * slots * FF);
         o.part = ws.take<float>(t * slots * H);
         o.counters = ws.take<unsigned>(decode_down_counter_words((int)t, (int)H));
@@ -485,7 +487,7 @@ mx_status moe_forward_impl(const mx_moe_layer *L, const float *x, int64_t t, con
         // launch (below).
         for (int r = 0; r < rep(0); r++)
             MX_TRY(launch_route_fused(x, L->rms_alpha, L->rms_eps, o.x_normed, L->router, L->exp_probs_b, (int)t,
-                                      (int)H, (int)E, o.route_ws, o.xstage, s));
+                                      (int)H, (int)E, o.route_ws, o.xstage, o.xstage_gm, s));
         if (L->rms_alpha) xin = o.x_normed;
     } else {
         if (L->rms_alpha) {
@@ -495,7 +497,7 @@ mx_status moe_forward_impl(const mx_moe_layer *L, const float *x, int64_t t, con
         MX_TRY(launch_route_logits(xin, L->router, (int)t, (int)H, (int)E, o.logits, s));
         MX_TRY(launch_route_select(o.logits, L->exp_probs_b, (int)t, (int)E, (int)K, scale, apply,
                                    L->weights_norm, ids, w, s));
-        if (!p.mm) MX_TRY(launch_stage_rows(xin, (int)t, (int)H, o.xstage, s));
+        if (!p.mm) MX_TRY(launch_stage_rows(xin, (int)t, (int)H, o.xstage, o.xstage_gm, s));
         if (p.expert_order)
             MX_TRY(launch_sort_pairs(ids, (int)t, (int)K, p.shared_in_decode ? 1 : 0, (int)E, o.order, s));
     }
@@ -517,7 +519,8 @@ mx_status moe_forward_impl(const mx_moe_layer *L, const float *x, int64_t t, con
             shared_out = o.sh_out;
         }
         DecodeGateUpArgs ga{gg.w, gu.w, gg.expert_bytes, gg.row_bytes, shf ? sg.w : nullptr, shf ? su.w : nullptr,
-                            sg.row_bytes, (int)E, (int)FF, (int)H, o.xstage, ids, (int)t, (int)K, o.act, o.order};
+                            sg.row_bytes, (int)E, (int)FF, (int)H, o.xstage, ids, (int)t, (int)K, o.act, o.order,
+                            o.xstage_gm};
         if (p.fused_router) {
             // the top-k of every token, next to the shared expert's gate/up rows (which
             // need no routing) -- then the routed slots, which read the selection

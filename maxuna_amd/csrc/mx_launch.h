@@ -38,6 +38,7 @@ struct DecodeGateUpArgs {
     int t, top_k;
     float *act;                          // [t, slots, ff], slots = top_k + (sh_gate != NULL)
     const int32_t *order;                // NULL, or the t * slots (token, slot) pairs sorted by expert
+    const uint8_t *xstage_gm;            // NULL, or the group-major copy of xstage (Q4_K / Q5_K reads)
 };
 // Optional top-k blocks in front of the gate/up blocks (decode router split):
 // block i < n_sel selects token i from keys/probs [n_sel, n_expert] (written by
@@ -100,9 +101,11 @@ size_t route_fused_ws_bytes(int t, int hidden, int n_expert);
 int route_fused_max_t();
 mx_status launch_route_fused(const float *x, const float *rms_alpha, float rms_eps,
                              float *x_normed, const float *router, const float *bias, int t,
-                             int hidden, int n_expert, void *ws, uint8_t *xstage, hipStream_t s);
+                             int hidden, int n_expert, void *ws, uint8_t *xstage, uint8_t *xstage_gm,
+                             hipStream_t s);
 // Stages t rows of k values (mx_stage.h layout, xstage_bytes(k) per row).
-mx_status launch_stage_rows(const float *x, int t, int k, uint8_t *xstage, hipStream_t s);
+// xstage_gm: optional group-major copy (mx_stage.h; k % 64 == 0)
+mx_status launch_stage_rows(const float *x, int t, int k, uint8_t *xstage, uint8_t *xstage_gm, hipStream_t s);
 size_t stage_row_bytes(int k);
 
 // mx_elem.hip

@@ -442,6 +442,34 @@ __device__ __forceinline__ void stream_rows(const uint8_t *const (&w)[NM], int64
     }
 }
 
+// Loads this lane's slices from the group-major staged copy (mx_stage.h):
+// nine 16-byte loads per group, each wave instruction 1 KB of consecutive bytes.
+template <int DT, int NG>
+__device__ __forceinline__ void load_xs_gm(const uint8_t *gm, int k, const Geo<DT> &geo,
+                                           typename Q<DT>::X (&xs)[NG]) {
+    static_assert(DT == kQ4_K || DT == kQ5_K, "group-major staging is the 64-value group layout");
+    const int G = k / 64;
+    const uint4 *c = reinterpret_cast<const uint4 *>(gm);
+    const int sub = (threadIdx.x & 63) & (geo.P - 1);
+#pragma unroll
+    for (int jg = 0; jg < NG; jg++) {
+        int g = sub + geo.P * jg;
+        g = g < G ? g : 0;
+        typename Q<DT>::X &x = xs[jg];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const uint4 h = c[(size_t)q * G + g], l = c[(size_t)(4 + q) * G + g];
+            x.h[4 * q] = h.x; x.h[4 * q + 1] = h.y; x.h[4 * q + 2] = h.z; x.h[4 * q + 3] = h.w;
+            x.l[4 * q] = l.x; x.l[4 * q + 1] = l.y; x.l[4 * q + 2] = l.z; x.l[4 * q + 3] = l.w;
+        }
+        const uint4 sc = c[(size_t)8 * G + g];
+        x.sa = __uint_as_float(sc.x);
+        x.sb = __uint_as_float(sc.y);
+        x.ssa = __uint_as_float(sc.z);
+        x.ssb = __uint_as_float(sc.w);
+    }
+}
+
 // Loads this lane's slices of a staged activation row (global memory or LDS).
 template <int DT, int NG>
 __device__ __forceinline__ void load_xs(const uint8_t *staged, int k, const Geo<DT> &geo,
@@ -589,7 +617,7 @@ mx_status launch_mul_mv_id(int dtype, const MvArgs &a, hipStream_t s) {
 #ifndef MX_GU_WPE
 #define MX_GU_WPE 6
 #endif
-template <int DT, int NG>
+template <int DT, int NG, bool GM>
 __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(MX_GU_WPE))) k_decode_gate_up(DecodeGateUpArgs a, int ni, int slot0, int nslot,
                                                                DecodeSelArgs sel) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -640,8 +668,13 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
     typename Q<DT>::X xs[NG];
     const uint8_t *staged = a.xstage + (int64_t)tok * xstage_stride(a.hidden);
     uint8_t *ring = lds + wave * (RING_GU * ni * 1024);
-    stream_rows<DT, NG, Batch<NG>::NIT, 2, RING_GU>(w, rb, geo, xs, r0, min(r0 + RW_GU, a.ff), ring, ni,
-                                                     [&] { load_xs<DT, NG>(staged, a.hidden, geo, xs); }, [] {},
+    // GM: the slices come from the group-major copy (a compile-time choice: a
+    // runtime branch between the two loaders measurably delays the loads)
+    auto pre = [&] {
+        if constexpr (GM) load_xs_gm<DT, NG>(a.xstage_gm + (int64_t)tok * xstage_gm_stride(a.hidden), a.hidden, geo, xs);
+        else load_xs<DT, NG>(staged, a.hidden, geo, xs);
+    };
+    stream_rows<DT, NG, Batch<NG>::NIT, 2, RING_GU>(w, rb, geo, xs, r0, min(r0 + RW_GU, a.ff), ring, ni, pre, [] {},
                                                      [&](int row, const float (&s)[2]) {
                                                          const float g = s[0];
                                                          const float sg = g / (1.0f + expf(-g));
@@ -652,12 +685,18 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
 template <int DT, int NG>
 static mx_status launch_gu_ng(const DecodeGateUpArgs &a, unsigned blocks, int slot0, int nslot,
                               const DecodeSelArgs &sel, hipStream_t s) {
+    constexpr bool GM_OK = DT == kQ4_K || DT == kQ5_K;
     const int ni = ring_insts<DT, NG>(2, a.hidden, a.gu_row_bytes);
     if (ni > DMA_MAX_INSTS) return fail(MX_ERR_SHAPE, "decode gate/up: rows too long for the LDS ring");
     size_t lds = (size_t)WAVES * RING_GU * ni * 1024;
     if (sel.n_sel && lds < sizeof(SelShared)) lds = sizeof(SelShared);
     if (lds > 160 * 1024) return fail(MX_ERR_SHAPE, "decode gate/up: hidden = %d needs %zu bytes of LDS", a.hidden, lds);
-    hipLaunchKernelGGL((k_decode_gate_up<DT, NG>), dim3(blocks), dim3(64 * WAVES), lds, s, a, ni, slot0, nslot, sel);
+    if (GM_OK && a.xstage_gm)
+        hipLaunchKernelGGL((k_decode_gate_up<DT, NG, GM_OK>), dim3(blocks), dim3(64 * WAVES), lds, s, a, ni, slot0, nslot,
+                           sel);
+    else
+        hipLaunchKernelGGL((k_decode_gate_up<DT, NG, false>), dim3(blocks), dim3(64 * WAVES), lds, s, a, ni, slot0,
+                           nslot, sel);
     return MX_OK;
 }
 

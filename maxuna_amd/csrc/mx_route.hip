@@ -254,7 +254,7 @@ __device__ __forceinline__ void block_sums(float (&v)[RF_MAX_T], int t, float (*
 __global__ void __launch_bounds__(RF_THREADS) k_route_fused(
     const float *__restrict__ x, const float *__restrict__ rms_alpha, float rms_eps, float *__restrict__ x_normed,
     const float *__restrict__ router, const float *__restrict__ bias, int t, int hidden, int n_expert,
-    uint8_t *__restrict__ ws, uint8_t *__restrict__ xstage) {
+    uint8_t *__restrict__ ws, uint8_t *__restrict__ xstage, uint8_t *__restrict__ xstage_gm) {
     __shared__ float s_red[RF_MAX_T][RF_THREADS / 64];
     uint64_t *keys = reinterpret_cast<uint64_t *>(ws);
     float *probs = reinterpret_cast<float *>(keys + (int64_t)t * n_expert);
@@ -296,7 +296,9 @@ __global__ void __launch_bounds__(RF_THREADS) k_route_fused(
                 o[1] = make_float4(v[4], v[5], v[6], v[7]);
             }
         }
-        if (xstage) stage_quarter(v, q, valid, xstage + (int64_t)(valid ? tok : 0) * xstage_stride(hidden), hidden);
+        if (xstage)
+            stage_quarter(v, q, valid, xstage + (int64_t)(valid ? tok : 0) * xstage_stride(hidden), hidden,
+                          xstage_gm ? xstage_gm + (int64_t)(valid ? tok : 0) * xstage_gm_stride(hidden) : nullptr);
         return;
     }
     // ---- expert blocks: the expert's router row against every token, RF_MAX_T
@@ -355,38 +357,41 @@ int route_fused_max_t() { return RF_TOKENS; }
 
 mx_status launch_route_fused(const float *x, const float *rms_alpha, float rms_eps, float *x_normed,
                              const float *router, const float *bias, int t, int hidden, int n_expert, void *ws,
-                             uint8_t *xstage, hipStream_t s) {
+                             uint8_t *xstage, uint8_t *xstage_gm, hipStream_t s) {
     if (t == 0) return MX_OK;
     if (t > RF_TOKENS) return fail(MX_ERR_SHAPE, "fused router handles at most %d tokens", RF_TOKENS);
     if (hidden % 32) return fail(MX_ERR_SHAPE, "fused router needs hidden %% 32 == 0");
+    if (xstage_gm && hidden % 64) return fail(MX_ERR_SHAPE, "group-major staging needs hidden %% 64 == 0");
     const int nq = t * (hidden / 8);
     const int n_stage = (xstage || x_normed) ? (nq + RF_THREADS - 1) / RF_THREADS : 0;
     hipLaunchKernelGGL(k_route_fused, dim3((unsigned)(n_expert + n_stage)), dim3(RF_THREADS), 0, s, x, rms_alpha,
                        rms_eps, x_normed, router, bias, t, hidden, n_expert, reinterpret_cast<uint8_t *>(ws),
-                       xstage);
+                       xstage, xstage_gm);
     MX_LAUNCH("k_route_fused");
     return MX_OK;
 }
 
 // ---- activation staging for the decode expert kernels (rows of t tokens) ---------------
 __global__ void __launch_bounds__(256) k_stage_rows(const float *__restrict__ x, int t, int k,
-                                                    uint8_t *__restrict__ xstage) {
+                                                    uint8_t *__restrict__ xstage, uint8_t *__restrict__ xstage_gm) {
     const int nq = k / 8;
     const int qi = blockIdx.x * 256 + threadIdx.x;
     const int tok = qi / nq, q = qi % nq;
     const bool valid = tok < t;
     float v[8] = {};
     if (valid) load8f(x + (int64_t)tok * k + 8 * q, v);
-    stage_quarter(v, q, valid, xstage + (int64_t)(valid ? tok : 0) * xstage_stride(k), k);
+    stage_quarter(v, q, valid, xstage + (int64_t)(valid ? tok : 0) * xstage_stride(k), k,
+                  xstage_gm ? xstage_gm + (int64_t)(valid ? tok : 0) * xstage_gm_stride(k) : nullptr);
 }
 
 size_t stage_row_bytes(int k) { return (size_t)xstage_stride(k); }
 
-mx_status launch_stage_rows(const float *x, int t, int k, uint8_t *xstage, hipStream_t s) {
+mx_status launch_stage_rows(const float *x, int t, int k, uint8_t *xstage, uint8_t *xstage_gm, hipStream_t s) {
     if (t == 0) return MX_OK;
     if (k % 32) return fail(MX_ERR_SHAPE, "staging needs k %% 32 == 0");
+    if (xstage_gm && k % 64) return fail(MX_ERR_SHAPE, "group-major staging needs k %% 64 == 0");
     const int64_t nq = (int64_t)t * (k / 8);
-    hipLaunchKernelGGL(k_stage_rows, dim3((unsigned)((nq + 255) / 256)), dim3(256), 0, s, x, t, k, xstage);
+    hipLaunchKernelGGL(k_stage_rows, dim3((unsigned)((nq + 255) / 256)), dim3(256), 0, s, x, t, k, xstage, xstage_gm);
     MX_LAUNCH("k_stage_rows");
     return MX_OK;
 }

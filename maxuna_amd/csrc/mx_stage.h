@@ -35,12 +35,24 @@ struct XView {
           S8(reinterpret_cast<const int *>(base + 2 * k) + 2 * (k / 32)) {}
 };
 
+// Group-major copy for 64-value groups (the Q4_K / Q5_K decode geometry, in
+// which lane g of a row reads values 64g .. 64g+63): group g has 9 16-byte
+// chunks and chunk c of every group is stored together, at byte (c * G + g) * 16
+// with G = k / 64.  Chunks 0-3: xh[64g, 64g+64); 4-7: xl[64g, 64g+64); 8: f32
+// {s[2g], s[2g+1], s[2g] * S32[2g], s[2g+1] * S32[2g+1]}.  A wave then reads its
+// slices with 9 loads of 1 KB of consecutive bytes each, instead of 16-byte
+// pieces 64 bytes apart (which made every load instruction touch ~32 lines).
+__host__ __device__ constexpr int xstage_gm_bytes(int k) { return (k / 64) * 144; }
+__host__ __device__ constexpr int xstage_gm_stride(int k) { return (xstage_gm_bytes(k) + 255) & ~255; }
+
 // Quantises quarter-group q (values 8q .. 8q+7, given in v) into the staged
-// layout at `base`.  The four quarters of a group must sit in four consecutive
+// layout at `base` (and, when gm != NULL and k % 64 == 0, into the group-major
+// copy at gm).  The four quarters of a group must sit in four consecutive
 // lanes (4m .. 4m+3) of one wave, and all four lanes must call this together
 // (cross-lane max and sum); `valid` = false lanes contribute nothing and store
 // nothing.
-__device__ __forceinline__ void stage_quarter(const float (&v)[8], int q, bool valid, uint8_t *base, int k) {
+__device__ __forceinline__ void stage_quarter(const float (&v)[8], int q, bool valid, uint8_t *base, int k,
+                                              uint8_t *gm = nullptr) {
     float mx = 0.f;
     if (valid) {
 #pragma unroll
@@ -80,6 +92,18 @@ __device__ __forceinline__ void stage_quarter(const float (&v)[8], int q, bool v
         if ((q & 3) == 0) {
             s[q >> 2] = mx / XQ_RANGE;
             S32[q >> 2] = s32;
+        }
+        if (gm) {
+            const int G = k / 64, g = q >> 3, cq = q & 7;
+            *reinterpret_cast<uint2 *>(gm + ((size_t)(cq >> 1) * G + g) * 16 + (cq & 1) * 8) = make_uint2(h[0], h[1]);
+            *reinterpret_cast<uint2 *>(gm + ((size_t)(4 + (cq >> 1)) * G + g) * 16 + (cq & 1) * 8) = make_uint2(l[0], l[1]);
+            if ((q & 3) == 0) {
+                float *sc = reinterpret_cast<float *>(gm + ((size_t)8 * G + g) * 16);
+                const int par = (q >> 2) & 1;
+                const float sg = mx / XQ_RANGE;
+                sc[par] = sg;
+                sc[2 + par] = sg * (float)s32;
+            }
         }
     }
 }
