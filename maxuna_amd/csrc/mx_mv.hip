@@ -279,13 +279,17 @@ template <> struct Q<kQ8_0> {
 #endif
 constexpr int NG_MAX = MX_NG_MAX;
 
+// full_wave: a row whose groups fit one wave takes the whole wave (one group per
+// lane, lanes past G idle) instead of P = the largest power of two dividing G;
+// fewer activation registers per lane at the cost of idle lanes.
 template <int DT> struct Geo {
     int G, P, NG, RPI;
-    __host__ __device__ explicit Geo(int k) {
+    __host__ __device__ explicit Geo(int k, bool full_wave = false) {
         G = (k / block_size(DT)) * Q<DT>::GPB;
         int p = G & (-G);
         if (p > 64) p = 64;
         if (G / p > NG_MAX) p = 64;
+        if (full_wave && G <= 64) p = 64;
         P = p;
         NG = (G + p - 1) / p;
         RPI = 64 / p;
@@ -409,7 +413,7 @@ __device__ __forceinline__ void stream_rows(const uint8_t *const (&w)[NM], int64
 #pragma unroll
                     for (int jg = 0; jg < NG; jg++) {
                         const int g = sub + geo.P * jg;
-                        if (NG == 1 || g < geo.G) a += Q<DT>::dot(Q<DT>::load(rl, g), g, xs[jg]);
+                        if (g < geo.G) a += Q<DT>::dot(Q<DT>::load(rl, g), g, xs[jg]);
                     }
                 }
                 acc[ib][m] = a;
@@ -508,6 +512,12 @@ __device__ __forceinline__ void load_xs(const uint8_t *staged, int k, const Geo<
 #ifndef MX_WAVES_DN
 #define MX_WAVES_DN 4
 #endif
+#ifndef MX_DN_FULL
+#define MX_DN_FULL 0
+#endif
+#ifndef MX_NIT_DN
+#define MX_NIT_DN 1
+#endif
 constexpr int WAVES = MX_WAVES;
 constexpr int WAVES_DN = MX_WAVES_DN;  // waves per block of the fused down kernel
 constexpr int RW_MV = 16, RW_GU = MX_RW_GU, RW_DN = MX_RW_DN;
@@ -516,10 +526,14 @@ constexpr int RING_MV = 2, RING_GU = MX_RING_GU, RING_DN = MX_RING_DN;
 // row-iterations per batch: NIT * RPI rows are copied per DMA batch
 template <int NG> struct Batch { static constexpr int NIT = NG == 1 ? MX_NIT1 : MX_NIT2; };
 
+// the down kernel's row layout (Geo full_wave) and row-iterations per batch
+constexpr bool DN_FULL = MX_DN_FULL != 0;
+template <int NG> struct BatchDn { static constexpr int NIT = NG == 1 && DN_FULL ? MX_NIT_DN : Batch<NG>::NIT; };
+
 // DMA instructions per batch for NM matrices of row_bytes rows at k
 template <int DT, int NG>
-static int ring_insts(int nm, int k, int64_t row_bytes) {
-    return dma_insts(nm, Batch<NG>::NIT * Geo<DT>(k).RPI, row_bytes);
+static int ring_insts(int nm, int k, int64_t row_bytes, int nit = Batch<NG>::NIT, bool full_wave = false) {
+    return dma_insts(nm, nit * Geo<DT>(k, full_wave).RPI, row_bytes);
 }
 __host__ __device__ inline size_t align16(size_t v) { return (v + 15) & ~size_t(15); }
 
@@ -785,10 +799,10 @@ __global__ void __launch_bounds__(64 * WAVES_DN) __attribute__((amdgpu_waves_per
             rb = a.sh_row_bytes;
         }
         const uint8_t *const w[1] = {wp};
-        const Geo<DT> geo(a.ff);
+        const Geo<DT> geo(a.ff, DN_FULL);
         typename Q<DT>::X xs[NG];
         float *part = a.part + ((int64_t)tok * slots + slot) * a.hidden;
-        stream_rows<DT, NG, Batch<NG>::NIT, 1, RING_DN>(w, rb, geo, xs, r0, min(r0 + RW_DN, a.hidden), ring, ni,
+        stream_rows<DT, NG, BatchDn<NG>::NIT, 1, RING_DN>(w, rb, geo, xs, r0, min(r0 + RW_DN, a.hidden), ring, ni,
                                                          [&] { stage_pre(xrow, a.ff, xp); },
                                                          [&] {
                                                              stage_post(xrow, a.ff, xp, lds);
@@ -811,12 +825,27 @@ __global__ void __launch_bounds__(64 * WAVES_DN) __attribute__((amdgpu_waves_per
         const int c = tile0 + r;
         if (c >= a.hidden) break;
         const float *pc = a.part + (int64_t)tok * slots * a.hidden + c;
-        float v = 0.f;
-        for (int s = 0; s < a.top_k; s++) v = v + ld_agent(pc + (int64_t)s * a.hidden) * wt[s];
         const int64_t o = (int64_t)tok * a.hidden + c;
-        if (a.sh_down) v = v + ld_agent(pc + (int64_t)a.top_k * a.hidden);
-        else if (a.shared_out) v = v + a.shared_out[o];
-        if (a.residual) v = a.residual[o] + v;
+        // shared-expert and residual terms are loaded up front with the first chunk
+        const float sh = a.sh_down ? ld_agent(pc + (int64_t)a.top_k * a.hidden) : a.shared_out ? a.shared_out[o] : 0.f;
+        const float res = a.residual ? a.residual[o] : 0.f;
+        float v = 0.f;
+        // slots in chunks of 8: the chunk's loads are all issued before the first
+        // is used (one L2 round trip per chunk instead of one per slot)
+        for (int s0 = 0; s0 < a.top_k; s0 += 8) {
+            float p[8], q[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int s = s0 + i;
+                p[i] = s < a.top_k ? ld_agent(pc + (int64_t)s * a.hidden) : 0.f;
+                q[i] = s < a.top_k ? wt[s] : 0.f;
+            }
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+                if (s0 + i < a.top_k) v = v + p[i] * q[i];
+        }
+        if (a.sh_down || a.shared_out) v = v + sh;
+        if (a.residual) v = res + v;
         a.out[o] = v;
     }
     if (threadIdx.x == 0) reset_counter(counter);
@@ -824,7 +853,7 @@ __global__ void __launch_bounds__(64 * WAVES_DN) __attribute__((amdgpu_waves_per
 
 template <int DT, int NG>
 static mx_status launch_dn_ng(const DecodeDownArgs &a, dim3 grid, hipStream_t s) {
-    const int ni = ring_insts<DT, NG>(1, a.ff, a.d_row_bytes);
+    const int ni = ring_insts<DT, NG>(1, a.ff, a.d_row_bytes, BatchDn<NG>::NIT, DN_FULL);
     if (ni > DMA_MAX_INSTS) return fail(MX_ERR_SHAPE, "decode down: rows too long for the LDS ring");
     const size_t lds = align16(xstage_bytes(a.ff)) + (size_t)WAVES_DN * RING_DN * ni * 1024;
     if (lds > 160 * 1024) return fail(MX_ERR_SHAPE, "decode down: expert_ff = %d needs %zu bytes of LDS", a.ff, lds);
@@ -834,7 +863,7 @@ static mx_status launch_dn_ng(const DecodeDownArgs &a, dim3 grid, hipStream_t s)
 
 template <int DT>
 static mx_status launch_dn_dt(const DecodeDownArgs &a, dim3 grid, hipStream_t s) {
-    const int ng = ng_variant(Geo<DT>(a.ff).NG);
+    const int ng = ng_variant(Geo<DT>(a.ff, DN_FULL).NG);
 #define MX_L(N) return launch_dn_ng<DT, N>(a, grid, s)
     MX_NG_SWITCH(ng, MX_L)
 #undef MX_L

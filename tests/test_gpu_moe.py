@@ -124,6 +124,20 @@ def test_prefill_full_size_mm_vs_decode_and_sample(dev, orc):
     assert_close(out, mv, rel=2e-3, max_of_rms=np.inf, what="C3 mm vs mv (all rows)")
 
 
+@pytest.mark.parametrize("gate_dt,down_dt", [(GgmlDType.Q8_0, GgmlDType.Q8_0), (GgmlDType.Q6_K, GgmlDType.Q4_K),
+                                             (GgmlDType.Q4_K, GgmlDType.Q8_0)], ids=["q8q8", "q6q4", "q4q8"])
+def test_prefill_weight_types(dev, orc, gate_dt, down_dt):
+    """Grouped GEMM (t = 160: the shared expert's pairs span two m-tiles, one
+    partial) with every weight type in both the SwiGLU gate/up and the plain down
+    GEMM."""
+    spec = LayerSpec(768, 512, 32, 4, gate_dt, down_dt, shared=True)
+    layer = build_layer(spec, seed=1040 + int(gate_dt) + int(down_dt))
+    _log(f"prefill {gate_dt.name}/{down_dt.name} t=160")
+    x = make_x(spec, 41, 160)
+    out, ids, w = run_block(layer, x)
+    oracle_check(orc, layer, x, out, ids, w, f"{gate_dt.name}/{down_dt.name} t=160", max_flips=1)
+
+
 @pytest.mark.parametrize("gate_dt,down_dt", [(GgmlDType.Q5_K, GgmlDType.Q5_K), (GgmlDType.Q5_K, GgmlDType.Q6_K),
                                              (GgmlDType.Q4_K, GgmlDType.Q5_K)], ids=["q5q5", "q5q6", "q4q5"])
 def test_q5_k_layers(dev, orc, gate_dt, down_dt):
