@@ -10,6 +10,8 @@
 // contains at least one requested byte (see load8_a2).
 #pragma once
 
+#include <type_traits>
+
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 #include <stdint.h>
@@ -106,8 +108,60 @@ __device__ __forceinline__ void reset_counter(unsigned *counter) {
     __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// The value held by this lane's partner for O in {1, 2, 4, 8, 16, 32}, exchanged
+// without LDS (DPP / permlane).  The partner differs from the lane in bit log2(O)
+// and possibly in lower bits, never in higher ones: lane ^ 1, ^ 2, ^ 7
+// (row_half_mirror), ^ 15 (row_mirror), ^ 16, ^ 32.  Butterfly reductions that
+// visit O from high to low therefore still combine every lane of the group, and
+// partners are mutual, so keep/send halving stays consistent.
+template <int O> __device__ __forceinline__ float lane_partner(float v) {
+    const int iv = __float_as_int(v);
+    if constexpr (O == 1) {
+        return __int_as_float(__builtin_amdgcn_update_dpp(0, iv, 0xB1, 0xF, 0xF, false));  // quad_perm 1,0,3,2
+    } else if constexpr (O == 2) {
+        return __int_as_float(__builtin_amdgcn_update_dpp(0, iv, 0x4E, 0xF, 0xF, false));  // quad_perm 2,3,0,1
+    } else if constexpr (O == 4) {
+        return __int_as_float(__builtin_amdgcn_update_dpp(0, iv, 0x141, 0xF, 0xF, false));  // row_half_mirror
+    } else if constexpr (O == 8) {
+        return __int_as_float(__builtin_amdgcn_update_dpp(0, iv, 0x140, 0xF, 0xF, false));  // row_mirror
+    } else if constexpr (O == 16) {
+        // odd rows of [0] and even rows of [1] hold the other row's values
+        const auto r = __builtin_amdgcn_permlane16_swap((uint32_t)iv, (uint32_t)iv, false, false);
+        return __uint_as_float((threadIdx.x & 16) ? r[0] : r[1]);
+    } else {
+        static_assert(O == 32, "lane_partner: O must be a power of two <= 32");
+        const auto r = __builtin_amdgcn_permlane32_swap((uint32_t)iv, (uint32_t)iv, false, false);
+        return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
+    }
+}
+
+// f(std::integral_constant<int, O>) for O = o, o / 2, ..., 1 (o a wave-uniform power
+// of two <= 32, or 0 for none): one dispatch for the whole chain
+template <class F> __device__ __forceinline__ void for_offsets_down(int o, F &&f) {
+    switch (o) {
+    case 32: f(std::integral_constant<int, 32>{}); [[fallthrough]];
+    case 16: f(std::integral_constant<int, 16>{}); [[fallthrough]];
+    case 8: f(std::integral_constant<int, 8>{}); [[fallthrough]];
+    case 4: f(std::integral_constant<int, 4>{}); [[fallthrough]];
+    case 2: f(std::integral_constant<int, 2>{}); [[fallthrough]];
+    case 1: f(std::integral_constant<int, 1>{}); break;
+    default: break;
+    }
+}
+// f(std::integral_constant<int, O>) for the single O = o
+template <class F> __device__ __forceinline__ void at_offset(int o, F &&f) {
+    switch (o) {
+    case 32: f(std::integral_constant<int, 32>{}); break;
+    case 16: f(std::integral_constant<int, 16>{}); break;
+    case 8: f(std::integral_constant<int, 8>{}); break;
+    case 4: f(std::integral_constant<int, 4>{}); break;
+    case 2: f(std::integral_constant<int, 2>{}); break;
+    default: f(std::integral_constant<int, 1>{}); break;
+    }
+}
+
 __device__ __forceinline__ float warp_sum_width(float v, int width) {
-    for (int off = width >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    for_offsets_down(width >> 1, [&](auto c) { v += lane_partner<decltype(c)::value>(v); });
     return v;
 }
 

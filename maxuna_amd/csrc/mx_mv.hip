@@ -302,8 +302,8 @@ __host__ __device__ constexpr int ng_variant(int ng) {
 }
 
 // Reduces NB tuples of NM floats over the P lanes of each row group.  While the
-// tuple count allows, each xor step halves the tuples a lane keeps (the lane
-// whose offset bit is set keeps the upper half), so NB tuples cost
+// tuple count allows, each exchange step (lane_partner) halves the tuples a lane
+// keeps (the lane whose offset bit is set keeps the upper half), so NB tuples cost
 // NB - 1 + log2(P / NB) shuffles per float instead of NB * log2(P).  On return
 // v[0] holds the full sums of tuple `*which` on the lanes that must publish it
 // (`*leader`).  Requires P >= NB; otherwise every tuple is reduced in place and
@@ -323,22 +323,24 @@ __device__ __forceinline__ void reduce_tuples(float (&v)[NB][NM], int P, int sub
 #pragma unroll
     for (int half = NB / 2; half >= 1; half /= 2) {
         const bool up = (sub & o) != 0;
+        at_offset(o, [&](auto c) {
 #pragma unroll
-        for (int i = 0; i < half; i++) {
+            for (int i = 0; i < half; i++) {
 #pragma unroll
-            for (int m = 0; m < NM; m++) {
-                const float keep = up ? v[half + i][m] : v[i][m];
-                const float send = up ? v[i][m] : v[half + i][m];
-                v[i][m] = keep + __shfl_xor(send, o, 64);
+                for (int m = 0; m < NM; m++) {
+                    const float keep = up ? v[half + i][m] : v[i][m];
+                    const float send = up ? v[i][m] : v[half + i][m];
+                    v[i][m] = keep + lane_partner<decltype(c)::value>(send);
+                }
             }
-        }
+        });
         if (up) which += half;
         o >>= 1;
     }
-    for (; o >= 1; o >>= 1) {
+    for_offsets_down(o, [&](auto c) {
 #pragma unroll
-        for (int m = 0; m < NM; m++) v[0][m] += __shfl_xor(v[0][m], o, 64);
-    }
+        for (int m = 0; m < NM; m++) v[0][m] += lane_partner<decltype(c)::value>(v[0][m]);
+    });
     leader = (sub & (P / NB - 1)) == 0;
 }
 
@@ -387,19 +389,23 @@ __device__ __forceinline__ void stream_rows(const uint8_t *const (&w)[NM], int64
             dma16(reinterpret_cast<const uint8_t *>(src), dst + 1024 * j);
         }
     };
-    // LDS address of row `row` of matrix m in the buffer of batch bi
-    auto row_at = [&](int bi, int m, int row) -> const uint8_t * {
-        const int r0 = r_begin + bi * step;
-        uintptr_t base0, base1 = 0;
-        int n0, n1 = 0;
-        span(0, r0, base0, n0);
-        if (NM > 1 && m == 1) span(1, r0, base1, n1);
-        const uintptr_t rp = reinterpret_cast<uintptr_t>(w[m] + (int64_t)row * row_bytes);
-        const uintptr_t off = m == 0 ? rp - base0 : 16 * (uintptr_t)n0 + (rp - base1);
-        return ring + (bi % RING) * bstride + off;
-    };
     auto process = [&](int bi) {
         const int r0 = r_begin + bi * step;
+        // LDS offset of each matrix's row r0 in the batch's buffer (wave-uniform);
+        // row r0 + i sits i * row_bytes after it
+        int moff[NM];
+        {
+            uintptr_t base0, base1 = 0;
+            int n0, n1 = 0;
+            span(0, r0, base0, n0);
+            moff[0] = (bi % RING) * bstride + (int)(reinterpret_cast<uintptr_t>(w[0] + (int64_t)r0 * row_bytes) - base0);
+            if (NM > 1) {
+                span(1, r0, base1, n1);
+                moff[NM - 1] = (bi % RING) * bstride + 16 * n0 +
+                               (int)(reinterpret_cast<uintptr_t>(w[NM - 1] + (int64_t)r0 * row_bytes) - base1);
+            }
+        }
+        const int rb32 = (int)row_bytes;
         float acc[NIT][NM];
 #pragma unroll
         for (int ib = 0; ib < NIT; ib++) {
@@ -409,7 +415,7 @@ __device__ __forceinline__ void stream_rows(const uint8_t *const (&w)[NM], int64
             for (int m = 0; m < NM; m++) {
                 float a = 0.f;
                 if (ok) {
-                    const uint8_t *rl = row_at(bi, m, row);
+                    const uint8_t *rl = ring + moff[m] + (row - r0) * rb32;
 #pragma unroll
                     for (int jg = 0; jg < NG; jg++) {
                         const int g = sub + geo.P * jg;

@@ -58,8 +58,8 @@ __device__ __forceinline__ void stage_quarter(const float (&v)[8], int q, bool v
 #pragma unroll
         for (int i = 0; i < 8; i++) mx = fmaxf(mx, fabsf(v[i]));
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+    mx = fmaxf(mx, lane_partner<1>(mx));
+    mx = fmaxf(mx, lane_partner<2>(mx));
     const float inv = mx > 0.f ? XQ_RANGE / mx : 0.f;
     uint32_t h[2], l[2];
     int s8 = 0;
@@ -78,8 +78,8 @@ __device__ __forceinline__ void stage_quarter(const float (&v)[8], int q, bool v
         h[w] = hw;
         l[w] = lw;
     }
-    int s32 = s8 + __shfl_xor(s8, 1, 64);
-    s32 = s32 + __shfl_xor(s32, 2, 64);
+    int s32 = s8 + __float_as_int(lane_partner<1>(__int_as_float(s8)));
+    s32 = s32 + __float_as_int(lane_partner<2>(__int_as_float(s32)));
     if (valid) {
         int8_t *xh = reinterpret_cast<int8_t *>(base);
         int8_t *xl = xh + k;
