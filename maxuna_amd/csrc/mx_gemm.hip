@@ -104,6 +104,62 @@ __device__ __forceinline__ void ubytes(uint32_t w, float *f) {
     for (int b = 0; b < 4; b++) f[b] = (float)((w >> (8 * b)) & 0xFFu);
 }
 
+// Packed-f16 dequantisation (MX_GEMM_PKDQ).  Bytes b < 1024 of two dwords become
+// the f16 numbers 1024 + b by placing them under the exponent byte 0x64
+// (v_perm_b32); the rest is v_pk_*_f16 arithmetic on small integers, exact
+// except where noted:
+//   K-quants with min (Q4_K, Q5_K): t = fma(1024 + q, sc, -1024 sc) = sc * q
+//     (exact: |sc * q| <= 63 * 31), y = fl16(fma(t, d, -fl16(dmin * m)))
+//   Q6_K: t = ((1024 + q) - 1056) * sc = sc * (q - 32) (exact while <= 2048 in
+//     magnitude), y = fl16(t * d)
+// d and dmin are the blocks' own f16 values, so against the f32 form (one f16
+// rounding of the f32 value) only fl16(dmin * m) adds an error.  About 1.5
+// VALU per weight instead of 3.
+#ifndef MX_GEMM_PKDQ
+#define MX_GEMM_PKDQ 1
+#endif
+__device__ __forceinline__ half2_t pk_bytes(uint32_t w, uint32_t sel) {
+    return __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, w, sel));
+}
+__device__ __forceinline__ void pk_bytes8(uint32_t w0, uint32_t w1, half2_t (&x)[4]) {
+    x[0] = pk_bytes(w0, 0x04010400u);  // bytes 0, 1
+    x[1] = pk_bytes(w0, 0x04030402u);  // bytes 2, 3
+    x[2] = pk_bytes(w1, 0x04010400u);
+    x[3] = pk_bytes(w1, 0x04030402u);
+}
+__device__ __forceinline__ half8_t pk_join(const half2_t (&y)[4]) {
+    half8_t r;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        r[2 * i] = y[i][0];
+        r[2 * i + 1] = y[i][1];
+    }
+    return r;
+}
+// sc2 = (sc, sc), d2 = (d, d), nm2 = -fl16(dmin * m) twice
+__device__ __forceinline__ half8_t dq8_kmin(uint32_t w0, uint32_t w1, half2_t sc2, half2_t d2, half2_t nm2) {
+    half2_t x[4], y[4];
+    pk_bytes8(w0, w1, x);
+    const half2_t nb = sc2 * half2_t{(_Float16)-1024.0f, (_Float16)-1024.0f};  // exact
+#pragma unroll
+    for (int i = 0; i < 4; i++) y[i] = __builtin_elementwise_fma(__builtin_elementwise_fma(x[i], sc2, nb), d2, nm2);
+    return pk_join(y);
+}
+__device__ __forceinline__ half8_t dq8_q6(uint32_t w0, uint32_t w1, half2_t sc2, half2_t d2) {
+    half2_t x[4], y[4];
+    pk_bytes8(w0, w1, x);
+#pragma unroll
+    for (int i = 0; i < 4; i++) y[i] = ((x[i] + half2_t{(_Float16)-1056.0f, (_Float16)-1056.0f}) * sc2) * d2;
+    return pk_join(y);
+}
+__device__ __forceinline__ half2_t h2splat(float v) {
+    const _Float16 h = (_Float16)v;
+    return half2_t{h, h};
+}
+__device__ __forceinline__ half2_t h2bits(uint32_t bits16) {
+    return __builtin_bit_cast(half2_t, (bits16 & 0xFFFFu) * 0x10001u);
+}
+
 // ---- per-type weight registers: one stage, one weight row, one lane half --------------
 template <int DT> struct WB;
 
@@ -119,16 +175,29 @@ template <> struct WB<kQ4_K> {
         q[0] = ld16(qs);
         q[1] = ld16(qs + 32);
     }
+#if MX_GEMM_PKDQ
+    half2_t sc2[4], m2[4], d2;
+#else
     float d[4], m[4];
+#endif
     template <int PAR> __device__ __forceinline__ void prep(int kh) {
         (void)kh;
-        const float dd = h2f((uint16_t)(h.x & 0xFFFFu)), dmin = h2f((uint16_t)(h.x >> 16));
+        [[maybe_unused]] const float dd = h2f((uint16_t)(h.x & 0xFFFFu));
+        const float dmin = h2f((uint16_t)(h.x >> 16));
+#if MX_GEMM_PKDQ
+        d2 = h2bits(h.x);
+#endif
 #pragma unroll
         for (int p = 0; p < 4; p++) {
             uint32_t sc, mn;
             q4k_scale_min(4 * PAR + p, h.y, h.z, h.w, sc, mn);
+#if MX_GEMM_PKDQ
+            sc2[p] = h2splat((float)sc);
+            m2[p] = h2splat(-(dmin * (float)mn));
+#else
             d[p] = dd * (float)sc;
             m[p] = dmin * (float)mn;
+#endif
         }
     }
     __device__ __forceinline__ half8_t step(int p, int hh) const {
@@ -136,12 +205,16 @@ template <> struct WB<kQ4_K> {
         const int sh = 4 * (p & 1);
         const uint32_t w0 = ((hh ? v.z : v.x) >> sh) & 0x0F0F0F0Fu;
         const uint32_t w1 = ((hh ? v.w : v.y) >> sh) & 0x0F0F0F0Fu;
+#if MX_GEMM_PKDQ
+        return dq8_kmin(w0, w1, sc2[p], d2, m2[p]);
+#else
         float f[8];
         ubytes(w0, f);
         ubytes(w1, f + 4);
 #pragma unroll
         for (int i = 0; i < 8; i++) f[i] = __builtin_fmaf(d[p], f[i], -m[p]);
         return pack8(f);
+#endif
     }
 };
 
@@ -157,17 +230,30 @@ template <> struct WB<kQ5_K> {
         q[0] = ld16(qs);
         q[1] = ld16(qs + 32);
     }
+#if MX_GEMM_PKDQ
+    half2_t sc2[4], m2[4], d2;
+#else
     float d[4], m[4];
+#endif
     int hsh;
     template <int PAR> __device__ __forceinline__ void prep(int kh) {
         (void)kh;
-        const float dd = h2f((uint16_t)(h.x & 0xFFFFu)), dmin = h2f((uint16_t)(h.x >> 16));
+        [[maybe_unused]] const float dd = h2f((uint16_t)(h.x & 0xFFFFu));
+        const float dmin = h2f((uint16_t)(h.x >> 16));
+#if MX_GEMM_PKDQ
+        d2 = h2bits(h.x);
+#endif
 #pragma unroll
         for (int p = 0; p < 4; p++) {
             uint32_t sc, mn;
             q4k_scale_min(4 * PAR + p, h.y, h.z, h.w, sc, mn);
+#if MX_GEMM_PKDQ
+            sc2[p] = h2splat((float)sc);
+            m2[p] = h2splat(-(dmin * (float)mn));
+#else
             d[p] = dd * (float)sc;
             m[p] = dmin * (float)mn;
+#endif
         }
         hsh = 4 * PAR;
     }
@@ -177,12 +263,16 @@ template <> struct WB<kQ5_K> {
         const uint32_t hb = hsh + p;
         const uint32_t w0 = (((hh ? v.z : v.x) >> sh) & 0x0F0F0F0Fu) | ((((hh ? qh.z : qh.x) >> hb) & 0x01010101u) << 4);
         const uint32_t w1 = (((hh ? v.w : v.y) >> sh) & 0x0F0F0F0Fu) | ((((hh ? qh.w : qh.y) >> hb) & 0x01010101u) << 4);
+#if MX_GEMM_PKDQ
+        return dq8_kmin(w0, w1, sc2[p], d2, m2[p]);
+#else
         float f[8];
         ubytes(w0, f);
         ubytes(w1, f + 4);
 #pragma unroll
         for (int i = 0; i < 8; i++) f[i] = __builtin_fmaf(d[p], f[i], -m[p]);
         return pack8(f);
+#endif
     }
 };
 
@@ -210,16 +300,28 @@ template <> struct WB<kQ6_K> {
         // every field of a block shares its 4-byte phase: the shift is a.sh
         dsh = (uint32_t)ld_u16(blk + 208) | (a.sh << 16);
     }
+#if MX_GEMM_PKDQ
+    half2_t sc2[4], d2;
+#else
     float ds[4];
+#endif
     template <int PAR> __device__ __forceinline__ void prep(int kh) {
         const float d = h2f((uint16_t)(dsh & 0xFFFFu));
         const uint32_t sh = dsh >> 16;
+#if MX_GEMM_PKDQ
+        d2 = h2bits(dsh);
+        (void)d;
+#endif
 #pragma unroll
         for (int p = 0; p < 4; p++) {
             const int j = 2 * p + kh;  // byte j of the stage's 8 scales
             const uint32_t word = j < 4 ? sc0 : sc1;
             const int8_t s8 = (int8_t)((word >> (8 * (j & 3))) & 0xFFu);
+#if MX_GEMM_PKDQ
+            sc2[p] = h2splat((float)s8);
+#else
             ds[p] = d * (float)s8;
+#endif
         }
         lo = fix16(Raw16{lo, lo_t, sh});
         hi = fix16(Raw16{hi, hi_t, sh});
@@ -232,6 +334,9 @@ template <> struct WB<kQ6_K> {
         const uint32_t a1 = ((hh ? ql.w : ql.y) >> shl) & 0x0F0F0F0Fu;
         const uint32_t b0 = (((hh ? qh.z : qh.x) >> shh) & 0x03030303u) << 4;
         const uint32_t b1 = (((hh ? qh.w : qh.y) >> shh) & 0x03030303u) << 4;
+#if MX_GEMM_PKDQ
+        return dq8_q6(a0 | b0, a1 | b1, sc2[p], d2);
+#else
         float f[8];
         ubytes(a0 | b0, f);
         ubytes(a1 | b1, f + 4);
@@ -239,6 +344,7 @@ template <> struct WB<kQ6_K> {
 #pragma unroll
         for (int i = 0; i < 8; i++) f[i] = __builtin_fmaf(ds[p], f[i], off);
         return pack8(f);
+#endif
     }
 };
 

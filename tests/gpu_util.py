@@ -39,6 +39,7 @@ def assert_close(got, want, rel=REL_L2, max_of_rms=MAX_ABS_OF_RMS, what=""):
     r = rel_l2(got, want)
     rms = float(np.sqrt((want ** 2).mean()))
     mx = float(np.abs(got - want).max()) if got.size else 0.0
+    print(f"{what}: rel-L2 {r:.3e}, max-abs/rms {mx / max(rms, 1e-30):.3e}", flush=True)
     assert r <= rel, f"{what}: rel-L2 {r:.3e} > {rel:.1e}"
     assert mx <= max_of_rms * rms + 1e-30, f"{what}: max-abs {mx:.3e} > {max_of_rms:.0e} * rms {rms:.3e}"
     return r, mx
