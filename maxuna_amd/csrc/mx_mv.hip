@@ -857,6 +857,112 @@ __global__ void __launch_bounds__(64 * WAVES_DN) __attribute__((amdgpu_waves_per
     if (threadIdx.x == 0) reset_counter(counter);
 }
 
+// ---- fused decode down, one workgroup per (token, row tile) holding every slot ---------
+// grid (hidden / RW_DN, t), 64 * slots threads: wave s stages slot s's act row into
+// its own LDS area and streams the slot's RW_DN down rows; the partial rows meet in
+// LDS and threads 0 .. RW_DN - 1 combine them in slot order, with the arithmetic of
+// k_decode_down's combine (combine.metal:70-97).  No partial rows in global
+// memory, no arrival counters, no cross-block tail.
+#ifndef MX_DN_SLOTS
+#define MX_DN_SLOTS 1
+#endif
+constexpr int DN_SLOTS_MAX = 12;  // 3 waves per SIMD: 168 VGPRs
+// row-iterations per DMA batch (NG > 1): 2 -> 8-row batches of Q6_K at ff = 1536
+#ifndef MX_NIT_DNS
+#define MX_NIT_DNS 2
+#endif
+template <int NG> struct BatchDnSlots { static constexpr int NIT = NG == 1 ? BatchDn<1>::NIT : MX_NIT_DNS; };
+constexpr int XPRE_W = 4;  // act quarters per lane held in registers before the weight copies
+template <int DT, int NG>
+__global__ void __launch_bounds__(64 * DN_SLOTS_MAX) k_decode_down_slots(DecodeDownArgs a, int ni) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    __shared__ float s_part[DN_SLOTS_MAX][RW_DN];
+    const int slots = a.top_k + (a.sh_down ? 1 : 0);
+    const int slot = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int tok = blockIdx.y;
+    const int r0 = blockIdx.x * RW_DN, r1 = min(r0 + RW_DN, a.hidden);
+    const int xs_bytes = (int)align16(xstage_bytes(a.ff));
+    uint8_t *xs_lds = lds + slot * (xs_bytes + RING_DN * ni * 1024);
+    uint8_t *ring = xs_lds + xs_bytes;
+    const float *xrow = a.act + ((int64_t)tok * slots + slot) * a.ff;
+    XPreT<XPRE_W> xp;
+    const uint8_t *wp;
+    int64_t rb;
+    if (slot < a.top_k) {
+        const uint32_t id = a.ids[tok * a.top_k + slot];
+        const int e = id < (uint32_t)a.n_expert ? (int)id : a.n_expert - 1;
+        wp = a.down + (int64_t)e * a.d_expert_bytes;
+        rb = a.d_row_bytes;
+    } else {
+        wp = a.sh_down;
+        rb = a.sh_row_bytes;
+    }
+    const uint8_t *const w[1] = {wp};
+    const Geo<DT> geo(a.ff, DN_FULL);
+    typename Q<DT>::X xs[NG];
+    stream_rows<DT, NG, BatchDnSlots<NG>::NIT, 1, RING_DN>(w, rb, geo, xs, r0, r1, ring, ni,
+                                                     [&] { stage_pre_t(xrow, a.ff, xp, lane, 64); },
+                                                     [&] {
+                                                         stage_post_t(xrow, a.ff, xp, xs_lds, lane, 64);
+                                                         load_xs<DT, NG>(xs_lds, a.ff, geo, xs);
+                                                     },
+                                                     [&](int row, const float (&v)[1]) { s_part[slot][row - r0] = v[0]; });
+    __syncthreads();
+    const int r = threadIdx.x;
+    if (r >= r1 - r0) return;
+    const int c = r0 + r;
+    const int64_t o = (int64_t)tok * a.hidden + c;
+    const float sh = a.sh_down ? s_part[a.top_k][r] : a.shared_out ? a.shared_out[o] : 0.f;
+    const float res = a.residual ? a.residual[o] : 0.f;
+    const float *wt = a.w + tok * a.top_k;
+    float v = 0.f;
+    for (int s = 0; s < a.top_k; s++) v = v + s_part[s][r] * wt[s];
+    if (a.sh_down || a.shared_out) v = v + sh;
+    if (a.residual) v = res + v;
+    a.out[o] = v;
+}
+
+template <int DT, int NG>
+static mx_status launch_dn_slots_ng(const DecodeDownArgs &a, hipStream_t s) {
+    const int ni = ring_insts<DT, NG>(1, a.ff, a.d_row_bytes, BatchDnSlots<NG>::NIT, DN_FULL);
+    if (ni > DMA_MAX_INSTS) return fail(MX_ERR_SHAPE, "decode down: rows too long for the LDS ring");
+    const int slots = a.top_k + (a.sh_down ? 1 : 0);
+    const size_t lds = (size_t)slots * (align16(xstage_bytes(a.ff)) + (size_t)RING_DN * ni * 1024);
+    const dim3 grid((unsigned)((a.hidden + RW_DN - 1) / RW_DN), (unsigned)a.t);
+    hipLaunchKernelGGL((k_decode_down_slots<DT, NG>), grid, dim3(64 * slots), lds, s, a, ni);
+    return MX_OK;
+}
+// LDS bytes of the slot-per-wave kernel (SIZE_MAX: its DMA batch does not fit)
+template <int DT, int NG>
+static size_t dn_slots_lds(const DecodeDownArgs &a) {
+    const int ni = ring_insts<DT, NG>(1, a.ff, a.d_row_bytes, BatchDnSlots<NG>::NIT, DN_FULL);
+    if (ni > DMA_MAX_INSTS) return SIZE_MAX;
+    const int slots = a.top_k + (a.sh_down ? 1 : 0);
+    return (size_t)slots * (align16(xstage_bytes(a.ff)) + (size_t)RING_DN * ni * 1024);
+}
+// true when the slot-per-wave kernel takes this launch
+template <int DT>
+static bool dn_slots_fit(const DecodeDownArgs &a) {
+    if (!MX_DN_SLOTS || a.order) return false;
+    if (a.top_k + (a.sh_down ? 1 : 0) > DN_SLOTS_MAX) return false;
+    const int ng = ng_variant(Geo<DT>(a.ff, DN_FULL).NG);
+    size_t lds = SIZE_MAX;
+    [&] {
+#define MX_L(N) { lds = dn_slots_lds<DT, N>(a); return; }
+        MX_NG_SWITCH(ng, MX_L)
+#undef MX_L
+    }();
+    return lds <= 160 * 1024 - sizeof(float) * DN_SLOTS_MAX * RW_DN;
+}
+template <int DT>
+static mx_status launch_dn_slots_dt(const DecodeDownArgs &a, hipStream_t s) {
+    const int ng = ng_variant(Geo<DT>(a.ff, DN_FULL).NG);
+#define MX_L(N) return launch_dn_slots_ng<DT, N>(a, s)
+    MX_NG_SWITCH(ng, MX_L)
+#undef MX_L
+    return MX_OK;
+}
+
 template <int DT, int NG>
 static mx_status launch_dn_ng(const DecodeDownArgs &a, dim3 grid, hipStream_t s) {
     const int ni = ring_insts<DT, NG>(1, a.ff, a.d_row_bytes, BatchDn<NG>::NIT, DN_FULL);
@@ -888,6 +994,23 @@ mx_status launch_decode_down(int dtype, const DecodeDownArgs &a, hipStream_t s) 
     if (a.ff % 32) return fail(MX_ERR_BLOCK, "decode down: expert_ff must be a multiple of 32");
     if (a.sh_down && a.sh_row_bytes != a.d_row_bytes)
         return fail(MX_ERR_SHAPE, "decode down: shared expert rows must match the routed rows");
+    bool slots_kernel = false;
+    switch (dtype) {
+    case kQ4_K: slots_kernel = dn_slots_fit<kQ4_K>(a); break;
+    case kQ5_K: slots_kernel = dn_slots_fit<kQ5_K>(a); break;
+    case kQ6_K: slots_kernel = dn_slots_fit<kQ6_K>(a); break;
+    default: slots_kernel = dn_slots_fit<kQ8_0>(a); break;
+    }
+    if (slots_kernel) {
+        switch (dtype) {
+        case kQ4_K: MX_TRY(launch_dn_slots_dt<kQ4_K>(a, s)); break;
+        case kQ5_K: MX_TRY(launch_dn_slots_dt<kQ5_K>(a, s)); break;
+        case kQ6_K: MX_TRY(launch_dn_slots_dt<kQ6_K>(a, s)); break;
+        default: MX_TRY(launch_dn_slots_dt<kQ8_0>(a, s)); break;
+        }
+        MX_LAUNCH("k_decode_down_slots");
+        return MX_OK;
+    }
     switch (dtype) {
     case kQ4_K: MX_TRY(launch_dn_dt<kQ4_K>(a, grid, s)); break;
     case kQ5_K: MX_TRY(launch_dn_dt<kQ5_K>(a, grid, s)); break;

@@ -122,33 +122,45 @@ __device__ __forceinline__ void load8f(const float *p, float (&v)[8]) {
 // quantises them (and any beyond XPRE, loading on the fly), then a block barrier.
 // Every thread of the block must call both.
 constexpr int XPRE = 2;
-struct XPre {
-    float v[XPRE][8];
+template <int NP> struct XPreT {
+    float v[NP][8];
 };
-__device__ __forceinline__ void stage_pre(const float *__restrict__ x, int k, XPre &p) {
+using XPre = XPreT<XPRE>;
+// Staging by a group of nth threads (thread tid of them): quarters tid + nth * i.
+template <int NP>
+__device__ __forceinline__ void stage_pre_t(const float *__restrict__ x, int k, XPreT<NP> &p, int tid, int nth) {
     const int nq = k / 8;
 #pragma unroll
-    for (int i = 0; i < XPRE; i++) {
-        const int q = threadIdx.x + blockDim.x * i;
+    for (int i = 0; i < NP; i++) {
+        const int q = tid + nth * i;
         if (q < nq) load8f(x + 8 * q, p.v[i]);
     }
 }
-__device__ __forceinline__ void stage_post(const float *__restrict__ x, int k, const XPre &p, uint8_t *lds) {
+// nth must be a multiple of 4 and uniform over the group; no barrier
+template <int NP>
+__device__ __forceinline__ void stage_post_t(const float *__restrict__ x, int k, const XPreT<NP> &p, uint8_t *lds,
+                                             int tid, int nth) {
     const int nq = k / 8;
-    const int iters = (nq + (int)blockDim.x - 1) / (int)blockDim.x;  // block-uniform
+    const int iters = (nq + nth - 1) / nth;  // group-uniform
 #pragma unroll
-    for (int i = 0; i < XPRE; i++) {
+    for (int i = 0; i < NP; i++) {
         if (i < iters) {
-            const int q = threadIdx.x + blockDim.x * i;
+            const int q = tid + nth * i;
             stage_quarter(p.v[i], q, q < nq, lds, k);
         }
     }
-    for (int i = XPRE; i < iters; i++) {
-        const int q = threadIdx.x + blockDim.x * i;
+    for (int i = NP; i < iters; i++) {
+        const int q = tid + nth * i;
         float v[8];
         if (q < nq) load8f(x + 8 * q, v);
         stage_quarter(v, q, q < nq, lds, k);
     }
+}
+__device__ __forceinline__ void stage_pre(const float *__restrict__ x, int k, XPre &p) {
+    stage_pre_t(x, k, p, (int)threadIdx.x, (int)blockDim.x);
+}
+__device__ __forceinline__ void stage_post(const float *__restrict__ x, int k, const XPre &p, uint8_t *lds) {
+    stage_post_t(x, k, p, lds, (int)threadIdx.x, (int)blockDim.x);
     __syncthreads();
 }
 
