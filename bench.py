@@ -169,17 +169,15 @@ def bench_decode(args):
     eb_gu = 2 * spec.ff * (spec.hidden // 256) * 144
     eb_dn = spec.hidden * (spec.ff // 256) * 210
     k = spec.top_k
-    sh_bytes = eb_gu + spec.hidden * 4
-    gu_bytes = k * eb_gu + spec.hidden * 4
+    gu_bytes = (k + 1) * eb_gu + spec.hidden * 4  # routed + shared gate/up
     dn_bytes = (k + 1) * eb_dn + (k + 1) * spec.ff * 4 + spec.hidden * 4
-    kern = {"k_decode_gate_up (shared + top-k)": (st[1], sh_bytes), "k_decode_gate_up (routed)": (st[2], gu_bytes),
-            "k_decode_down": (st[3], dn_bytes)}
+    kern = {"k_decode_gate_up (routed + shared)": (st[2], gu_bytes), "k_decode_down": (st[3], dn_bytes)}
     dom = max(kern, key=lambda n: kern[n][0])
     dms, dbytes = kern[dom]
     roof = {"bound": "hbm", "kernel": dom, "achieved": round(dbytes / (dms * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(dbytes / (dms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "traffic": measured_traffic().get(dom), "bytes_per_launch": dbytes, "launch_us": round(dms * 1e3, 2)}
-    stage_us = {"route_logits": st[0] * 1e3, "select_shared_gate_up": st[1] * 1e3, "gate_up": st[2] * 1e3,
+    stage_us = {"route_logits": st[0] * 1e3, "topk": st[1] * 1e3, "gate_up": st[2] * 1e3,
                 "down": st[3] * 1e3, "eager_events": [round(v * 1e3, 2) for v in eager]}
     return dict(ms_per_step=ms, steps=steps, gbs=gbs, bytes_per_step=bytes_per_step, uniq=uniq,
                 stage_us=stage_us, roofline=roof,

@@ -8,6 +8,12 @@
 #include "mx_launch.h"
 #include "mx_stage.h"
 
+// decode: the shared expert's gate/up rides in the top-k launch (1) or with the
+// routed slots (0)
+#ifndef MX_SHARED_WITH_SELECT
+#define MX_SHARED_WITH_SELECT 0
+#endif
+
 namespace mx {
 
 static thread_local char g_err[512] = "";
@@ -528,10 +534,17 @@ mx_status moe_forward_impl(const mx_moe_layer *L, const float *x, int64_t t, con
             DecodeSelArgs sel{reinterpret_cast<const uint64_t *>(keys),
                               reinterpret_cast<const float *>(keys + (size_t)t * E * sizeof(uint64_t)), (int)E,
                               (int)t, scale, apply, L->weights_norm, ids, w};
+#if MX_SHARED_WITH_SELECT
             for (int r = 0; r < rep(1); r++)
                 MX_TRY(launch_decode_gate_up(L->gate.dtype, ga, (int)K, shf ? 1 : 0, &sel, s));
             MX_STAGE();
             for (int r = 0; r < rep(2); r++) MX_TRY(launch_decode_gate_up(L->gate.dtype, ga, 0, (int)K, nullptr, s));
+#else
+            for (int r = 0; r < rep(1); r++) MX_TRY(launch_decode_gate_up(L->gate.dtype, ga, (int)K, 0, &sel, s));
+            MX_STAGE();
+            for (int r = 0; r < rep(2); r++)
+                MX_TRY(launch_decode_gate_up(L->gate.dtype, ga, 0, (int)K + (shf ? 1 : 0), nullptr, s));
+#endif
         } else {
             MX_STAGE();
             MX_TRY(launch_decode_gate_up(L->gate.dtype, ga, 0, (int)K + (shf ? 1 : 0), nullptr, s));
