@@ -43,11 +43,12 @@ __device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }
 
-// DMA instructions for a batch of `rows` rows of `row_bytes` of nm matrices
-// (worst-case alignment: one extra chunk per matrix span)
+// DMA instructions for a batch of `rows` rows of `row_bytes` of nm matrices:
+// each matrix's span gets its own instructions (worst-case alignment: one extra
+// chunk per span)
 __host__ __device__ inline int dma_insts(int nm, int rows, int64_t row_bytes) {
-    const int64_t chunks = nm * ((rows * row_bytes + 15) / 16 + 1);
-    return (int)((chunks + 63) / 64);
+    const int64_t chunks = (rows * row_bytes + 15) / 16 + 1;  // per matrix
+    return nm * (int)((chunks + 63) / 64);
 }
 constexpr int DMA_MAX_INSTS = 15;  // per batch (vmcnt budget of the waits, up to 2 batches ahead)
 
@@ -376,17 +377,15 @@ __device__ __forceinline__ void stream_rows(const uint8_t *const (&w)[NM], int64
         int nch[NM];
 #pragma unroll
         for (int m = 0; m < NM; m++) span(m, r0, base[m], nch[m]);
-        int tot = 0;
-#pragma unroll
-        for (int m = 0; m < NM; m++) tot += nch[m];
         uint8_t *dst = ring + (bi % RING) * bstride;
-        for (int j = 0; j < ni; j++) {
-            int ci = min(64 * j + lane, tot - 1);  // spare lanes re-copy the last chunk
-            uintptr_t src = base[0] + 16 * (uintptr_t)ci;
-            if (NM > 1) {
-                if (ci >= nch[0]) src = base[1] + 16 * (uintptr_t)(ci - nch[0]);
+        const int per = ni / NM;  // instructions per matrix span
+#pragma unroll
+        for (int m = 0; m < NM; m++) {
+            const uint8_t *b = reinterpret_cast<const uint8_t *>(base[m]);
+            for (int q = 0; q < per; q++) {
+                const int ci = min(64 * q + lane, nch[m] - 1);  // spare lanes re-copy the last chunk
+                dma16(b + (uint32_t)(16 * ci), dst + 1024 * (m * per + q));
             }
-            dma16(reinterpret_cast<const uint8_t *>(src), dst + 1024 * j);
         }
     };
     auto process = [&](int bi) {
@@ -401,7 +400,7 @@ __device__ __forceinline__ void stream_rows(const uint8_t *const (&w)[NM], int64
             moff[0] = (bi % RING) * bstride + (int)(reinterpret_cast<uintptr_t>(w[0] + (int64_t)r0 * row_bytes) - base0);
             if (NM > 1) {
                 span(1, r0, base1, n1);
-                moff[NM - 1] = (bi % RING) * bstride + 16 * n0 +
+                moff[NM - 1] = (bi % RING) * bstride + 1024 * (ni / NM) +
                                (int)(reinterpret_cast<uintptr_t>(w[NM - 1] + (int64_t)r0 * row_bytes) - base1);
             }
         }
@@ -558,7 +557,7 @@ __global__ void __launch_bounds__(64 * WAVES) k_mul_mv_id(MvArgs a, int ni) {
     }
     const float *xrow = a.x + ((int64_t)tok * a.x_per_row + (a.x_per_row == 1 ? 0 : slot)) * a.k;
     const uint8_t *const w[1] = {a.w + (int64_t)e * a.expert_bytes};
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (scalar)
     const int r0 = blockIdx.x * (WAVES * RW_MV) + wave * RW_MV;
     const Geo<DT> geo(a.k);
     typename Q<DT>::X xs[NG];
@@ -661,12 +660,16 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
         tile = bid / npair;
         tok = pair / slots;
         slot = pair % slots;
+    } else if (sel.n_sel == 0) {  // grid (tiles, nslot, t)
+        tile = blockIdx.x;
+        slot = slot0 + blockIdx.y;
+        tok = blockIdx.z;
     } else {
         tile = bid % tiles;
         slot = slot0 + (bid / tiles) % nslot;
         tok = bid / (tiles * nslot);
     }
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (scalar)
     const int r0 = tile * (WAVES * RW_GU) + wave * RW_GU;
     if (r0 >= a.ff) return;  // wave-uniform; no block barrier below
     float *act = a.act + ((int64_t)tok * slots + slot) * a.ff;
@@ -705,6 +708,8 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
 template <int DT, int NG>
 static mx_status launch_gu_ng(const DecodeGateUpArgs &a, unsigned blocks, int slot0, int nslot,
                               const DecodeSelArgs &sel, hipStream_t s) {
+    const unsigned tiles = (unsigned)((a.ff + WAVES * RW_GU - 1) / (WAVES * RW_GU));
+    const dim3 grid = (sel.n_sel == 0 && !a.order) ? dim3(tiles, (unsigned)nslot, (unsigned)a.t) : dim3(blocks);
     constexpr bool GM_OK = DT == kQ4_K || DT == kQ5_K;
     const int ni = ring_insts<DT, NG>(2, a.hidden, a.gu_row_bytes);
     if (ni > DMA_MAX_INSTS) return fail(MX_ERR_SHAPE, "decode gate/up: rows too long for the LDS ring");
@@ -712,11 +717,9 @@ static mx_status launch_gu_ng(const DecodeGateUpArgs &a, unsigned blocks, int sl
     if (sel.n_sel && lds < sizeof(SelShared)) lds = sizeof(SelShared);
     if (lds > 160 * 1024) return fail(MX_ERR_SHAPE, "decode gate/up: hidden = %d needs %zu bytes of LDS", a.hidden, lds);
     if (GM_OK && a.xstage_gm)
-        hipLaunchKernelGGL((k_decode_gate_up<DT, NG, GM_OK>), dim3(blocks), dim3(64 * WAVES), lds, s, a, ni, slot0, nslot,
-                           sel);
+        hipLaunchKernelGGL((k_decode_gate_up<DT, NG, GM_OK>), grid, dim3(64 * WAVES), lds, s, a, ni, slot0, nslot, sel);
     else
-        hipLaunchKernelGGL((k_decode_gate_up<DT, NG, false>), dim3(blocks), dim3(64 * WAVES), lds, s, a, ni, slot0,
-                           nslot, sel);
+        hipLaunchKernelGGL((k_decode_gate_up<DT, NG, false>), grid, dim3(64 * WAVES), lds, s, a, ni, slot0, nslot, sel);
     return MX_OK;
 }
 
@@ -787,7 +790,7 @@ __global__ void __launch_bounds__(64 * WAVES_DN) __attribute__((amdgpu_waves_per
     }
     constexpr int ROWS_PER_WG = WAVES_DN * RW_DN;
     const int tile0 = tile * ROWS_PER_WG;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (scalar)
     const int r0 = tile0 + wave * RW_DN;
     const float *xrow = a.act + ((int64_t)tok * slots + slot) * a.ff;
     uint8_t *ring = lds + align16(xstage_bytes(a.ff)) + wave * (RING_DN * ni * 1024);
@@ -878,7 +881,7 @@ __global__ void __launch_bounds__(64 * DN_SLOTS_MAX) k_decode_down_slots(DecodeD
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     __shared__ float s_part[DN_SLOTS_MAX][RW_DN];
     const int slots = a.top_k + (a.sh_down ? 1 : 0);
-    const int slot = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int slot = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int tok = blockIdx.y;
     const int r0 = blockIdx.x * RW_DN, r1 = min(r0 + RW_DN, a.hidden);
     const int xs_bytes = (int)align16(xstage_bytes(a.ff));
