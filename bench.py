@@ -211,6 +211,7 @@ def bench_prefill(args):
     st = np.array([profiled(layer.block, x, out, t) for _ in range(3)]).mean(0)
     names = ["route", "map0", "x_f16", "gate_up_gemm", "act_f16", "down_gemm", "combine"]
     stage_us = {n: round(v * 1e3, 1) for n, v in zip(names, st)}
+    log("prefill stage us (eager events): " + ", ".join(f"{n} {v}" for n, v in stage_us.items()))
     kk = spec.top_k + (1 if spec.shared else 0)
     gu_flops = 2 * 2 * t * kk * spec.ff * spec.hidden
     dn_flops = 2 * t * kk * spec.hidden * spec.ff

@@ -25,52 +25,87 @@ size_t map0_bytes(int n_expert, int t, int top_k) {
     return (size_t)MapLayout(n_expert, t, top_k).words * 4;
 }
 
-// chunk histogram: cnt[c][e] = pairs of chunk c routed to e; flags duplicates.
+// Flags of a chunk (duplicate id within a token: 1, out-of-range id: 2) ride in
+// bits 28-29 of the chunk's expert-0 count; the scan folds them into the dup word.
+constexpr int BK_FLAG_SHIFT = 28;
+constexpr int32_t BK_COUNT_MASK = (1 << BK_FLAG_SHIFT) - 1;
+
+// Copies the chunk's ids into LDS (the duplicate checks then read LDS).
+__device__ __forceinline__ void stage_chunk_ids(const uint32_t *__restrict__ ids, int tok0, int n, int top_k,
+                                                uint32_t *s_ids) {
+    for (int i = threadIdx.x; i < n; i += blockDim.x) s_ids[i] = ids[(int64_t)tok0 * top_k + i];
+}
+// true when slot `slot` of row `row` is the first slot of its token with this id
+__device__ __forceinline__ bool first_of_token(const uint32_t *row, int slot, uint32_t id) {
+    bool first = true;
+    for (int s2 = 0; s2 < slot; s2++) first = first && (row[s2] != id);
+    return first;
+}
+
+// chunk histogram: cnt[c][e] = pairs of chunk c routed to e, plus the chunk's flags.
 __global__ void __launch_bounds__(256) k_bucket_count(const uint32_t *__restrict__ ids, int t,
                                                       int top_k, int n_expert,
                                                       int32_t *__restrict__ map) {
-    extern __shared__ int32_t s_hist[];
+    extern __shared__ int32_t s_hist[];  // [n_expert] counts | [BK_CHUNK * top_k] ids
+    __shared__ int s_flag;
+    uint32_t *s_ids = reinterpret_cast<uint32_t *>(s_hist + n_expert);
     const MapLayout L(n_expert, t, top_k);
     const int c = blockIdx.x, tid = threadIdx.x;
-    for (int e = tid; e < n_expert; e += 256) s_hist[e] = 0;
-    __syncthreads();
     const int tok0 = c * BK_CHUNK;
     const int ntok = min(BK_CHUNK, t - tok0);
+    for (int e = tid; e < n_expert; e += 256) s_hist[e] = 0;
+    if (tid == 0) s_flag = 0;
+    stage_chunk_ids(ids, tok0, ntok * top_k, top_k, s_ids);
+    __syncthreads();
+    int flag = 0;
     for (int i = tid; i < ntok * top_k; i += 256) {
-        const uint32_t id = ids[(int64_t)tok0 * top_k + i];
-        const int slot = i % top_k;
-        const uint32_t *row = ids + (int64_t)(tok0 + i / top_k) * top_k;
-        bool first = true;  // a token counts once per expert (the fill collapses repeats)
-        for (int s2 = 0; s2 < slot; s2++) first = first && (row[s2] != id);
-        if (!first) atomicOr(&map[L.dup], 1);  // duplicate id within a token
-        if (id >= (uint32_t)n_expert) atomicOr(&map[L.dup], 2);  // out-of-range id: dropped
+        const uint32_t id = s_ids[i];
+        const bool first = first_of_token(s_ids + (i / top_k) * top_k, i % top_k, id);  // a token counts once per expert
+        if (!first) flag |= 1;
+        if (id >= (uint32_t)n_expert) flag |= 2;  // out-of-range id: dropped
         else if (first) atomicAdd(&s_hist[id], 1);
     }
+    if (flag) atomicOr(&s_flag, flag);
     __syncthreads();
-    for (int e = tid; e < n_expert; e += 256) map[L.chunk + (int64_t)c * n_expert + e] = s_hist[e];
+    for (int e = tid; e < n_expert; e += 256)
+        map[L.chunk + (int64_t)c * n_expert + e] = s_hist[e] | (e == 0 ? s_flag << BK_FLAG_SHIFT : 0);
 }
 
-// per-expert scan over chunks, expert offsets, tile list.  One block of 1024.
+// per-expert scan over chunks, expert offsets, tile list, dup word.  One block of
+// 1024; also the whole header when t == 0 (no chunks).
 __global__ void __launch_bounds__(1024) k_bucket_scan(int t, int top_k, int n_expert, int bm,
                                                       int32_t *__restrict__ map) {
     __shared__ int32_t s_a[1024], s_b[1024];
+    __shared__ int s_flag;
     const MapLayout L(n_expert, t, top_k);
     const int tid = threadIdx.x;
+    if (tid == 0) s_flag = 0;
+    __syncthreads();
     const int per = (n_expert + 1023) / 1024;
     const int e0 = min(tid * per, n_expert), e1 = min(e0 + per, n_expert);
-    int sum_pairs = 0, sum_tiles = 0;
+    int sum_pairs = 0, sum_tiles = 0, flag = 0;
+    constexpr int CB = 16;  // chunk counts loaded together (independent loads in flight)
     for (int e = e0; e < e1; e++) {
         int run = 0;
-        for (int64_t c = 0; c < L.nchunks; c++) {
-            int32_t *p = map + L.chunk + c * n_expert + e;
-            const int v = *p;
-            *p = run;  // exclusive prefix within the expert
-            run += v;
+        int32_t *p = map + L.chunk + e;
+        for (int64_t c0 = 0; c0 < L.nchunks; c0 += CB) {
+            int32_t v[CB];
+#pragma unroll
+            for (int i = 0; i < CB; i++) v[i] = c0 + i < L.nchunks ? p[(c0 + i) * n_expert] : 0;
+#pragma unroll
+            for (int i = 0; i < CB; i++) {
+                if (c0 + i < L.nchunks) {
+                    flag |= v[i] >> BK_FLAG_SHIFT;
+                    p[(c0 + i) * n_expert] = run;  // exclusive prefix within the expert
+                    run += v[i] & BK_COUNT_MASK;
+                }
+            }
         }
         map[L.tpe + e] = run;
         sum_pairs += run;
         sum_tiles += (run + bm - 1) / bm;
     }
+    if (flag) atomicOr(&s_flag, flag);
     // block exclusive scan of (pairs, tiles) over threads
     s_a[tid] = sum_pairs;
     s_b[tid] = sum_tiles;
@@ -94,6 +129,7 @@ __global__ void __launch_bounds__(1024) k_bucket_scan(int t, int top_k, int n_ex
     if (tid == 1023) {
         map[L.off + n_expert] = s_a[1023];
         map[L.n_tiles] = s_b[1023];
+        map[L.dup] = s_flag;
     }
 }
 
@@ -103,21 +139,23 @@ __global__ void __launch_bounds__(256) k_bucket_fill(const uint32_t *__restrict_
                                                      int32_t *__restrict__ map) {
     // s_slot[tt * n_expert + e]: the first slot of token tt that picked expert e
     // (0xFF: none), so each expert's thread walks the chunk's tokens in order
-    // with one LDS byte per token
+    // with one LDS byte per token; the chunk's ids follow the table
     extern __shared__ uint8_t s_slot[];
+    const int table = BK_CHUNK * ((n_expert + 3) & ~3);
+    uint32_t *s_ids = reinterpret_cast<uint32_t *>(s_slot + table);
     const MapLayout L(n_expert, t, top_k);
     const int c = blockIdx.x, tid = threadIdx.x;
     const int tok0 = c * BK_CHUNK;
     const int ntok = min(BK_CHUNK, t - tok0);
     uint32_t *w32 = reinterpret_cast<uint32_t *>(s_slot);
-    for (int i = tid; i < BK_CHUNK * n_expert / 4; i += 256) w32[i] = 0xFFFFFFFFu;
+    for (int i = tid; i < table / 4; i += 256) w32[i] = 0xFFFFFFFFu;
+    stage_chunk_ids(ids, tok0, ntok * top_k, top_k, s_ids);
     __syncthreads();
     for (int i = tid; i < ntok * top_k; i += 256) {
-        const uint32_t *row = ids + (int64_t)(tok0 + i / top_k) * top_k;
         const int slot = i % top_k;
-        const uint32_t id = row[slot];
-        bool first = id < (uint32_t)n_expert;  // out-of-range ids are dropped (flagged by the count pass)
-        for (int s2 = 0; s2 < slot; s2++) first = first && (row[s2] != id);
+        const uint32_t id = s_ids[i];
+        // out-of-range ids are dropped (flagged by the count pass)
+        const bool first = id < (uint32_t)n_expert && first_of_token(s_ids + (i / top_k) * top_k, slot, id);
         if (first) s_slot[(i / top_k) * n_expert + id] = (uint8_t)slot;  // one writer per (token, expert)
     }
     __syncthreads();
@@ -155,27 +193,20 @@ __global__ void __launch_bounds__(256) k_bucket_fill_scan(const uint32_t *__rest
     }
 }
 
-// Clears words [0, n) with a kernel (no memset node: callers may capture this
-// stream into a HIP graph).
-__global__ void k_zero_words(int32_t *__restrict__ p, int64_t n) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) p[i] = 0;
-}
-
 mx_status launch_map0(const uint32_t *ids, int t, int top_k, int n_expert, int32_t *map,
                       hipStream_t s, int bm) {
     const MapLayout L(n_expert, t, top_k);
-    // header (tpe, off, n_tiles, dup) starts at zero; the passes below fill it
-    hipLaunchKernelGGL(k_zero_words, dim3((unsigned)((L.tiles + 255) / 256)), dim3(256), 0, s, map,
-                       L.tiles);
-    MX_LAUNCH("k_zero_words");
-    if (t == 0) return MX_OK;
-    hipLaunchKernelGGL(k_bucket_count, dim3((unsigned)L.nchunks), dim3(256), n_expert * 4, s, ids, t,
-                       top_k, n_expert, map);
-    MX_LAUNCH("k_bucket_count");
+    const size_t ids_lds = (size_t)BK_CHUNK * top_k * 4;
+    if (t > 0) {
+        hipLaunchKernelGGL(k_bucket_count, dim3((unsigned)L.nchunks), dim3(256), n_expert * 4 + ids_lds, s, ids, t,
+                           top_k, n_expert, map);
+        MX_LAUNCH("k_bucket_count");
+    }
+    // writes the whole header (tpe, off, n_tiles, dup), also for t == 0
     hipLaunchKernelGGL(k_bucket_scan, dim3(1), dim3(1024), 0, s, t, top_k, n_expert, bm, map);
     MX_LAUNCH("k_bucket_scan");
-    const size_t slot_lds = (size_t)BK_CHUNK * ((n_expert + 3) & ~3);
+    if (t == 0) return MX_OK;
+    const size_t slot_lds = (size_t)BK_CHUNK * ((n_expert + 3) & ~3) + ids_lds;
     if (slot_lds <= 96 * 1024) {
         hipLaunchKernelGGL(k_bucket_fill, dim3((unsigned)L.nchunks), dim3(256), slot_lds, s, ids, t, top_k,
                            n_expert, map);
