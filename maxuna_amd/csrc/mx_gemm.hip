@@ -167,6 +167,7 @@ template <int DT> struct WB;
 // Lane half kh holds qs bytes [32 i + 16 kh, +16) of both chunks; step p = 2c + nib
 // uses the low (nib 0) or high nibbles, sub-block 2 i + nib (mm_id.metal:95-113).
 template <> struct WB<kQ4_K> {
+    static constexpr int kMinLoads = 3;  // memory instructions load() always issues: header + 2 quant pieces
     uint4 h, q[2];
     __device__ __forceinline__ void load(const uint8_t *row, int ks, int kh) {
         const uint8_t *blk = row + (ks >> 1) * 144;
@@ -221,6 +222,7 @@ template <> struct WB<kQ4_K> {
 // Q5_K: Q4_K's stage layout (qs at byte 48) plus lane half kh's 16 bytes of qh;
 // step p of half `par` adds bit 4 par + p of qh[l] as the fifth bit (mm_id.metal:113-134).
 template <> struct WB<kQ5_K> {
+    static constexpr int kMinLoads = 4;  // memory instructions load() always issues: header + qh + 2 quant pieces
     uint4 h, q[2], qh;
     __device__ __forceinline__ void load(const uint8_t *row, int ks, int kh) {
         const uint8_t *blk = row + (ks >> 1) * 176;
@@ -281,6 +283,7 @@ template <> struct WB<kQ5_K> {
 // step p takes the 4-bit part from the low (p even) / high (p odd) ql piece,
 // nibble p / 2, and bits 2p of qh; scale 8n + 2p + kh (mm_id.metal:115-135).
 template <> struct WB<kQ6_K> {
+    static constexpr int kMinLoads = 4;  // memory instructions load() always issues: 3 pieces + d (tails and scale words only add)
     // raw bytes, realigned in place by prep(): ql low piece, ql high piece, qh
     uint4 lo, hi, qh;
     uint32_t lo_t, hi_t, qh_t;  // the dword after each piece (2-byte aligned blocks)
@@ -350,6 +353,7 @@ template <> struct WB<kQ6_K> {
 
 // Q8_0: stage = blocks 4 ks + p; lane half kh holds quants [16 kh, +16) of each.
 template <> struct WB<kQ8_0> {
+    static constexpr int kMinLoads = 8;  // memory instructions load() always issues: 4 x (piece + d)
     Raw16 q[4];
     uint16_t dh[4];
     __device__ __forceinline__ void load(const uint8_t *row, int ks, int kh) {
@@ -383,6 +387,11 @@ template <> struct WB<kQ8_0> {
         return pack8(f);
     }
 };
+
+// leave the next stage's weight loads outstanding across the stage barrier
+#ifndef MX_GEMM_WSLACK
+#define MX_GEMM_WSLACK 1
+#endif
 
 struct Tile {
     int e, pos0, mrows, nt;
@@ -521,7 +530,10 @@ __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
 #pragma unroll
         for (int nb = 0; nb < NB; nb++) w0[nb].template prep<0>(kh);
         compute(sA[0], w0);
-        wait_vmcnt(0);
+        // the A copy was issued before the weight loads: all but the last
+        // NB * kMinLoads memory operations done covers it (the weights are
+        // waited for where they are first used)
+        wait_vmcnt(MX_GEMM_WSLACK ? NB * WB<DT>::kMinLoads : 0);
         __syncthreads();
         if (ks + 2 < nks) {
             issue_a(ks + 2, sA[0]);
@@ -531,7 +543,7 @@ __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
 #pragma unroll
         for (int nb = 0; nb < NB; nb++) w1[nb].template prep<1>(kh);
         compute(sA[1], w1);
-        wait_vmcnt(0);
+        wait_vmcnt(MX_GEMM_WSLACK && ks + 2 < nks ? NB * WB<DT>::kMinLoads : 0);
         __syncthreads();
     }
 
