@@ -559,7 +559,11 @@ __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
             if constexpr (SWIGLU) {
                 if (col[0] < a.n_out) {
                     const float g = acc[mb][0][r] * sc, u = acc[mb][1][r] * sc;
-                    orow[col[0]] = g / (1.0f + expf(-g)) * u;  // silu(g) * u (silu_mul.metal:57-72)
+                    // silu(g) * u (silu_mul.metal:57-72) on the hardware exp2 and
+                    // reciprocal (about 1 ulp each): the act row is rounded to f16
+                    // for the down GEMM, far above these errors
+                    const float e = __builtin_amdgcn_exp2f(-g * 1.4426950408889634f);  // exp(-g)
+                    orow[col[0]] = g * __builtin_amdgcn_rcpf(1.0f + e) * u;
                 }
             } else {
 #pragma unroll
