@@ -366,6 +366,7 @@ def main():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-decode", action="store_true", help="prefill only (profiling); prints no JSON line")
     ap.add_argument("--no-extra", action="store_true", help="skip the C2 verify, C4 chain and lm_head figures")
+    ap.add_argument("--no-chain", action="store_true", help="skip the C4 chain and lm_head figures (keep C2)")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="only run N device-to-device copies of this many MB (HBM counter calibration) and exit")
     args = ap.parse_args()
@@ -394,7 +395,7 @@ def main():
     pre = None if args.no_prefill else bench_prefill(args)
     cpu = None if args.no_cpu_baseline else cpu_baseline(args, dec)
     extra = {}
-    if not args.no_extra:
+    if not args.no_extra and not args.no_chain:
         extra["lm_head"] = bench_lm_head(args)
         del dec["layers"]
         torch.cuda.empty_cache()

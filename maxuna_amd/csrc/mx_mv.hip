@@ -869,6 +869,9 @@ __global__ void __launch_bounds__(64 * WAVES_DN) __attribute__((amdgpu_waves_per
 #ifndef MX_DN_SLOTS
 #define MX_DN_SLOTS 1
 #endif
+#ifndef MX_DN_SLOTS_MAX_T
+#define MX_DN_SLOTS_MAX_T 4  // above this, more and smaller blocks (k_decode_down) keep the CUs fuller
+#endif
 constexpr int DN_SLOTS_MAX = 12;  // 3 waves per SIMD: 168 VGPRs
 // row-iterations per DMA batch (NG > 1): 2 -> 8-row batches of Q6_K at ff = 1536
 #ifndef MX_NIT_DNS
@@ -946,7 +949,7 @@ static size_t dn_slots_lds(const DecodeDownArgs &a) {
 // true when the slot-per-wave kernel takes this launch
 template <int DT>
 static bool dn_slots_fit(const DecodeDownArgs &a) {
-    if (!MX_DN_SLOTS || a.order) return false;
+    if (!MX_DN_SLOTS || a.order || a.t > MX_DN_SLOTS_MAX_T) return false;
     if (a.top_k + (a.sh_down ? 1 : 0) > DN_SLOTS_MAX) return false;
     const int ng = ng_variant(Geo<DT>(a.ff, DN_FULL).NG);
     size_t lds = SIZE_MAX;
