@@ -58,7 +58,7 @@ def test_decode_layer(dev, orc, name):
         oracle_check(orc, layer, x, out, ids, w, f"{name} seed={seed}", max_flips=0)
 
 
-@pytest.mark.parametrize("t", [2, 5, 16, 31])
+@pytest.mark.parametrize("t", [2, 4, 5, 16, 31])
 def test_verify_block(dev, orc, t):
     """C2: speculative verify blocks below MM_ID_MIN_SEQ (decode kernels, (token,
     slot) pairs walked in expert order)."""
@@ -126,16 +126,17 @@ def test_prefill_full_size_mm_vs_decode_and_sample(dev, orc):
 
 @pytest.mark.parametrize("gate_dt,down_dt", [(GgmlDType.Q8_0, GgmlDType.Q8_0), (GgmlDType.Q6_K, GgmlDType.Q4_K),
                                              (GgmlDType.Q4_K, GgmlDType.Q8_0)], ids=["q8q8", "q6q4", "q4q8"])
-def test_prefill_weight_types(dev, orc, gate_dt, down_dt):
-    """Grouped GEMM (t = 160: the shared expert's pairs span two m-tiles, one
-    partial) with every weight type in both the SwiGLU gate/up and the plain down
-    GEMM."""
+def test_weight_types(dev, orc, gate_dt, down_dt):
+    """Every weight type in both matrices: decode at t = 1 (per-slot down
+    workgroups) and the grouped GEMM at t = 160 (the shared expert's pairs span
+    two m-tiles, one partial; SwiGLU gate/up and plain down GEMM)."""
     spec = LayerSpec(768, 512, 32, 4, gate_dt, down_dt, shared=True)
     layer = build_layer(spec, seed=1040 + int(gate_dt) + int(down_dt))
-    _log(f"prefill {gate_dt.name}/{down_dt.name} t=160")
-    x = make_x(spec, 41, 160)
-    out, ids, w = run_block(layer, x)
-    oracle_check(orc, layer, x, out, ids, w, f"{gate_dt.name}/{down_dt.name} t=160", max_flips=1)
+    for t in (1, 160):
+        _log(f"{gate_dt.name}/{down_dt.name} t={t}")
+        x = make_x(spec, 41 + t, t)
+        out, ids, w = run_block(layer, x)
+        oracle_check(orc, layer, x, out, ids, w, f"{gate_dt.name}/{down_dt.name} t={t}", max_flips=1)
 
 
 @pytest.mark.parametrize("gate_dt,down_dt", [(GgmlDType.Q5_K, GgmlDType.Q5_K), (GgmlDType.Q5_K, GgmlDType.Q6_K),
