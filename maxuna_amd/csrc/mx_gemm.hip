@@ -434,7 +434,11 @@ __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
     constexpr int NB = GemmNb<DT, SWIGLU>::nb;
     constexpr int NWAVE = GemmNb<DT, SWIGLU>::waves;
     constexpr int DMA_PER_WAVE = STAGE_BYTES / 1024 / NWAVE;
-    __shared__ __attribute__((aligned(1024))) uint8_t sA[2][STAGE_BYTES];
+    // two separate LDS objects (not one 2-D array): the compiler can then tell
+    // that a copy into one buffer does not feed reads of the other, and does
+    // not wait for the next stage's copies before this stage's reads
+    __shared__ __attribute__((aligned(1024))) uint8_t sA0[STAGE_BYTES];
+    __shared__ __attribute__((aligned(1024))) uint8_t sA1[STAGE_BYTES];
     __shared__ int64_t s_src[GM_BM];  // byte offset of the A row
     __shared__ float s_scale[GM_BM];
     __shared__ int s_out[GM_BM];      // output row
@@ -518,32 +522,36 @@ __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
 
     WB<DT> w0[NB], w1[NB];
     const int nks = a.k / KS;  // even
-    issue_a(0, sA[0]);
+    issue_a(0, sA0);
 #pragma unroll
     for (int nb = 0; nb < NB; nb++) w0[nb].load(wrow[nb], 0, kh);
     wait_vmcnt(0);
     __syncthreads();
     for (int ks = 0; ks < nks; ks += 2) {
-        issue_a(ks + 1, sA[1]);
+        issue_a(ks + 1, sA1);
 #pragma unroll
         for (int nb = 0; nb < NB; nb++) w1[nb].load(wrow[nb], ks + 1, kh);
 #pragma unroll
         for (int nb = 0; nb < NB; nb++) w0[nb].template prep<0>(kh);
-        compute(sA[0], w0);
+        compute(sA0, w0);
         // the A copy was issued before the weight loads: all but the last
         // NB * kMinLoads memory operations done covers it (the weights are
         // waited for where they are first used)
         wait_vmcnt(MX_GEMM_WSLACK ? NB * WB<DT>::kMinLoads : 0);
         __syncthreads();
-        if (ks + 2 < nks) {
-            issue_a(ks + 2, sA[0]);
+        {
+            // unconditional, clamped at the last stage (a harmless re-copy into
+            // the buffer nobody reads next): no branch merge in front of the
+            // next waits, so the compiler keeps exact memory counters
+            const int kn = min(ks + 2, nks - 1);
+            issue_a(kn, sA0);
 #pragma unroll
-            for (int nb = 0; nb < NB; nb++) w0[nb].load(wrow[nb], ks + 2, kh);
+            for (int nb = 0; nb < NB; nb++) w0[nb].load(wrow[nb], kn, kh);
         }
 #pragma unroll
         for (int nb = 0; nb < NB; nb++) w1[nb].template prep<1>(kh);
-        compute(sA[1], w1);
-        wait_vmcnt(MX_GEMM_WSLACK && ks + 2 < nks ? NB * WB<DT>::kMinLoads : 0);
+        compute(sA1, w1);
+        wait_vmcnt(MX_GEMM_WSLACK ? NB * WB<DT>::kMinLoads : 0);
         __syncthreads();
     }
 
