@@ -169,15 +169,15 @@ template <int DT> struct WB;
 template <> struct WB<kQ4_K> {
     static constexpr int kMinLoads = 3;  // memory instructions load() always issues: header + 2 quant pieces
     uint4 h, q[2];
-    __device__ __forceinline__ void load(const uint8_t *row, int ks, int kh) {
-        const uint8_t *blk = row + (ks >> 1) * 144;
+    __device__ __forceinline__ void load(const uint8_t *base, uint32_t row, int ks, int kh) {
+        const uint8_t *blk = base + (row + (uint32_t)(ks >> 1) * 144u);
         h = ld16(blk);
         const uint8_t *qs = blk + 16 + 64 * (ks & 1) + 16 * kh;
         q[0] = ld16(qs);
         q[1] = ld16(qs + 32);
     }
 #if MX_GEMM_PKDQ
-    half2_t sc2[4], m2[4], d2;
+    half2_t scm[4], d2;  // (sc, -fl16(dmin * m)) of each sub-block, packed
 #else
     float d[4], m[4];
 #endif
@@ -193,8 +193,7 @@ template <> struct WB<kQ4_K> {
             uint32_t sc, mn;
             q4k_scale_min(4 * PAR + p, h.y, h.z, h.w, sc, mn);
 #if MX_GEMM_PKDQ
-            sc2[p] = h2splat((float)sc);
-            m2[p] = h2splat(-(dmin * (float)mn));
+            scm[p] = half2_t{(_Float16)(float)sc, (_Float16)(-(dmin * (float)mn))};
 #else
             d[p] = dd * (float)sc;
             m[p] = dmin * (float)mn;
@@ -207,7 +206,7 @@ template <> struct WB<kQ4_K> {
         const uint32_t w0 = ((hh ? v.z : v.x) >> sh) & 0x0F0F0F0Fu;
         const uint32_t w1 = ((hh ? v.w : v.y) >> sh) & 0x0F0F0F0Fu;
 #if MX_GEMM_PKDQ
-        return dq8_kmin(w0, w1, sc2[p], d2, m2[p]);
+        return dq8_kmin(w0, w1, half2_t{scm[p][0], scm[p][0]}, d2, half2_t{scm[p][1], scm[p][1]});
 #else
         float f[8];
         ubytes(w0, f);
@@ -224,8 +223,8 @@ template <> struct WB<kQ4_K> {
 template <> struct WB<kQ5_K> {
     static constexpr int kMinLoads = 4;  // memory instructions load() always issues: header + qh + 2 quant pieces
     uint4 h, q[2], qh;
-    __device__ __forceinline__ void load(const uint8_t *row, int ks, int kh) {
-        const uint8_t *blk = row + (ks >> 1) * 176;
+    __device__ __forceinline__ void load(const uint8_t *base, uint32_t row, int ks, int kh) {
+        const uint8_t *blk = base + (row + (uint32_t)(ks >> 1) * 176u);
         h = ld16(blk);
         qh = ld16(blk + 16 + 16 * kh);
         const uint8_t *qs = blk + 48 + 64 * (ks & 1) + 16 * kh;
@@ -233,7 +232,7 @@ template <> struct WB<kQ5_K> {
         q[1] = ld16(qs + 32);
     }
 #if MX_GEMM_PKDQ
-    half2_t sc2[4], m2[4], d2;
+    half2_t scm[4], d2;  // (sc, -fl16(dmin * m)) of each sub-block, packed
 #else
     float d[4], m[4];
 #endif
@@ -250,8 +249,7 @@ template <> struct WB<kQ5_K> {
             uint32_t sc, mn;
             q4k_scale_min(4 * PAR + p, h.y, h.z, h.w, sc, mn);
 #if MX_GEMM_PKDQ
-            sc2[p] = h2splat((float)sc);
-            m2[p] = h2splat(-(dmin * (float)mn));
+            scm[p] = half2_t{(_Float16)(float)sc, (_Float16)(-(dmin * (float)mn))};
 #else
             d[p] = dd * (float)sc;
             m[p] = dmin * (float)mn;
@@ -266,7 +264,7 @@ template <> struct WB<kQ5_K> {
         const uint32_t w0 = (((hh ? v.z : v.x) >> sh) & 0x0F0F0F0Fu) | ((((hh ? qh.z : qh.x) >> hb) & 0x01010101u) << 4);
         const uint32_t w1 = (((hh ? v.w : v.y) >> sh) & 0x0F0F0F0Fu) | ((((hh ? qh.w : qh.y) >> hb) & 0x01010101u) << 4);
 #if MX_GEMM_PKDQ
-        return dq8_kmin(w0, w1, sc2[p], d2, m2[p]);
+        return dq8_kmin(w0, w1, half2_t{scm[p][0], scm[p][0]}, d2, half2_t{scm[p][1], scm[p][1]});
 #else
         float f[8];
         ubytes(w0, f);
@@ -288,8 +286,8 @@ template <> struct WB<kQ6_K> {
     uint4 lo, hi, qh;
     uint32_t lo_t, hi_t, qh_t;  // the dword after each piece (2-byte aligned blocks)
     uint32_t sc0, sc1, dsh;     // scale dwords covering scales[8n .. 8n+7]; d and the shift
-    __device__ __forceinline__ void load(const uint8_t *row, int ks, int kh) {
-        const uint8_t *blk = row + (int64_t)(ks >> 1) * 210;
+    __device__ __forceinline__ void load(const uint8_t *base, uint32_t row, int ks, int kh) {
+        const uint8_t *blk = base + (row + (uint32_t)(ks >> 1) * 210u);
         const int n = ks & 1;
         const Raw16 a = ld16_a2(blk + 64 * n + 16 * kh);
         const Raw16 b = ld16_a2(blk + 64 * n + 32 + 16 * kh);
@@ -356,10 +354,10 @@ template <> struct WB<kQ8_0> {
     static constexpr int kMinLoads = 8;  // memory instructions load() always issues: 4 x (piece + d)
     Raw16 q[4];
     uint16_t dh[4];
-    __device__ __forceinline__ void load(const uint8_t *row, int ks, int kh) {
+    __device__ __forceinline__ void load(const uint8_t *base, uint32_t row, int ks, int kh) {
 #pragma unroll
         for (int p = 0; p < 4; p++) {
-            const uint8_t *blk = row + (int64_t)(4 * ks + p) * 34;
+            const uint8_t *blk = base + (row + (uint32_t)(4 * ks + p) * 34u);
             q[p] = ld16_a2(blk + 2 + 16 * kh);
             dh[p] = ld_u16(blk);
         }
@@ -392,6 +390,17 @@ template <> struct WB<kQ8_0> {
 #ifndef MX_GEMM_WSLACK
 #define MX_GEMM_WSLACK 1
 #endif
+
+// Makes the compiler wait for every register of `v` here (an empty asm that
+// reads them).  Placed before a stage's A copies, the wait then covers weight
+// loads only: the compiler's counters cannot order weight loads against LDS
+// copies issued after them and would otherwise wait for everything.
+template <class T> __device__ __forceinline__ void touch_regs(const T &v) {
+    static_assert(sizeof(T) % 4 == 0, "touch_regs: whole dwords");
+    const uint32_t *w = reinterpret_cast<const uint32_t *>(&v);
+#pragma unroll
+    for (int i = 0; i < (int)(sizeof(T) / 4); i++) asm volatile("" ::"v"(w[i]));
+}
 
 struct Tile {
     int e, pos0, mrows, nt;
@@ -439,7 +448,7 @@ __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
     // not wait for the next stage's copies before this stage's reads
     __shared__ __attribute__((aligned(1024))) uint8_t sA0[STAGE_BYTES];
     __shared__ __attribute__((aligned(1024))) uint8_t sA1[STAGE_BYTES];
-    __shared__ int64_t s_src[GM_BM];  // byte offset of the A row
+    __shared__ uint32_t s_src[GM_BM];  // byte offset of the A row from the tile's first row
     __shared__ float s_scale[GM_BM];
     __shared__ int s_out[GM_BM];      // output row
     constexpr int NCOL = SWIGLU ? BN / 2 : BN;
@@ -455,7 +464,10 @@ __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
             const int pos = tl.pos0 + r;
             const int pair = a.map[L.list + pos];
             const int64_t arow = a.a_by_token ? pair / a.top_k : pos;
-            s_src[tid] = arow * a.k * 2;
+            // rows ascend within a tile (tokens ascend within a bucket), so the
+            // offsets from the first row stay below (t or GM_BM) * k * 2 bytes
+            const int64_t arow0 = a.a_by_token ? a.map[L.list + tl.pos0] / a.top_k : tl.pos0;
+            s_src[tid] = (uint32_t)((arow - arow0) * a.k * 2);
             s_scale[tid] = a.a_scale[arow];
             s_out[tid] = SWIGLU ? pos : pair / a.top_k * a.out_stride + pair % a.top_k + a.out_add;
         }
@@ -465,17 +477,21 @@ __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
     // this lane's two weight rows (one per 32-column MFMA block)
     const bool shared = tl.e >= a.n_expert;
     const int64_t rb = shared ? a.sh_row_bytes : a.row_bytes;
-    const uint8_t *wrow[NB];
+    const uint8_t *wbase[NB];  // wave-uniform expert base
+    uint32_t wrow[NB];         // this lane's row offset from it (the launcher checks it fits)
     int col[NB];
 #pragma unroll
     for (int nb = 0; nb < NB; nb++) {
         const int m = SWIGLU ? nb : 0;
         const uint8_t *base = shared ? a.w_sh[m] : a.w[m] + (int64_t)tl.e * a.expert_bytes;
         col[nb] = SWIGLU ? tl.nt * NCOL + wave * 32 + j : tl.nt * NCOL + wave * 32 * NB + nb * 32 + j;
-        wrow[nb] = base + (int64_t)min(col[nb], a.n_out - 1) * rb;
+        wbase[nb] = base;
+        wrow[nb] = (uint32_t)(min(col[nb], a.n_out - 1) * rb);
     }
 
-    const uint8_t *abase = reinterpret_cast<const uint8_t *>(a.a);
+    const MapLayout L0(a.n_map_expert, a.t, a.top_k);
+    const int64_t arow0 = a.a_by_token ? a.map[L0.list + tl.pos0] / a.top_k : tl.pos0;
+    const uint8_t *abase = reinterpret_cast<const uint8_t *>(a.a) + arow0 * a.k * 2;  // tile's first A row
     // A stage copy: wave instruction i fills LDS rows 4 (8 wave + i) + lane / 16
     auto issue_a = [&](int ks, uint8_t *buf) {
 #pragma unroll
@@ -483,8 +499,12 @@ __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
             const int inst = DMA_PER_WAVE * wave + i;
             const int row = 4 * inst + (lane >> 4);
             const int c = (lane & 15) ^ (row & 15);
-            dma16(abase + s_src[row] + ks * ROWB + c * 16, buf + inst * 1024);
+            dma16(abase + (s_src[row] + (uint32_t)(ks * ROWB + c * 16)), buf + inst * 1024);
         }
+        // keep the copies at the start of the stage: without this the compiler
+        // sinks them behind the stage's LDS reads (the buffers are separate
+        // objects), which leaves the copy no time to land before the barrier
+        asm volatile("" ::: "memory");
     };
 
     // per-lane LDS offsets of the A operand for the 8 steps of a stage
@@ -524,21 +544,30 @@ __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
     const int nks = a.k / KS;  // even
     issue_a(0, sA0);
 #pragma unroll
-    for (int nb = 0; nb < NB; nb++) w0[nb].load(wrow[nb], 0, kh);
+    for (int nb = 0; nb < NB; nb++) w0[nb].load(wbase[nb], wrow[nb], 0, kh);
     wait_vmcnt(0);
     __syncthreads();
+    // Each stage: prep the weights loaded one stage ago, issue the next
+    // stage's A copy and weight loads, compute.  Stage ends wait for the A copy
+    // only and use a bare s_barrier: the copies are complete (vmcnt) and LDS
+    // needs no further fence between the waves of a workgroup.
+    auto stage_end = [&] {
+        wait_vmcnt(MX_GEMM_WSLACK ? NB * WB<DT>::kMinLoads : 0);
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+    };
     for (int ks = 0; ks < nks; ks += 2) {
+#pragma unroll
+        for (int nb = 0; nb < NB; nb++) touch_regs(w0[nb]);
         issue_a(ks + 1, sA1);
 #pragma unroll
-        for (int nb = 0; nb < NB; nb++) w1[nb].load(wrow[nb], ks + 1, kh);
+        for (int nb = 0; nb < NB; nb++) w1[nb].load(wbase[nb], wrow[nb], ks + 1, kh);
 #pragma unroll
         for (int nb = 0; nb < NB; nb++) w0[nb].template prep<0>(kh);
         compute(sA0, w0);
-        // the A copy was issued before the weight loads: all but the last
-        // NB * kMinLoads memory operations done covers it (the weights are
-        // waited for where they are first used)
-        wait_vmcnt(MX_GEMM_WSLACK ? NB * WB<DT>::kMinLoads : 0);
-        __syncthreads();
+        stage_end();
+#pragma unroll
+        for (int nb = 0; nb < NB; nb++) touch_regs(w1[nb]);
         {
             // unconditional, clamped at the last stage (a harmless re-copy into
             // the buffer nobody reads next): no branch merge in front of the
@@ -546,14 +575,14 @@ __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
             const int kn = min(ks + 2, nks - 1);
             issue_a(kn, sA0);
 #pragma unroll
-            for (int nb = 0; nb < NB; nb++) w0[nb].load(wrow[nb], kn, kh);
+            for (int nb = 0; nb < NB; nb++) w0[nb].load(wbase[nb], wrow[nb], kn, kh);
         }
 #pragma unroll
         for (int nb = 0; nb < NB; nb++) w1[nb].template prep<1>(kh);
         compute(sA1, w1);
-        wait_vmcnt(MX_GEMM_WSLACK ? NB * WB<DT>::kMinLoads : 0);
-        __syncthreads();
+        stage_end();
     }
+    __syncthreads();
 
     // epilogue: acc[mb][nb][r] = D[row 32 mb + 8 (r / 4) + 4 kh + r % 4][col[nb]]
 #pragma unroll
@@ -665,6 +694,12 @@ mx_status launch_gemm(int dtype, bool swiglu, const GemmArgs &a, hipStream_t s) 
     const int ncol = swiglu ? 128 : 256;
     const int64_t nt = (a.n_out + ncol - 1) / ncol;
     const int64_t t_max = ((int64_t)a.t * a.top_k + GM_BM - 1) / GM_BM + a.n_map_expert;  // m-tiles of GM_BM
+    // the kernel addresses a tile's A rows from its first row, and one expert's
+    // weight rows from the expert, with 32-bit offsets
+    const int64_t a_span = a.a_by_token ? a.t : GM_BM;
+    if (a_span * a.k * 2 >= (INT64_C(1) << 32) ||
+        (int64_t)a.n_out * (a.row_bytes > a.sh_row_bytes ? a.row_bytes : a.sh_row_bytes) >= (INT64_C(1) << 32))
+        return fail(MX_ERR_OVERFLOW, "gemm: an operand span beyond 4 GiB (t * k * 2 bytes of x); split the batch");
     const int64_t blocks = (t_max * nt + 7) / 8 * 8;
     if (blocks > INT32_MAX) return fail(MX_ERR_OVERFLOW, "gemm: too many tiles");
     const dim3 grid((unsigned)blocks);
