@@ -53,9 +53,17 @@ constexpr int BN = 256;  // weight rows (output columns) per block
 #ifndef MX_GEMM_NB_PLAIN
 #define MX_GEMM_NB_PLAIN 1
 #endif
+// waves of the NB = 2 (SwiGLU, Q4_K) tiles: 4 (256 weight rows, two workgroups
+// per CU) or 8 (512 rows, one workgroup per CU at the same 2 waves per SIMD:
+// each A tile is gathered once for twice the columns)
+#ifndef MX_GEMM_WAVES2
+#define MX_GEMM_WAVES2 8
+#endif
 template <int DT, bool SWIGLU> struct GemmNb {
     static constexpr int nb = (SWIGLU || DT == kQ4_K) ? 2 : MX_GEMM_NB_PLAIN;
-    static constexpr int waves = BN / (32 * nb);
+    // (Q6_K / Q8_0 SwiGLU keep 4 waves: at 8 a workgroup caps them at 256 VGPRs)
+    static constexpr int waves = nb == 2 ? ((DT == kQ4_K || DT == kQ5_K) ? MX_GEMM_WAVES2 : 4) : BN / (32 * nb);
+    static constexpr int bn = waves * 32 * nb;  // weight rows per workgroup
 };
 
 typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
@@ -451,7 +459,7 @@ __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
     __shared__ uint32_t s_src[GM_BM];  // byte offset of the A row from the tile's first row
     __shared__ float s_scale[GM_BM];
     __shared__ int s_out[GM_BM];      // output row
-    constexpr int NCOL = SWIGLU ? BN / 2 : BN;
+    constexpr int NCOL = SWIGLU ? GemmNb<DT, SWIGLU>::bn / 2 : GemmNb<DT, SWIGLU>::bn;
     const int nt_count = (a.n_out + NCOL - 1) / NCOL;
     Tile tl;
     if (!tile_of(a, nt_count, tl)) return;
@@ -691,7 +699,13 @@ bool gemm_supported(int dtype, int k) {
 mx_status launch_gemm(int dtype, bool swiglu, const GemmArgs &a, hipStream_t s) {
     if (a.t == 0) return MX_OK;
     const MapLayout L(a.n_map_expert, a.t, a.top_k);
-    const int ncol = swiglu ? 128 : 256;
+    int ncol = 256;
+    switch (dtype) {  // output columns per workgroup of the instantiation launched below
+    case kQ4_K: ncol = swiglu ? GemmNb<kQ4_K, true>::bn / 2 : GemmNb<kQ4_K, false>::bn; break;
+    case kQ5_K: ncol = swiglu ? GemmNb<kQ5_K, true>::bn / 2 : GemmNb<kQ5_K, false>::bn; break;
+    case kQ6_K: ncol = swiglu ? GemmNb<kQ6_K, true>::bn / 2 : GemmNb<kQ6_K, false>::bn; break;
+    default: ncol = swiglu ? GemmNb<kQ8_0, true>::bn / 2 : GemmNb<kQ8_0, false>::bn; break;
+    }
     const int64_t nt = (a.n_out + ncol - 1) / ncol;
     const int64_t t_max = ((int64_t)a.t * a.top_k + GM_BM - 1) / GM_BM + a.n_map_expert;  // m-tiles of GM_BM
     // the kernel addresses a tile's A rows from its first row, and one expert's
