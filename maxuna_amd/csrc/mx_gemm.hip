@@ -177,7 +177,7 @@ template <int DT> struct WB;
 template <> struct WB<kQ4_K> {
     static constexpr int kMinLoads = 3;  // memory instructions load() always issues: header + 2 quant pieces
     uint4 h, q[2];
-    __device__ __forceinline__ void load(const uint8_t *base, uint32_t row, int ks, int kh) {
+    __device__ __forceinline__ void load(const uint8_t *base, __amdgpu_buffer_rsrc_t rs, uint32_t row, int ks, int kh) {
         const uint8_t *blk = base + (row + (uint32_t)(ks >> 1) * 144u);
         h = ld16(blk);
         const uint8_t *qs = blk + 16 + 64 * (ks & 1) + 16 * kh;
@@ -231,7 +231,7 @@ template <> struct WB<kQ4_K> {
 template <> struct WB<kQ5_K> {
     static constexpr int kMinLoads = 4;  // memory instructions load() always issues: header + qh + 2 quant pieces
     uint4 h, q[2], qh;
-    __device__ __forceinline__ void load(const uint8_t *base, uint32_t row, int ks, int kh) {
+    __device__ __forceinline__ void load(const uint8_t *base, __amdgpu_buffer_rsrc_t rs, uint32_t row, int ks, int kh) {
         const uint8_t *blk = base + (row + (uint32_t)(ks >> 1) * 176u);
         h = ld16(blk);
         qh = ld16(blk + 16 + 16 * kh);
@@ -289,25 +289,33 @@ template <> struct WB<kQ5_K> {
 // step p takes the 4-bit part from the low (p even) / high (p odd) ql piece,
 // nibble p / 2, and bits 2p of qh; scale 8n + 2p + kh (mm_id.metal:115-135).
 template <> struct WB<kQ6_K> {
-    static constexpr int kMinLoads = 4;  // memory instructions load() always issues: 3 pieces + d (tails and scale words only add)
+    static constexpr int kMinLoads = 11;  // buffer loads load() issues: 3 x (piece + next dword) + 3 scale words + d
     // raw bytes, realigned in place by prep(): ql low piece, ql high piece, qh
     uint4 lo, hi, qh;
     uint32_t lo_t, hi_t, qh_t;  // the dword after each piece (2-byte aligned blocks)
-    uint32_t sc0, sc1, dsh;     // scale dwords covering scales[8n .. 8n+7]; d and the shift
-    __device__ __forceinline__ void load(const uint8_t *base, uint32_t row, int ks, int kh) {
-        const uint8_t *blk = base + (row + (uint32_t)(ks >> 1) * 210u);
+    uint32_t sc0, sc1, sc2w, dsh;  // 3 dwords covering scales[8n .. 8n+7]; d and the shift
+    // Buffer loads through the expert's resource: every word is loaded whatever
+    // the block's 4-byte phase (no branches, so exact wait counts), and the
+    // words past the end of the expert's rows read 0 instead of faulting.
+    __device__ __forceinline__ void load(const uint8_t *base, __amdgpu_buffer_rsrc_t rs, uint32_t row, int ks, int kh) {
+        const uint32_t blk = row + (uint32_t)(ks >> 1) * 210u;  // byte offset in the expert
         const int n = ks & 1;
-        const Raw16 a = ld16_a2(blk + 64 * n + 16 * kh);
-        const Raw16 b = ld16_a2(blk + 64 * n + 32 + 16 * kh);
-        const Raw16 c = ld16_a2(blk + 128 + 32 * n + 16 * kh);
-        lo = a.v; lo_t = a.tail;
-        hi = b.v; hi_t = b.tail;
-        qh = c.v; qh_t = c.tail;
-        const uint2 sc = load8_a2(blk + 192 + 8 * n);
-        sc0 = sc.x;
-        sc1 = sc.y;
-        // every field of a block shares its 4-byte phase: the shift is a.sh
-        dsh = (uint32_t)ld_u16(blk + 208) | (a.sh << 16);
+        auto piece = [&](uint32_t off, uint4 &v, uint32_t &t) {
+            const uint32_t al = off & ~3u;
+            const auto q = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)al, 0, 0);
+            v = make_uint4(q[0], q[1], q[2], q[3]);
+            t = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(al + 16), 0, 0);
+        };
+        piece(blk + 64 * n + 16 * kh, lo, lo_t);
+        piece(blk + 64 * n + 32 + 16 * kh, hi, hi_t);
+        piece(blk + 128 + 32 * n + 16 * kh, qh, qh_t);
+        const uint32_t sa = (blk + 192 + 8 * n) & ~3u;
+        sc0 = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)sa, 0, 0);
+        sc1 = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(sa + 4), 0, 0);
+        sc2w = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(sa + 8), 0, 0);
+        // every field of a block shares its 4-byte phase
+        const uint32_t sh = (uint32_t)((reinterpret_cast<uintptr_t>(base) + blk) & 2) * 8;
+        dsh = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, (int)(blk + 208), 0, 0) | (sh << 16);
     }
 #if MX_GEMM_PKDQ
     half2_t sc2[4], d2;
@@ -321,10 +329,11 @@ template <> struct WB<kQ6_K> {
         d2 = h2bits(dsh);
         (void)d;
 #endif
+        const uint32_t s0 = __builtin_amdgcn_alignbit(sc1, sc0, sh), s1 = __builtin_amdgcn_alignbit(sc2w, sc1, sh);
 #pragma unroll
         for (int p = 0; p < 4; p++) {
             const int j = 2 * p + kh;  // byte j of the stage's 8 scales
-            const uint32_t word = j < 4 ? sc0 : sc1;
+            const uint32_t word = j < 4 ? s0 : s1;
             const int8_t s8 = (int8_t)((word >> (8 * (j & 3))) & 0xFFu);
 #if MX_GEMM_PKDQ
             sc2[p] = h2splat((float)s8);
@@ -362,7 +371,7 @@ template <> struct WB<kQ8_0> {
     static constexpr int kMinLoads = 8;  // memory instructions load() always issues: 4 x (piece + d)
     Raw16 q[4];
     uint16_t dh[4];
-    __device__ __forceinline__ void load(const uint8_t *base, uint32_t row, int ks, int kh) {
+    __device__ __forceinline__ void load(const uint8_t *base, __amdgpu_buffer_rsrc_t rs, uint32_t row, int ks, int kh) {
 #pragma unroll
         for (int p = 0; p < 4; p++) {
             const uint8_t *blk = base + (row + (uint32_t)(4 * ks + p) * 34u);
@@ -394,6 +403,9 @@ template <> struct WB<kQ8_0> {
     }
 };
 
+#ifndef MX_GEMM_PIN_W
+#define MX_GEMM_PIN_W 1
+#endif
 // leave the next stage's weight loads outstanding across the stage barrier
 #ifndef MX_GEMM_WSLACK
 #define MX_GEMM_WSLACK 1
@@ -403,11 +415,14 @@ template <> struct WB<kQ8_0> {
 // reads them).  Placed before a stage's A copies, the wait then covers weight
 // loads only: the compiler's counters cannot order weight loads against LDS
 // copies issued after them and would otherwise wait for everything.
-template <class T> __device__ __forceinline__ void touch_regs(const T &v) {
+// The operands are in-out, so nothing computed from `v` can be hoisted above
+// this point either (the compiler would otherwise start the next stage's prep
+// inside this stage and wait for the loads just issued).
+template <class T> __device__ __forceinline__ void touch_regs(T &v) {
     static_assert(sizeof(T) % 4 == 0, "touch_regs: whole dwords");
-    const uint32_t *w = reinterpret_cast<const uint32_t *>(&v);
+    uint32_t *w = reinterpret_cast<uint32_t *>(&v);
 #pragma unroll
-    for (int i = 0; i < (int)(sizeof(T) / 4); i++) asm volatile("" ::"v"(w[i]));
+    for (int i = 0; i < (int)(sizeof(T) / 4); i++) asm volatile("" : "+v"(w[i]));
 }
 
 struct Tile {
@@ -486,6 +501,7 @@ __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
     const bool shared = tl.e >= a.n_expert;
     const int64_t rb = shared ? a.sh_row_bytes : a.row_bytes;
     const uint8_t *wbase[NB];  // wave-uniform expert base
+    __amdgpu_buffer_rsrc_t wres[NB];  // the expert's rows as a buffer (range-checked loads)
     uint32_t wrow[NB];         // this lane's row offset from it (the launcher checks it fits)
     int col[NB];
 #pragma unroll
@@ -494,6 +510,8 @@ __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
         const uint8_t *base = shared ? a.w_sh[m] : a.w[m] + (int64_t)tl.e * a.expert_bytes;
         col[nb] = SWIGLU ? tl.nt * NCOL + wave * 32 + j : tl.nt * NCOL + wave * 32 * NB + nb * 32 + j;
         wbase[nb] = base;
+        wres[nb] = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(base), (short)0, (int)(a.n_out * rb),
+                                                     0x00020000);
         wrow[nb] = (uint32_t)(min(col[nb], a.n_out - 1) * rb);
     }
 
@@ -552,13 +570,20 @@ __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
     const int nks = a.k / KS;  // even
     issue_a(0, sA0);
 #pragma unroll
-    for (int nb = 0; nb < NB; nb++) w0[nb].load(wbase[nb], wrow[nb], 0, kh);
+    for (int nb = 0; nb < NB; nb++) w0[nb].load(wbase[nb], wres[nb], wrow[nb], 0, kh);
     wait_vmcnt(0);
     __syncthreads();
     // Each stage: prep the weights loaded one stage ago, issue the next
     // stage's A copy and weight loads, compute.  Stage ends wait for the A copy
     // only and use a bare s_barrier: the copies are complete (vmcnt) and LDS
     // needs no further fence between the waves of a workgroup.
+    // One-column tiles (NB = 1) have the registers to hold the next stage's
+    // weights through the compute: keep their loads at the stage start (the
+    // compiler would sink them next to their use).  The two-column tiles
+    // would spill, so their loads stay where the compiler puts them.
+    auto pin_weight_loads = [] {
+        if constexpr (NB == 1 && MX_GEMM_PIN_W) asm volatile("" ::: "memory");
+    };
     auto stage_end = [&] {
         wait_vmcnt(MX_GEMM_WSLACK ? NB * WB<DT>::kMinLoads : 0);
         __builtin_amdgcn_s_barrier();
@@ -569,7 +594,8 @@ __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
         for (int nb = 0; nb < NB; nb++) touch_regs(w0[nb]);
         issue_a(ks + 1, sA1);
 #pragma unroll
-        for (int nb = 0; nb < NB; nb++) w1[nb].load(wbase[nb], wrow[nb], ks + 1, kh);
+        for (int nb = 0; nb < NB; nb++) w1[nb].load(wbase[nb], wres[nb], wrow[nb], ks + 1, kh);
+        pin_weight_loads();
 #pragma unroll
         for (int nb = 0; nb < NB; nb++) w0[nb].template prep<0>(kh);
         compute(sA0, w0);
@@ -583,7 +609,8 @@ __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
             const int kn = min(ks + 2, nks - 1);
             issue_a(kn, sA0);
 #pragma unroll
-            for (int nb = 0; nb < NB; nb++) w0[nb].load(wbase[nb], wrow[nb], kn, kh);
+            for (int nb = 0; nb < NB; nb++) w0[nb].load(wbase[nb], wres[nb], wrow[nb], kn, kh);
+            pin_weight_loads();
         }
 #pragma unroll
         for (int nb = 0; nb < NB; nb++) w1[nb].template prep<1>(kh);
@@ -712,7 +739,7 @@ mx_status launch_gemm(int dtype, bool swiglu, const GemmArgs &a, hipStream_t s) 
     // weight rows from the expert, with 32-bit offsets
     const int64_t a_span = a.a_by_token ? a.t : GM_BM;
     if (a_span * a.k * 2 >= (INT64_C(1) << 32) ||
-        (int64_t)a.n_out * (a.row_bytes > a.sh_row_bytes ? a.row_bytes : a.sh_row_bytes) >= (INT64_C(1) << 32))
+        (int64_t)a.n_out * (a.row_bytes > a.sh_row_bytes ? a.row_bytes : a.sh_row_bytes) >= (INT64_C(1) << 31))
         return fail(MX_ERR_OVERFLOW, "gemm: an operand span beyond 4 GiB (t * k * 2 bytes of x); split the batch");
     const int64_t blocks = (t_max * nt + 7) / 8 * 8;
     if (blocks > INT32_MAX) return fail(MX_ERR_OVERFLOW, "gemm: too many tiles");
