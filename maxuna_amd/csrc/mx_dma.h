@@ -24,6 +24,10 @@ __device__ __forceinline__ void wait_vmcnt(int n) {
         MX_VMW(8) MX_VMW(9) MX_VMW(10) MX_VMW(11) MX_VMW(12) MX_VMW(13) MX_VMW(14) MX_VMW(15)
         MX_VMW(16) MX_VMW(17) MX_VMW(18) MX_VMW(19) MX_VMW(20) MX_VMW(21) MX_VMW(22) MX_VMW(23)
         MX_VMW(24) MX_VMW(25) MX_VMW(26) MX_VMW(27) MX_VMW(28) MX_VMW(29) MX_VMW(30) MX_VMW(31)
+        MX_VMW(32) MX_VMW(33) MX_VMW(34) MX_VMW(35) MX_VMW(36) MX_VMW(37) MX_VMW(38) MX_VMW(39)
+        MX_VMW(40) MX_VMW(41) MX_VMW(42) MX_VMW(43) MX_VMW(44) MX_VMW(45) MX_VMW(46) MX_VMW(47)
+        MX_VMW(48) MX_VMW(49) MX_VMW(50) MX_VMW(51) MX_VMW(52) MX_VMW(53) MX_VMW(54) MX_VMW(55)
+        MX_VMW(56) MX_VMW(57) MX_VMW(58) MX_VMW(59) MX_VMW(60) MX_VMW(61) MX_VMW(62) MX_VMW(63)
         default: __builtin_amdgcn_s_waitcnt(0x0F70); break;
     }
     asm volatile("" ::: "memory");
