@@ -167,7 +167,7 @@ template <> struct Q<kQ6_K> {
     static constexpr int GPB = 8;
     struct X {
         uint32_t h[8], l[8];  // part p: [2p], [2p+1] = 8 activation digits
-        int S8[4];            // sum of x16 over the part's 8 positions
+        int nS32[4];          // -32 * (sum of x16 over the part's 8 positions)
         float s[4];           // group scale of the part's positions
     };
     // raw dwords of the 8-byte fields (3 aligned dwords each, funnel-shifted in dot()
@@ -182,32 +182,37 @@ template <> struct Q<kQ6_K> {
             const uint2 vl = *reinterpret_cast<const uint2 *>(xv.xl + pos);
             x.h[2 * p] = vh.x; x.h[2 * p + 1] = vh.y;
             x.l[2 * p] = vl.x; x.l[2 * p + 1] = vl.y;
-            x.S8[p] = xv.S8[pos >> 3];
+            x.nS32[p] = -32 * xv.S8[pos >> 3];
             x.s[p] = xv.s[pos >> 5];
         }
     }
-    // 3 aligned dwords covering the 8 bytes at p (p 2-byte aligned; the third
-    // dword holds field bytes or, for dword-aligned p, bytes of the same block)
+    // 3 dwords at a 4-byte aligned p: the 8 bytes of a field that starts at p or p + 2
     __device__ static void ld3(const uint8_t *p, uint32_t (&d)[3]) {
-        // pointer arithmetic (not an integer round trip) keeps the LDS address space visible
-        const uint32_t *q = reinterpret_cast<const uint32_t *>(p - (reinterpret_cast<uintptr_t>(p) & 3));
+        const uint32_t *q = reinterpret_cast<const uint32_t *>(p);
         d[0] = q[0]; d[1] = q[1]; d[2] = q[2];
     }
     __device__ static Raw load(const uint8_t *__restrict__ row, int g) {
         const int b = g >> 3, gi = g & 7, n = gi >> 2, j = gi & 3;
         const uint8_t *blk = row + b * 210;
+        // Every field sits at a multiple of 8 inside the block, so all of them
+        // share the block's offset mod 4 (0 or 2): one aligned base serves all.
+        // Pointer arithmetic (not an integer round trip) keeps the LDS address
+        // space visible.
+        const uint32_t mis = (uint32_t)reinterpret_cast<uintptr_t>(blk) & 2;
+        const uint8_t *ab = blk - mis;
         Raw r;
-        r.sh = (uint32_t)(reinterpret_cast<uintptr_t>(blk) & 2) << 3;  // every field shares the block's parity
-        ld3(blk + 64 * n + 8 * j, r.a);          // ql[l]    : part 0 low nibble, part 2 high
-        ld3(blk + 64 * n + 32 + 8 * j, r.b);     // ql[l+32] : part 1 low nibble, part 3 high
-        ld3(blk + 128 + 32 * n + 8 * j, r.hq);   // qh[l]    : 2 bits of each part
-        ld3(blk + 192 + 8 * n, r.sc);            // scales[8n .. 8n+7]
+        r.sh = mis << 3;
+        ld3(ab + 64 * n + 8 * j, r.a);          // ql[l]    : part 0 low nibble, part 2 high
+        ld3(ab + 64 * n + 32 + 8 * j, r.b);     // ql[l+32] : part 1 low nibble, part 3 high
+        ld3(ab + 128 + 32 * n + 8 * j, r.hq);   // qh[l]    : 2 bits of each part
+        ld3(ab + 192 + 8 * n, r.sc);            // scales[8n .. 8n+7]
         r.d = ld_u16(blk + 208);
         return r;
     }
     __device__ static float dot(const Raw &r, int g, const X &x) {
         const int jh = ((g & 7) & 3) >> 1;  // scale byte is scales[8n + jh + 2p]
-        int hacc[4] = {0, 0, 0, 0}, lacc[4] = {0, 0, 0, 0};
+        // the low-digit sums start at -32 * S8: (hacc << 8) + lacc = sum (q - 32) x16
+        int hacc[4] = {0, 0, 0, 0}, lacc[4] = {x.nS32[0], x.nS32[1], x.nS32[2], x.nS32[3]};
         auto fun = [&](const uint32_t (&d)[3], int w) { return __builtin_amdgcn_alignbit(d[w + 1], d[w], r.sh); };
         const uint32_t A[2] = {fun(r.a, 0), fun(r.a, 1)}, B[2] = {fun(r.b, 0), fun(r.b, 1)},
                        H[2] = {fun(r.hq, 0), fun(r.hq, 1)};
@@ -230,7 +235,7 @@ template <> struct Q<kQ6_K> {
         for (int p = 0; p < 4; p++) {
             const uint32_t src = SC[p >> 1];
             const int sc = (int)(int8_t)((src >> (8 * (jh + 2 * (p & 1)))) & 0xFFu);
-            const int acc = (hacc[p] << 8) + lacc[p] - 32 * x.S8[p];  // sum (q - 32) x16, exact
+            const int acc = (hacc[p] << 8) + lacc[p];  // sum (q - 32) x16, exact
             tot = __builtin_fmaf((float)sc * x.s[p], (float)acc, tot);
         }
         return h2f((uint16_t)r.d) * tot;
