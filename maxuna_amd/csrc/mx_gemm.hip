@@ -689,26 +689,39 @@ __global__ void k_ids_with_shared(const uint32_t *__restrict__ ids, int t, int t
 }
 
 // out = residual + (sum_s w_s down_s) + shared   (moe.rs:78; combine.metal:16-40 order)
+// KK > 0: compiled for kk = top_k + has_shared == KK, so every slot's load is
+// issued before the first one is used; KK == 0: any kk, one slot at a time.
+template <int KK>
 __global__ void __launch_bounds__(256) k_combine_prefill(const float *__restrict__ down, const float *__restrict__ w,
                                                          const float *__restrict__ residual, int top_k,
                                                          int has_shared, int n, float *__restrict__ out) {
     const int64_t tok = blockIdx.y;
     const int i = (blockIdx.x * 256 + threadIdx.x) * 4;
     if (i >= n) return;
-    const int kk = top_k + has_shared;
+    const int kk = KK > 0 ? KK : top_k + has_shared;
     const float *d = down + tok * kk * n + i;
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int s = 0; s < top_k; s++) {
-        const float ws = w[tok * top_k + s];
-        const float4 v = *reinterpret_cast<const float4 *>(d + (int64_t)s * n);
+    auto fma4 = [](float ws, const float4 &v, float4 &acc) {
         acc.x = __builtin_fmaf(ws, v.x, acc.x);
         acc.y = __builtin_fmaf(ws, v.y, acc.y);
         acc.z = __builtin_fmaf(ws, v.z, acc.z);
         acc.w = __builtin_fmaf(ws, v.w, acc.w);
+    };
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 sh = make_float4(0.f, 0.f, 0.f, 0.f);
+    if constexpr (KK > 0) {
+        float4 v[KK];
+#pragma unroll
+        for (int s = 0; s < KK; s++) v[s] = *reinterpret_cast<const float4 *>(d + (int64_t)s * n);
+#pragma unroll
+        for (int s = 0; s < KK; s++)
+            if (s < top_k) fma4(w[tok * top_k + s], v[s], acc);
+        if (has_shared) sh = v[KK - 1];
+    } else {
+        for (int s = 0; s < top_k; s++) fma4(w[tok * top_k + s], *reinterpret_cast<const float4 *>(d + (int64_t)s * n), acc);
+        if (has_shared) sh = *reinterpret_cast<const float4 *>(d + (int64_t)top_k * n);
     }
     if (has_shared) {
-        const float4 v = *reinterpret_cast<const float4 *>(d + (int64_t)top_k * n);
-        acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+        acc.x += sh.x; acc.y += sh.y; acc.z += sh.z; acc.w += sh.w;
     }
     if (residual) {
         const float4 r = *reinterpret_cast<const float4 *>(residual + tok * n + i);
@@ -779,7 +792,13 @@ mx_status launch_combine_prefill(const float *down, const float *w, const float 
                                  int has_shared, int n, float *out, hipStream_t s) {
     if (t == 0) return MX_OK;
     const dim3 grid((unsigned)((n / 4 + 255) / 256), (unsigned)t);
-    hipLaunchKernelGGL(k_combine_prefill, grid, dim3(256), 0, s, down, w, residual, top_k, has_shared, n, out);
+    switch (top_k + has_shared) {
+#define MX_CB(K) \
+    case K: hipLaunchKernelGGL(k_combine_prefill<K>, grid, dim3(256), 0, s, down, w, residual, top_k, has_shared, n, out); break;
+        MX_CB(2) MX_CB(3) MX_CB(4) MX_CB(5) MX_CB(6) MX_CB(7) MX_CB(8) MX_CB(9) MX_CB(10) MX_CB(11) MX_CB(12)
+#undef MX_CB
+        default: hipLaunchKernelGGL(k_combine_prefill<0>, grid, dim3(256), 0, s, down, w, residual, top_k, has_shared, n, out);
+    }
     MX_LAUNCH("k_combine_prefill");
     return MX_OK;
 }
