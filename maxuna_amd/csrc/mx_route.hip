@@ -239,7 +239,7 @@ __device__ __forceinline__ void block_sums(float (&v)[RF_MAX_T], int t, float (*
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     for (int tok = 0; tok < t; tok++) {
         float a = v[tok];
-        for (int off = 32; off > 0; off >>= 1) a += __shfl_xor(a, off, 64);
+        a = warp_sum_width(a, 64);
         if (lane == 0) s_red[tok][wave] = a;
     }
     __syncthreads();

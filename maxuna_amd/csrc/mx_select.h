@@ -35,9 +35,10 @@ __device__ __forceinline__ uint64_t sel_key(float v, int e) {
     return ((uint64_t)o << 32) | (uint32_t)(~(uint32_t)e);
 }
 
-__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
-    const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, m, 64);
-    const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), m, 64);
+// the 64-bit value of this lane's lane_partner<O> (a DPP move of both halves)
+template <int O> __device__ __forceinline__ uint64_t lane_partner_u64(uint64_t v) {
+    const uint32_t lo = __float_as_uint(lane_partner<O>(__uint_as_float((uint32_t)v)));
+    const uint32_t hi = __float_as_uint(lane_partner<O>(__uint_as_float((uint32_t)(v >> 32))));
     return ((uint64_t)hi << 32) | lo;
 }
 
@@ -65,12 +66,14 @@ __device__ __forceinline__ void topk_select(const uint64_t (&key)[SEL_PER], cons
 #pragma unroll
     for (int j = 0; j < SEL_PER; j++) {
         if (j * SEL_THREADS < n_expert) {  // block-uniform
+            // partners lane ^ 1, lane ^ 2, then the mirror lane of the 8: the
+            // maximum of all 8 lanes reaches every lane of the group
             uint64_t g = key[j];
-            uint64_t o = shfl_xor_u64(g, 1);
+            uint64_t o = lane_partner_u64<1>(g);
             g = o > g ? o : g;
-            o = shfl_xor_u64(g, 2);
+            o = lane_partner_u64<2>(g);
             g = o > g ? o : g;
-            o = shfl_xor_u64(g, 4);
+            o = lane_partner_u64<4>(g);
             g = o > g ? o : g;
             const int e = tid + SEL_THREADS * j;
             if ((tid & 7) == 0 && e < n_expert) sh.gmax[e >> 3] = g;
