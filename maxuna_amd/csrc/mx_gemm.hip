@@ -647,6 +647,10 @@ __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
 }
 
 // ---- f32 rows -> scaled f16 rows ----------------------------------------------------
+// RPT > 0: k <= 1024 * RPT; the row's float4s stay in registers between the
+// max pass and the conversion (all loads issued up front).  RPT == 0: any k,
+// the row is read twice.
+template <int RPT>
 __global__ void __launch_bounds__(256) k_to_f16_rows(const float *__restrict__ x, int k,
                                                      const int32_t *__restrict__ count,
                                                      _Float16 *__restrict__ y, float *__restrict__ scale) {
@@ -655,13 +659,26 @@ __global__ void __launch_bounds__(256) k_to_f16_rows(const float *__restrict__ x
     __shared__ float s_red[4];
     const float4 *xr = reinterpret_cast<const float4 *>(x + row * k);
     const int n4 = k / 4;
+    auto amax4 = [](const float4 &v) { return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))); };
     float mx = 0.f;
-    for (int i = threadIdx.x; i < n4; i += 256) {
-        const float4 v = xr[i];
-        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-    }
+    float4 cache[RPT > 0 ? RPT : 1];
+    if constexpr (RPT > 0) {
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+        for (int j = 0; j < RPT; j++) {
+            const int i = threadIdx.x + 256 * j;
+            cache[j] = i < n4 ? xr[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int j = 0; j < RPT; j++) mx = fmaxf(mx, amax4(cache[j]));
+    } else {
+        for (int i = threadIdx.x; i < n4; i += 256) mx = fmaxf(mx, amax4(xr[i]));
+    }
+    mx = fmaxf(mx, lane_partner<32>(mx));
+    mx = fmaxf(mx, lane_partner<16>(mx));
+    mx = fmaxf(mx, lane_partner<8>(mx));
+    mx = fmaxf(mx, lane_partner<4>(mx));
+    mx = fmaxf(mx, lane_partner<2>(mx));
+    mx = fmaxf(mx, lane_partner<1>(mx));
     if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = mx;
     __syncthreads();
     mx = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
@@ -669,11 +686,19 @@ __global__ void __launch_bounds__(256) k_to_f16_rows(const float *__restrict__ x
     const int ex = mx > 0.f ? ilogbf(mx) - 14 : 0;
     const float inv = ldexpf(1.0f, -ex);
     half4_t *yr = reinterpret_cast<half4_t *>(y + row * k);
-    for (int i = threadIdx.x; i < n4; i += 256) {
-        const float4 v = xr[i];
+    auto put = [&](int i, const float4 &v) {
         const half2_t lo = __builtin_convertvector((float2_t){v.x * inv, v.y * inv}, half2_t);
         const half2_t hi = __builtin_convertvector((float2_t){v.z * inv, v.w * inv}, half2_t);
         yr[i] = (half4_t){lo[0], lo[1], hi[0], hi[1]};
+    };
+    if constexpr (RPT > 0) {
+#pragma unroll
+        for (int j = 0; j < RPT; j++) {
+            const int i = threadIdx.x + 256 * j;
+            if (i < n4) put(i, cache[j]);
+        }
+    } else {
+        for (int i = threadIdx.x; i < n4; i += 256) put(i, xr[i]);
     }
     if (threadIdx.x == 0) scale[row] = ldexpf(1.0f, ex);
 }
@@ -773,7 +798,10 @@ mx_status launch_gemm(int dtype, bool swiglu, const GemmArgs &a, hipStream_t s) 
 mx_status launch_to_f16_rows(const float *x, int64_t rows, int k, const int32_t *count, _Float16 *y, float *scale,
                              hipStream_t s) {
     if (rows == 0) return MX_OK;
-    hipLaunchKernelGGL(k_to_f16_rows, dim3((unsigned)rows), dim3(256), 0, s, x, k, count, y, scale);
+    const dim3 grid((unsigned)rows);
+    if (k <= 1024 * 2) hipLaunchKernelGGL(k_to_f16_rows<2>, grid, dim3(256), 0, s, x, k, count, y, scale);
+    else if (k <= 1024 * 4) hipLaunchKernelGGL(k_to_f16_rows<4>, grid, dim3(256), 0, s, x, k, count, y, scale);
+    else hipLaunchKernelGGL(k_to_f16_rows<0>, grid, dim3(256), 0, s, x, k, count, y, scale);
     MX_LAUNCH("k_to_f16_rows");
     return MX_OK;
 }
