@@ -183,3 +183,19 @@ def test_chain_with_rmsnorm_and_residual(dev, orc):
         y, _, _ = orc.moe_layer(spec, L.keys, L.router_t, L.bias, xn)
         x = (x + y).astype(np.float32)
     assert_close(got, x, what="3-layer chain")
+
+
+def test_wide_rows_generic_conversion(dev, orc):
+    """hidden = 5120 and ff = 2304: the prefill's f16 row conversion takes its
+    any-width form for x (k > 4096) and the partial register-cached form for the
+    activation.  Grouped-GEMM path (t = 48) only: the decode gate/up kernel
+    rejects Q4_K rows this wide (MX_ERR_SHAPE, its LDS ring batch), checked too."""
+    spec = LayerSpec(5120, 2304, 16, 4, GgmlDType.Q4_K, GgmlDType.Q6_K, shared=True)
+    layer = build_layer(spec, seed=1041)
+    with pytest.raises(Exception, match="rows too long for the LDS ring"):
+        run_block(layer, make_x(spec, 58, 1))
+    for t in (48,):
+        _log(f"wide rows t={t}")
+        x = make_x(spec, 57 + t, t)
+        out, ids, w = run_block(layer, x)
+        oracle_check(orc, layer, x, out, ids, w, f"wide rows t={t}", max_flips=1)
