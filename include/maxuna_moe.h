@@ -89,11 +89,24 @@ mx_status mx_dequantize(int32_t dtype, const void *blocks, int64_t n, float *out
  *   x   [t, x_per_row, k] f32, x_per_row in {1, top_k}
  *   ids [t, top_k] u32 (ids_t must equal t)
  *   dst [t, top_k, n_out] f32:  dst[i,s,:] = W[ids[i,s]] . x[i, x_per_row==1 ? 0 : s]
- * Supported: Q4_K, Q6_K, Q8_0.  Out-of-range ids are clamped into range on
- * the device (no fault); callers must pass valid ids. */
+ * Supported: Q4_K, Q5_K, Q6_K, Q8_0, any k that is a multiple of the block
+ * size (rows the LDS-ring kernel cannot hold take an f32 kernel).  Out-of-range
+ * ids are clamped into range on the device (no fault); mx_check_ids detects
+ * them. */
 mx_status mx_mul_mv_id(const mx_expert_stack *stack, const float *x, int64_t t,
                        int64_t x_per_row, int64_t k, const uint32_t *ids, int64_t ids_t,
                        int64_t top_k, float *dst, mx_stream_t stream);
+
+/* Validates routing ids on the device, the fail-closed check the reference's
+ * host-side validation (dispatch.rs:812-847) cannot make on device-resident
+ * ids: *flags (one device u32, written by a single store) becomes
+ * (1 if some token repeats an id across its top_k slots) | (2 if some id is
+ * >= n_expert).  The gather kernels clamp an out-of-range id into range (no
+ * fault, wrong expert) and the bucket pass collapses repeats (mm_id.metal:
+ * 243-251), so callers that take ids from outside the router check them here.
+ * Ids produced by mx_route_from_logits / mx_moe_forward are always valid. */
+mx_status mx_check_ids(const uint32_t *ids, int64_t t, int64_t top_k, int64_t n_expert,
+                       uint32_t *flags, mx_stream_t stream);
 
 /* Plain quantised mat-vec.  Replaces ops::mv_id::mul_mv (mv_id.rs:54-56 ->
  * dispatch.rs:964-1057).  w: [n_out, k] raw blocks; x [t, k]; dst [t, n_out]. */
@@ -112,7 +125,8 @@ mx_status mx_mul_mv(const void *w, int32_t dtype, int64_t n_out, int64_t k, cons
  *   then chunk tables (internal).
  * Within a token the top_k ids must be distinct (real top-k guarantees it;
  * mm_id.metal:243-251 collapses duplicate slots).  The bucket pass checks this
- * on the device and records a duplicate in a flag that mx_map0_check reads. */
+ * on the device and records a duplicate (1) or an out-of-range id (2) in the
+ * dup word at [2E+2]; mx_check_ids gives the same flags without a map. */
 typedef struct mx_map0 {
     void *buffer;
     size_t bytes;
@@ -130,7 +144,7 @@ mx_status mx_prepare_map0(int64_t n_expert, const uint32_t *ids, int64_t t, int6
 /* Replaces ops::mm_id::mul_mm_id_shared (mm_id.rs:32-39 -> dispatch.rs:789).
  * Shapes as mx_mul_mv_id; `map` must come from mx_prepare_map0 with the same
  * ids, and its geometry must match (n_expert, t, top_k), else MX_ERR_SCRATCH
- * (dispatch.rs:886-896).  Supported: Q4_K, Q6_K, Q8_0. */
+ * (dispatch.rs:886-896).  Supported: Q4_K, Q5_K, Q6_K, Q8_0. */
 mx_status mx_mul_mm_id_shared(const mx_expert_stack *stack, const float *x, int64_t t,
                               int64_t x_per_row, int64_t k, const uint32_t *ids,
                               int64_t ids_t, int64_t top_k, const mx_map0 *map,
@@ -211,8 +225,12 @@ size_t mx_moe_workspace_bytes(const mx_moe_layer *layer, int64_t t);
 
 /* x [t, hidden] f32 -> out [t, hidden] f32.  `residual` is NULL or
  * [t, hidden] f32 and is added to the output.  `ids_out`/`w_out` (optional,
- * [t, top_k]) receive the routing decision.  The workspace must be zeroed
- * once when first allocated (the kernels leave it reusable). */
+ * [t, top_k]) receive the routing decision.  The workspace holds no state
+ * between calls: every forward initialises what it reads, so any bytes will
+ * do, and one workspace serves calls of any t (sized for the largest).  Calls
+ * that share a workspace must be ordered on one stream.  Every shape that
+ * passes validation runs: rows too wide for the fused decode kernels' LDS
+ * take the f32 gather mat-vec path (chosen before the first launch). */
 mx_status mx_moe_forward(const mx_moe_layer *layer, const float *x, int64_t t,
                          const float *residual, float *out, uint32_t *ids_out, float *w_out,
                          void *workspace, size_t workspace_bytes, mx_stream_t stream);

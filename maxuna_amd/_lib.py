@@ -101,6 +101,7 @@ SIGNATURES = {
                                   C.POINTER(Map0C), P, P]),
     "mx_mul_mm_id_workspace_bytes": (SZ, [I64, I64, I64, I64, I64]),
     "mx_mul_mm_id": (I32, [C.POINTER(ExpertStackC), P, I64, I64, I64, P, I64, I64, P, SZ, P, P]),
+    "mx_check_ids": (I32, [P, I64, I64, I64, P, P]),
     "mx_silu_mul": (I32, [P, P, I64, P, P]),
     "mx_combine": (I32, [P, P, P, I64, I64, I64, P, P]),
     "mx_rms_norm": (I32, [P, P, I64, I64, F32, P, P]),

@@ -215,6 +215,17 @@ mx_status mx_mul_mm_id(const mx_expert_stack *stack, const float *x, int64_t t, 
     return mx_mul_mm_id_shared(stack, x, t, x_per_row, k, ids, ids_t, top_k, &m, dst, stream);
 }
 
+mx_status mx_check_ids(const uint32_t *ids, int64_t t, int64_t top_k, int64_t n_expert, uint32_t *flags,
+                       mx_stream_t stream) {
+    if (t < 0 || top_k <= 0 || top_k > 64 || n_expert <= 0 || n_expert > INT32_MAX)
+        return fail(MX_ERR_SHAPE, "check_ids: bad shape t=%lld top_k=%lld n_expert=%lld", (long long)t,
+                    (long long)top_k, (long long)n_expert);
+    if (t * top_k > (int64_t)1 << 22) return fail(MX_ERR_OVERFLOW, "check_ids: t*top_k exceeds 4M pairs");
+    if (!flags) return fail(MX_ERR_NULL, "check_ids: flags is NULL");
+    if (t > 0 && !ids) return fail(MX_ERR_NULL, "check_ids: ids is NULL");
+    return launch_check_ids(ids, t, (int)top_k, (int)n_expert, flags, (hipStream_t)stream);
+}
+
 mx_status mx_silu_mul(const float *gate, const float *up, int64_t n, float *dst, mx_stream_t stream) {
     if (n < 0) return fail(MX_ERR_SHAPE, "silu_mul: negative n");
     if (n == 0) return MX_OK;
@@ -292,11 +303,19 @@ struct Ws {
 
 struct Plan {
     bool mm, fused_router, has_shared;
+    bool generic;           // below the GEMM threshold, shapes the fused decode kernels cannot hold:
+                            // router + f32 gather mat-vecs + SwiGLU + combine
     bool shared_in_decode;  // shared expert rides in the fused decode kernels (same quant types)
     bool expert_order;      // decode kernels walk (token, slot) pairs in expert order (unfused router)
     int64_t min_seq;
 };
 
+int64_t stack_row_bytes(const mx_expert_stack &st) {
+    return supported(st.dtype) ? st.k / block_size(st.dtype) * type_size(st.dtype) : 0;
+}
+
+// Chooses the kernels of a forward; every shape limit of the chosen kernels is
+// checked here, so a validated call never fails after its first launch.
 Plan plan_for(const mx_moe_layer *L, int64_t t) {
     Plan p;
     p.min_seq = L->mm_min_seq > 0 ? L->mm_min_seq : kDefaultMmMinSeq;
@@ -306,12 +325,21 @@ Plan plan_for(const mx_moe_layer *L, int64_t t) {
     if (L->shared_gate.data)
         shapes = shapes && gemm_supported(L->shared_gate.dtype, (int)L->hidden) &&
                  gemm_supported(L->shared_down.dtype, (int)L->expert_ff);
+    shapes = shapes && gemm_fits((int)t, (int)L->hidden, (int)L->expert_ff, stack_row_bytes(L->gate),
+                                 stack_row_bytes(L->down));
+    if (L->shared_gate.data)
+        shapes = shapes && gemm_fits((int)t, (int)L->hidden, (int)L->expert_ff, stack_row_bytes(L->shared_gate),
+                                     stack_row_bytes(L->shared_down));
     p.mm = L->mm_min_seq >= 0 && t >= p.min_seq && shapes;
-    p.fused_router = !p.mm && t <= route_fused_max_t();
     p.has_shared = L->shared_gate.data != nullptr;
     p.shared_in_decode = p.has_shared && L->shared_gate.dtype == L->gate.dtype &&
                          L->shared_down.dtype == L->down.dtype;
-    p.expert_order = !p.mm && !p.fused_router && t * (L->top_k + (p.shared_in_decode ? 1 : 0)) <= SORT_PAIRS_MAX;
+    const bool decode_fits = decode_gate_up_fits(L->gate.dtype, (int)L->hidden, stack_row_bytes(L->gate)) &&
+                             decode_down_fits(L->down.dtype, (int)L->expert_ff, stack_row_bytes(L->down));
+    p.generic = !p.mm && !decode_fits;
+    p.fused_router = !p.mm && !p.generic && t <= route_fused_max_t();
+    p.expert_order = !p.mm && !p.generic && !p.fused_router &&
+                     t * (L->top_k + (p.shared_in_decode ? 1 : 0)) <= SORT_PAIRS_MAX;
     return p;
 }
 
@@ -322,11 +350,10 @@ struct Layout {
     uint32_t *ids = nullptr, *zero_ids = nullptr;
     uint8_t *xstage = nullptr, *xstage_gm = nullptr;
     float *part = nullptr;
-    unsigned *counters = nullptr;
     int32_t *map = nullptr, *map_sh = nullptr, *order = nullptr;
     uint32_t *ids_aug = nullptr;
     _Float16 *x16 = nullptr, *act16 = nullptr;
-    float *x16s = nullptr, *act16s = nullptr, *down = nullptr;
+    float *x16s = nullptr, *act16s = nullptr, *down = nullptr, *act_u = nullptr;
     float *sh_g = nullptr, *sh_u = nullptr, *sh_out = nullptr;
     size_t bytes = 0;
 };
@@ -343,13 +370,21 @@ Layout carve(const mx_moe_layer *L, int64_t t, const Plan &p, void *base) {
     } else {
         o.logits = ws.take<float>(t * E);
     }
-    if (!p.mm) {
+    if (p.generic) {
+        const int64_t KK = K + (p.has_shared ? 1 : 0);
+        o.act = ws.take<float>(t * K * FF);
+        o.act_u = ws.take<float>(t * K * FF);
+        if (p.has_shared) {
+            o.sh_g = ws.take<float>(t * FF);
+            o.sh_u = ws.take<float>(t * FF);
+        }
+        o.down = ws.take<float>(t * KK * H);
+    } else if (!p.mm) {
         const int64_t slots = K + (p.shared_in_decode ? 1 : 0);
         o.xstage = ws.take<uint8_t>(t * stage_row_bytes((int)H));
         if (H % 64 == 0) o.xstage_gm = ws.take<uint8_t>(t * xstage_gm_stride((int)H));
         o.act = ws.take<float>(t * slots * FF);
         o.part = ws.take<float>(t * slots * H);
-        o.counters = ws.take<unsigned>(decode_down_counter_words((int)t, (int)H));
         if (p.expert_order) o.order = ws.take<int32_t>(t * slots);
         if (p.has_shared && !p.shared_in_decode) {
             o.sh_g = ws.take<float>(t * FF);
@@ -503,11 +538,41 @@ mx_status moe_forward_impl(const mx_moe_layer *L, const float *x, int64_t t, con
         MX_TRY(launch_route_logits(xin, L->router, (int)t, (int)H, (int)E, o.logits, s));
         MX_TRY(launch_route_select(o.logits, L->exp_probs_b, (int)t, (int)E, (int)K, scale, apply,
                                    L->weights_norm, ids, w, s));
-        if (!p.mm) MX_TRY(launch_stage_rows(xin, (int)t, (int)H, o.xstage, o.xstage_gm, s));
+        if (!p.mm && !p.generic) MX_TRY(launch_stage_rows(xin, (int)t, (int)H, o.xstage, o.xstage_gm, s));
         if (p.expert_order)
             MX_TRY(launch_sort_pairs(ids, (int)t, (int)K, p.shared_in_decode ? 1 : 0, (int)E, o.order, s));
     }
     MX_STAGE();
+
+    if (p.generic) {
+        // f32 gather mat-vecs (any row width), then the prefill combine
+        const int S = p.has_shared ? 1 : 0, KK = (int)K + S;
+        MvfArgs m{gg.w, gg.expert_bytes, gg.row_bytes, (int)E, (int)FF, (int)H, xin, 1, ids, (int)t, (int)K,
+                  o.act, (int)K, 0};
+        MX_TRY(launch_mv_f32(L->gate.dtype, m, s));
+        m.w = gu.w;
+        m.dst = o.act_u;
+        MX_TRY(launch_mv_f32(L->up.dtype, m, s));
+        MX_TRY(launch_silu_mul(o.act, o.act_u, t * K * FF, o.act, s));
+        MvfArgs d{gd.w, gd.expert_bytes, gd.row_bytes, (int)E, (int)H, (int)FF, o.act, (int)K, ids, (int)t,
+                  (int)K, o.down, KK, 0};
+        MX_TRY(launch_mv_f32(L->down.dtype, d, s));
+        if (S) {
+            MvfArgs sgm{sg.w, sg.expert_bytes, sg.row_bytes, 1, (int)FF, (int)H, xin, 1, nullptr, (int)t, 1,
+                        o.sh_g, 1, 0};
+            MX_TRY(launch_mv_f32(L->shared_gate.dtype, sgm, s));
+            sgm.w = su.w;
+            sgm.dst = o.sh_u;
+            MX_TRY(launch_mv_f32(L->shared_up.dtype, sgm, s));
+            MX_TRY(launch_silu_mul(o.sh_g, o.sh_u, t * FF, o.sh_g, s));
+            MvfArgs sdm{sd.w, sd.expert_bytes, sd.row_bytes, 1, (int)H, (int)FF, o.sh_g, 1, nullptr, (int)t, 1,
+                        o.down, KK, (int)K};
+            MX_TRY(launch_mv_f32(L->shared_down.dtype, sdm, s));
+        }
+        MX_TRY(launch_combine_prefill(o.down, w, residual, (int)t, (int)K, S, (int)H, out, s));
+        MX_STAGE();
+        return MX_OK;
+    }
 
     if (!p.mm) {
         const bool shf = p.shared_in_decode;
@@ -552,7 +617,7 @@ mx_status moe_forward_impl(const mx_moe_layer *L, const float *x, int64_t t, con
         MX_STAGE();
         DecodeDownArgs da{gd.w, gd.expert_bytes, gd.row_bytes, shf ? sd.w : nullptr, sd.row_bytes, shared_out,
                           (int)E, (int)FF, (int)H, o.act, ids, w, residual, (int)t, (int)K, out, o.part,
-                          o.counters, o.order};
+                          o.order};
         for (int r = 0; r < (p.fused_router ? rep(3) : 1); r++) MX_TRY(launch_decode_down(L->down.dtype, da, s));
         MX_STAGE();
         return MX_OK;

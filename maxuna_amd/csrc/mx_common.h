@@ -79,35 +79,6 @@ __device__ __forceinline__ void q4k_scale_min(int j, uint32_t s0, uint32_t s1, u
     }
 }
 
-// ---- cross-workgroup hand-off without cache maintenance ----------------------------
-// A block publishes values with agent-scope relaxed atomic stores (coherent at
-// device scope by themselves: no L2 write-back of unrelated dirty lines), waits
-// until its stores have completed, then bumps a counter; the last block reads the
-// values with agent-scope relaxed atomic loads.  This replaces a release/acquire
-// fence pair, which on this multi-XCD part writes back and invalidates a whole
-// L2 per block.
-__device__ __forceinline__ void st_agent(float *p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ld_agent(const float *p) {
-    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// wait for this wave's outstanding memory operations (the published stores)
-__device__ __forceinline__ void drain_vmem() {
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-// counts the calling block in; true in the last of `expected` blocks (thread 0's
-// view; callers broadcast it through shared memory)
-__device__ __forceinline__ bool arrive_last(unsigned *counter, unsigned expected) {
-    const unsigned prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return prev == expected - 1;
-}
-__device__ __forceinline__ void reset_counter(unsigned *counter) {
-    __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 // The value held by this lane's partner for O in {1, 2, 4, 8, 16, 32}, exchanged
 // without LDS (DPP / permlane).  The partner differs from the lane in bit log2(O)
 // and possibly in lower bits, never in higher ones: lane ^ 1, ^ 2, ^ 7

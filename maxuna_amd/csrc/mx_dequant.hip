@@ -10,6 +10,7 @@
 // This file is compiled with -ffp-contract=off, so no product/difference pair
 // is fused into an FMA.
 #include "mx_launch.h"
+#include "mx_deq.h"
 
 namespace mx {
 
@@ -22,63 +23,11 @@ __global__ void __launch_bounds__(256) k_dequantize(const uint8_t *__restrict__ 
     if (c >= n_chunks) return;
     constexpr int CPB = block_size(DT) / 32;  // 32-weight chunks per block
     const int64_t b = c / CPB;
-    const int part = (int)(c % CPB);
-    const uint8_t *blk = blocks + b * type_size(DT);
     float y[32];
-    if constexpr (DT == kQ4_K || DT == kQ5_K) {
-        const int i = part >> 1, hi = part & 1;
-        const float d = h2f(ld_u16(blk)), dmin = h2f(ld_u16(blk + 2));
-        const uint32_t s0 = ld_u32(blk + 4), s1 = ld_u32(blk + 8), s2 = ld_u32(blk + 12);
-        uint32_t sc, m;
-        q4k_scale_min(2 * i + hi, s0, s1, s2, sc, m);
-        const float d1 = d * (float)sc;
-        const float m1 = dmin * (float)m;
-        constexpr int QS = DT == kQ5_K ? 48 : 16;  // Q5_K: qh[32] sits before qs
-        const uint8_t *q = blk + QS + 32 * i;
+    dequant_chunk<DT>(blocks + b * type_size(DT), (int)(c % CPB), y);
+    float4 *o = reinterpret_cast<float4 *>(out + 32 * c);
 #pragma unroll
-        for (int w = 0; w < 8; w++) {
-            const uint32_t v = ld_u32(q + 4 * w);
-            const uint32_t hb = DT == kQ5_K ? ld_u32(blk + 16 + 4 * w) >> (2 * i + hi) : 0u;
-#pragma unroll
-            for (int bb = 0; bb < 4; bb++) {
-                const uint32_t byte = (v >> (8 * bb)) & 0xFFu;
-                const uint32_t qq = (hi ? (byte >> 4) : (byte & 0xFu)) | (((hb >> (8 * bb)) & 1u) << 4);
-                const float p = d1 * (float)qq;
-                y[4 * w + bb] = p - m1;
-            }
-        }
-        const int64_t base = b * 256 + 64 * i + 32 * hi;
-        float4 *o = reinterpret_cast<float4 *>(out + base);
-#pragma unroll
-        for (int w = 0; w < 8; w++) o[w] = make_float4(y[4 * w], y[4 * w + 1], y[4 * w + 2], y[4 * w + 3]);
-    } else if constexpr (DT == kQ6_K) {
-        // part = 4*n + p: half n (0/1), quarter p (0..3) -> weights 128n + 32p + l
-        const int n = part >> 2, p = part & 3;
-        const float d = h2f(ld_u16(blk + 208));
-        const uint8_t *ql = blk + 64 * n + ((p & 1) ? 32 : 0);
-        const uint8_t *qh = blk + 128 + 32 * n;
-        const int8_t *scp = reinterpret_cast<const int8_t *>(blk + 192 + 8 * n);
-        const int shift_l = (p & 2) ? 4 : 0;    // q3/q4 use the high nibble
-        const int shift_h = 2 * p;              // qh bits 0-1, 2-3, 4-5, 6-7
-#pragma unroll
-        for (int l = 0; l < 32; l++) {
-            const int ql_b = ql[l], qh_b = qh[l];
-            const int q = (((ql_b >> shift_l) & 0xF) | (((qh_b >> shift_h) & 3) << 4)) - 32;
-            const float s = d * (float)scp[(l >> 4) + 2 * p];
-            y[l] = s * (float)q;
-        }
-        float4 *o = reinterpret_cast<float4 *>(out + b * 256 + 128 * n + 32 * p);
-#pragma unroll
-        for (int w = 0; w < 8; w++) o[w] = make_float4(y[4 * w], y[4 * w + 1], y[4 * w + 2], y[4 * w + 3]);
-    } else {
-        const float d = h2f(ld_u16(blk));
-        const int8_t *qs = reinterpret_cast<const int8_t *>(blk + 2);
-#pragma unroll
-        for (int l = 0; l < 32; l++) y[l] = (float)qs[l] * d;
-        float4 *o = reinterpret_cast<float4 *>(out + b * 32);
-#pragma unroll
-        for (int w = 0; w < 8; w++) o[w] = make_float4(y[4 * w], y[4 * w + 1], y[4 * w + 2], y[4 * w + 3]);
-    }
+    for (int w = 0; w < 8; w++) o[w] = make_float4(y[4 * w], y[4 * w + 1], y[4 * w + 2], y[4 * w + 3]);
 }
 
 mx_status launch_dequantize(int dtype, const uint8_t *blocks, int64_t n, float *out,

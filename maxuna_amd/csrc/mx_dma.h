@@ -34,4 +34,12 @@ __device__ __forceinline__ void wait_vmcnt(int n) {
 }
 #undef MX_VMW
 
+// s_waitcnt lgkmcnt(0): every LDS read this wave issued has returned (before an
+// LDS DMA may overwrite what they read)
+__device__ __forceinline__ void wait_lgkmcnt0() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    asm volatile("" ::: "memory");
+}
+
 }  // namespace mx

@@ -99,4 +99,37 @@ mx_status launch_add3(const float *a, const float *b, const float *c, int64_t n,
     return MX_OK;
 }
 
+// Routing-id validation: flags = (1 if some token repeats an id across its
+// top_k slots) | (2 if some id >= n_expert).  One block walks every token, so
+// the flag word is written once, by a plain store (no memset, no atomics).
+__global__ void __launch_bounds__(1024) k_check_ids(const uint32_t *__restrict__ ids, int64_t t, int top_k,
+                                                    uint32_t n_expert, uint32_t *__restrict__ flags) {
+    __shared__ uint32_t s_f[16];
+    uint32_t f = 0;
+    for (int64_t tok = threadIdx.x; tok < t; tok += blockDim.x) {
+        const uint32_t *r = ids + tok * top_k;
+        for (int a = 0; a < top_k; a++) {
+            const uint32_t ia = r[a];
+            if (ia >= n_expert) f |= 2u;
+            for (int b = a + 1; b < top_k; b++)
+                if (r[b] == ia) f |= 1u;
+        }
+    }
+    for (int off = 32; off > 0; off >>= 1) f |= (uint32_t)__shfl_xor((int)f, off, 64);
+    if ((threadIdx.x & 63) == 0) s_f[threadIdx.x >> 6] = f;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t v = 0;
+        for (int i = 0; i < (int)(blockDim.x >> 6); i++) v |= s_f[i];
+        *flags = v;
+    }
+}
+
+mx_status launch_check_ids(const uint32_t *ids, int64_t t, int top_k, int n_expert, uint32_t *flags,
+                           hipStream_t s) {
+    hipLaunchKernelGGL(k_check_ids, dim3(1), dim3(1024), 0, s, ids, t, top_k, (uint32_t)n_expert, flags);
+    MX_LAUNCH("k_check_ids");
+    return MX_OK;
+}
+
 }  // namespace mx

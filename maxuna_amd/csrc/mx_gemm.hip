@@ -718,7 +718,8 @@ __global__ void k_ids_with_shared(const uint32_t *__restrict__ ids, int t, int t
 // issued before the first one is used; KK == 0: any kk, one slot at a time.
 template <int KK>
 __global__ void __launch_bounds__(256) k_combine_prefill(const float *__restrict__ down, const float *__restrict__ w,
-                                                         const float *__restrict__ residual, int top_k,
+                                                         const float *__restrict__ residual,
+                                                         const float *__restrict__ shared_sep, int top_k,
                                                          int has_shared, int n, float *__restrict__ out) {
     const int64_t tok = blockIdx.y;
     const int i = (blockIdx.x * 256 + threadIdx.x) * 4;
@@ -745,7 +746,8 @@ __global__ void __launch_bounds__(256) k_combine_prefill(const float *__restrict
         for (int s = 0; s < top_k; s++) fma4(w[tok * top_k + s], *reinterpret_cast<const float4 *>(d + (int64_t)s * n), acc);
         if (has_shared) sh = *reinterpret_cast<const float4 *>(d + (int64_t)top_k * n);
     }
-    if (has_shared) {
+    if (shared_sep) sh = *reinterpret_cast<const float4 *>(shared_sep + tok * n + i);
+    if (has_shared || shared_sep) {
         acc.x += sh.x; acc.y += sh.y; acc.z += sh.z; acc.w += sh.w;
     }
     if (residual) {
@@ -759,6 +761,14 @@ __global__ void __launch_bounds__(256) k_combine_prefill(const float *__restrict
 
 bool gemm_supported(int dtype, int k) {
     return (dtype == kQ4_K || dtype == kQ5_K || dtype == kQ6_K || dtype == kQ8_0) && k > 0 && k % 256 == 0;
+}
+
+static bool gemm_spans_fit(int64_t a_span, int k, int n_out, int64_t row_bytes) {
+    return a_span * k * 2 < (INT64_C(1) << 32) && (int64_t)n_out * row_bytes < (INT64_C(1) << 31);
+}
+
+bool gemm_fits(int t, int hidden, int ff, int64_t gu_row_bytes, int64_t d_row_bytes) {
+    return gemm_spans_fit(t, hidden, ff, gu_row_bytes) && gemm_spans_fit(GM_BM, ff, hidden, d_row_bytes);
 }
 
 mx_status launch_gemm(int dtype, bool swiglu, const GemmArgs &a, hipStream_t s) {
@@ -776,8 +786,7 @@ mx_status launch_gemm(int dtype, bool swiglu, const GemmArgs &a, hipStream_t s) 
     // the kernel addresses a tile's A rows from its first row, and one expert's
     // weight rows from the expert, with 32-bit offsets
     const int64_t a_span = a.a_by_token ? a.t : GM_BM;
-    if (a_span * a.k * 2 >= (INT64_C(1) << 32) ||
-        (int64_t)a.n_out * (a.row_bytes > a.sh_row_bytes ? a.row_bytes : a.sh_row_bytes) >= (INT64_C(1) << 31))
+    if (!gemm_spans_fit(a_span, a.k, a.n_out, a.row_bytes > a.sh_row_bytes ? a.row_bytes : a.sh_row_bytes))
         return fail(MX_ERR_OVERFLOW, "gemm: an operand span beyond 4 GiB (t * k * 2 bytes of x); split the batch");
     const int64_t blocks = (t_max * nt + 7) / 8 * 8;
     if (blocks > INT32_MAX) return fail(MX_ERR_OVERFLOW, "gemm: too many tiles");
@@ -817,15 +826,15 @@ mx_status launch_ids_with_shared(const uint32_t *ids, int t, int top_k, int n_ex
 }
 
 mx_status launch_combine_prefill(const float *down, const float *w, const float *residual, int t, int top_k,
-                                 int has_shared, int n, float *out, hipStream_t s) {
+                                 int has_shared, int n, float *out, hipStream_t s, const float *shared_sep) {
     if (t == 0) return MX_OK;
     const dim3 grid((unsigned)((n / 4 + 255) / 256), (unsigned)t);
     switch (top_k + has_shared) {
 #define MX_CB(K) \
-    case K: hipLaunchKernelGGL(k_combine_prefill<K>, grid, dim3(256), 0, s, down, w, residual, top_k, has_shared, n, out); break;
+    case K: hipLaunchKernelGGL(k_combine_prefill<K>, grid, dim3(256), 0, s, down, w, residual, shared_sep, top_k, has_shared, n, out); break;
         MX_CB(2) MX_CB(3) MX_CB(4) MX_CB(5) MX_CB(6) MX_CB(7) MX_CB(8) MX_CB(9) MX_CB(10) MX_CB(11) MX_CB(12)
 #undef MX_CB
-        default: hipLaunchKernelGGL(k_combine_prefill<0>, grid, dim3(256), 0, s, down, w, residual, top_k, has_shared, n, out);
+        default: hipLaunchKernelGGL(k_combine_prefill<0>, grid, dim3(256), 0, s, down, w, residual, shared_sep, top_k, has_shared, n, out);
     }
     MX_LAUNCH("k_combine_prefill");
     return MX_OK;

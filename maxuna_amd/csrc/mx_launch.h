@@ -25,6 +25,24 @@ struct MvArgs {
     float *dst;             // [t, top_k, n_out]
 };
 mx_status launch_mul_mv_id(int dtype, const MvArgs &a, hipStream_t s);
+// true when the LDS-ring mat-vec (k_mul_mv_id) takes this shape; otherwise
+// launch_mul_mv_id runs the f32 mat-vec (mx_mvf.hip)
+bool mv_ring_fits(int dtype, int k);
+
+// mx_mvf.hip -- f32 gather mat-vec for any k (a multiple of the block size).
+// dst row of (token, slot): (token * dst_stride + slot + dst_add) * n_out.
+struct MvfArgs {
+    const uint8_t *w;
+    int64_t expert_bytes, row_bytes;
+    int n_expert, n_out, k;
+    const float *x;
+    int x_per_row;
+    const uint32_t *ids;    // [t, top_k] or NULL (expert 0)
+    int t, top_k;
+    float *dst;
+    int dst_stride, dst_add;
+};
+mx_status launch_mv_f32(int dtype, const MvfArgs &a, hipStream_t s);
 
 // Fused decode layer pieces (mx_mv.hip).
 struct DecodeGateUpArgs {
@@ -56,6 +74,10 @@ struct DecodeSelArgs {
 // expert, which must have the routed experts' quant type); sel may be NULL.
 mx_status launch_decode_gate_up(int dtype, const DecodeGateUpArgs &a, int slot0, int nslot,
                                 const DecodeSelArgs *sel, hipStream_t s);
+// true when the fused decode kernels take a layer of these shapes (their DMA
+// batches and LDS fit); checked before any launch of a forward
+bool decode_gate_up_fits(int dtype, int hidden, int64_t row_bytes);
+bool decode_down_fits(int dtype, int ff, int64_t row_bytes);
 
 struct DecodeDownArgs {
     const uint8_t *down;
@@ -71,7 +93,6 @@ struct DecodeDownArgs {
     int t, top_k;
     float *out;                          // [t, hidden]
     float *part;                         // [t, top_k + (sh_down != NULL), hidden] scratch
-    unsigned *counters;                  // decode_down_counter_words(t, hidden), zero, self-resetting
     const int32_t *order;                // NULL, or the t * slots (token, slot) pairs sorted by expert
 };
 mx_status launch_decode_down(int dtype, const DecodeDownArgs &a, hipStream_t s);
@@ -83,7 +104,6 @@ mx_status launch_decode_down(int dtype, const DecodeDownArgs &a, hipStream_t s);
 mx_status launch_sort_pairs(const uint32_t *ids, int t, int top_k, int has_shared, int n_expert, int32_t *order,
                             hipStream_t s);
 constexpr int SORT_PAIRS_MAX = 1024;
-size_t decode_down_counter_words(int t, int hidden);
 
 // mx_route.hip
 // router: [n_expert, hidden] (GGUF ffn_gate_inp layout)
@@ -114,6 +134,8 @@ mx_status launch_combine(const float *down, const float *col_l2, const float *w,
                          int top_k, int n_out, float *dst, hipStream_t s);
 mx_status launch_rms_norm(const float *x, const float *alpha, int rows, int dim, float eps,
                           float *dst, hipStream_t s);
+mx_status launch_check_ids(const uint32_t *ids, int64_t t, int top_k, int n_expert, uint32_t *flags,
+                           hipStream_t s);
 mx_status launch_add3(const float *a, const float *b, const float *c, int64_t n, float *dst,
                       hipStream_t s);
 
@@ -179,6 +201,9 @@ struct GemmArgs {
     int out_stride, out_add;
 };
 bool gemm_supported(int dtype, int k);
+// the kernel's 32-bit operand offsets hold for t tokens of x [t, hidden] and
+// weight rows of these byte widths
+bool gemm_fits(int t, int hidden, int ff, int64_t gu_row_bytes, int64_t d_row_bytes);
 mx_status launch_gemm(int dtype, bool swiglu, const GemmArgs &a, hipStream_t s);
 // rows of x (f32, [rows, k], k % 4 == 0) -> f16 times a per-row power of two;
 // rows at or beyond *count (when count != NULL) are skipped
@@ -187,9 +212,9 @@ mx_status launch_to_f16_rows(const float *x, int64_t rows, int k, const int32_t 
 // ids_aug[t, top_k + 1]: ids with a last slot = n_expert (the shared expert)
 mx_status launch_ids_with_shared(const uint32_t *ids, int t, int top_k, int n_expert, uint32_t *ids_aug,
                                  hipStream_t s);
-// out[t, n] = residual + sum_s w[t, s] * down[t * kk + s] + (has_shared ? down[t * kk + top_k] : 0),
-// kk = top_k + has_shared
+// out[t, n] = residual + (sum_s w[t, s] * down[t * kk + s] + shared), kk = top_k + has_shared,
+// shared = down[t * kk + top_k] (has_shared), shared_sep[t] (shared_sep != NULL) or 0; n % 4 == 0
 mx_status launch_combine_prefill(const float *down, const float *w, const float *residual, int t, int top_k,
-                                 int has_shared, int n, float *out, hipStream_t s);
+                                 int has_shared, int n, float *out, hipStream_t s, const float *shared_sep = nullptr);
 
 }  // namespace mx

@@ -2,15 +2,18 @@
 // the fused decode MoE kernels built from it.
 //
 // Activations are consumed in the staged integer form of mx_stage.h: per
-// 32-value group a scale s_g and integers x16 = 256 * xh + xl in two int8 digit
-// planes, plus sums of x16 over every 8 and 32 values.  The gate/up kernel
+// 32-value group a power-of-two scale s_g and 24-bit integers
+// x24 = 65536 * xh + 256 * xm + xl in three int8 digit planes, plus the sum of
+// x24 over every 32 values.  The gate/up kernel
 // reads the token rows staged once by the router kernel (global memory); the
 // down kernel and the generic mat-vec stage their row into LDS per workgroup
-// (activation loads issued before the weight loads).  The weight quants are unpacked to bytes with masks and shifts and contracted with both
-// digit planes on v_dot4_i32_i8, so each sub-block's sum of q * x16 is exact in
-// int32; the per-sub-block scales (d*sc, dmin*m) and the group scale s_g are
-// applied once per sub-block in f32 (the factored form of mv.metal:263-267).
-// Relative error per activation value <= 2^-16 of its group maximum.
+// (activation loads issued before the weight loads).  The weight quants are unpacked to bytes with masks and shifts and contracted with all three
+// digit planes on v_dot4_i32_i8, so each plane's sum of q * digit is exact in
+// int32; the three plane sums are recombined in f32 (two roundings), and the
+// per-sub-block scales (d*sc, dmin*m) and the group scale s_g are applied once
+// per sub-block in f32 (the factored form of mv.metal:263-267).  Each activation
+// value is carried to within 2^-23 * (1 + 2^-8) of its group's largest
+// magnitude -- the 24-bit width of the reference's f32 y (mv.metal:227-275).
 //
 // Work layout (gfx950, wave64).  A row of k weights is cut into "groups":
 //   Q4_K  group = one 64-weight sub-block pair (2i, 2i+1) of a super-block (4 per block)
@@ -63,18 +66,30 @@ __device__ __forceinline__ void lds_words(const int8_t *p, uint32_t *dst, int n1
 
 template <int DT> struct Q;
 
+// sum over the 4 bytes of each of two dwords times c (c = 1: the plain digit sum)
+__device__ __forceinline__ int digit_sum2(uint32_t a, uint32_t b, uint32_t c) { return dot4(c, a, dot4(c, b, 0)); }
+
+// 65536 * h + 256 * m + l in f32: the three exact int32 digit-plane sums of a
+// dot product recombined with at most two roundings (m * 256 + l is formed in
+// int32, exact; its conversion and the final fma each round once).
+__device__ __forceinline__ float planes(int h, int m, int l) {
+    return __builtin_fmaf((float)h, 65536.0f, (float)(m * 256 + l));
+}
+
 // ---- Q4_K -------------------------------------------------------------------------
 template <> struct Q<kQ4_K> {
     static constexpr int GPB = 4;
     struct X {
-        uint32_t h[16], l[16];  // [0..8): sub-block 2i positions 0..31, [8..16): sub-block 2i+1
-        float sa, sb, ssa, ssb;  // group scales and scale * sum(x16)
+        // [0..8): sub-block 2i positions 0..31, [8..16): sub-block 2i+1; one array per digit plane
+        uint32_t h[16], m[16], l[16];
+        float sa, sb, ssa, ssb;  // group scales and scale * sum(x24)
     };
     struct Raw { uint4 hd, qa, qb; };
     __device__ static void load_x(const XView &xv, int g, X &x) {
 #pragma unroll
         for (int half = 0; half < 2; half++) {
             lds_words(xv.xh + 64 * g + 32 * half, x.h + 8 * half, 2);
+            lds_words(xv.xm + 64 * g + 32 * half, x.m + 8 * half, 2);
             lds_words(xv.xl + 64 * g + 32 * half, x.l + 8 * half, 2);
         }
         x.sa = xv.s[2 * g];
@@ -91,28 +106,41 @@ template <> struct Q<kQ4_K> {
         r.qb = *reinterpret_cast<const uint4 *>(blk + 32 + 32 * i);
         return r;
     }
-    __device__ static float dot(const Raw &r, int g, const X &x) {
-        const uint32_t q[8] = {r.qa.x, r.qa.y, r.qa.z, r.qa.w, r.qb.x, r.qb.y, r.qb.z, r.qb.w};
-        int ah = 0, al = 0, bh = 0, bl = 0;
+    // sum_q x over a 64-weight sub-block pair (sub-block 2i: low nibbles, 2i+1: high
+    // nibbles), with the pair's per-sub-block scales applied
+    __device__ static float pair(const uint32_t (&q)[8], uint32_t hd0, uint32_t s0, uint32_t s1, uint32_t s2, int i,
+                                 const X &x, const uint32_t *hb = nullptr) {
+        int ah = 0, am = 0, al = 0, bh = 0, bm = 0, bl = 0;
 #pragma unroll
         for (int w = 0; w < 8; w++) {
-            const uint32_t lo = q[w] & 0x0F0F0F0Fu;
-            const uint32_t hi = (q[w] >> 4) & 0x0F0F0F0Fu;
+            uint32_t lo = q[w] & 0x0F0F0F0Fu;
+            uint32_t hi = (q[w] >> 4) & 0x0F0F0F0Fu;
+            if (hb) {  // Q5_K: the fifth bit of each weight
+                const uint32_t hs = hb[w] >> (2 * i);
+                lo |= (hs & 0x01010101u) << 4;
+                hi |= ((hs >> 1) & 0x01010101u) << 4;
+            }
             ah = dot4(lo, x.h[w], ah);
+            am = dot4(lo, x.m[w], am);
             al = dot4(lo, x.l[w], al);
             bh = dot4(hi, x.h[8 + w], bh);
+            bm = dot4(hi, x.m[8 + w], bm);
             bl = dot4(hi, x.l[8 + w], bl);
         }
-        const int A = (ah << 8) + al, B = (bh << 8) + bl;
+        const float A = planes(ah, am, al), B = planes(bh, bm, bl);
         uint32_t sc0, m0, sc1, m1;
-        const int i = g & 3;
-        q4k_scale_min(2 * i, r.hd.y, r.hd.z, r.hd.w, sc0, m0);
-        q4k_scale_min(2 * i + 1, r.hd.y, r.hd.z, r.hd.w, sc1, m1);
-        const float d = h2f((uint16_t)(r.hd.x & 0xFFFFu));
-        const float dmin = h2f((uint16_t)(r.hd.x >> 16));
-        const float p = __builtin_fmaf((float)sc0 * x.sa, (float)A, (float)sc1 * x.sb * (float)B);
+        q4k_scale_min(2 * i, s0, s1, s2, sc0, m0);
+        q4k_scale_min(2 * i + 1, s0, s1, s2, sc1, m1);
+        const float d = h2f((uint16_t)(hd0 & 0xFFFFu));
+        const float dmin = h2f((uint16_t)(hd0 >> 16));
+        // sa, sb are powers of two: (float)sc * sa is exact
+        const float p = __builtin_fmaf((float)sc0 * x.sa, A, (float)sc1 * x.sb * B);
         const float m = __builtin_fmaf((float)m0, x.ssa, (float)m1 * x.ssb);
         return __builtin_fmaf(d, p, -dmin * m);
+    }
+    __device__ static float dot(const Raw &r, int g, const X &x) {
+        const uint32_t q[8] = {r.qa.x, r.qa.y, r.qa.z, r.qa.w, r.qb.x, r.qb.y, r.qb.z, r.qb.w};
+        return pair(q, r.hd.x, r.hd.y, r.hd.z, r.hd.w, g & 3, x);
     }
 };
 
@@ -138,27 +166,7 @@ template <> struct Q<kQ5_K> {
     __device__ static float dot(const Raw &r, int g, const X &x) {
         const uint32_t q[8] = {r.qa.x, r.qa.y, r.qa.z, r.qa.w, r.qb.x, r.qb.y, r.qb.z, r.qb.w};
         const uint32_t h[8] = {r.ha.x, r.ha.y, r.ha.z, r.ha.w, r.hb.x, r.hb.y, r.hb.z, r.hb.w};
-        const int i = g & 3;
-        int ah = 0, al = 0, bh = 0, bl = 0;
-#pragma unroll
-        for (int w = 0; w < 8; w++) {
-            const uint32_t hs = h[w] >> (2 * i);
-            const uint32_t lo = (q[w] & 0x0F0F0F0Fu) | ((hs & 0x01010101u) << 4);
-            const uint32_t hi = ((q[w] >> 4) & 0x0F0F0F0Fu) | (((hs >> 1) & 0x01010101u) << 4);
-            ah = dot4(lo, x.h[w], ah);
-            al = dot4(lo, x.l[w], al);
-            bh = dot4(hi, x.h[8 + w], bh);
-            bl = dot4(hi, x.l[8 + w], bl);
-        }
-        const int A = (ah << 8) + al, B = (bh << 8) + bl;
-        uint32_t sc0, m0, sc1, m1;
-        q4k_scale_min(2 * i, r.hd.y, r.hd.z, r.hd.w, sc0, m0);
-        q4k_scale_min(2 * i + 1, r.hd.y, r.hd.z, r.hd.w, sc1, m1);
-        const float d = h2f((uint16_t)(r.hd.x & 0xFFFFu));
-        const float dmin = h2f((uint16_t)(r.hd.x >> 16));
-        const float p = __builtin_fmaf((float)sc0 * x.sa, (float)A, (float)sc1 * x.sb * (float)B);
-        const float m = __builtin_fmaf((float)m0, x.ssa, (float)m1 * x.ssb);
-        return __builtin_fmaf(d, p, -dmin * m);
+        return Q<kQ4_K>::pair(q, r.hd.x, r.hd.y, r.hd.z, r.hd.w, g & 3, x, h);
     }
 };
 
@@ -166,23 +174,27 @@ template <> struct Q<kQ5_K> {
 template <> struct Q<kQ6_K> {
     static constexpr int GPB = 8;
     struct X {
-        uint32_t h[8], l[8];  // part p: [2p], [2p+1] = 8 activation digits
-        int nS32[4];          // -32 * (sum of x16 over the part's 8 positions)
-        float s[4];           // group scale of the part's positions
+        uint32_t h[8], m[8], l[8];  // part p: [2p], [2p+1] = 8 activation values, one array per digit plane
+        int nh[4], nml[4];          // -32 * (digit sums of the part's 8 values): h plane; 256 * m + l planes
+        float s[4];                 // group scale of the part's positions
     };
     // raw dwords of the 8-byte fields (3 aligned dwords each, funnel-shifted in dot()
     // so that no arithmetic on loaded values sits between the loads and their use)
     struct Raw { uint32_t a[3], b[3], hq[3], sc[3]; uint32_t sh, d; };
     __device__ static void load_x(const XView &xv, int g, X &x) {
         const int b = g >> 3, gi = g & 7, n = gi >> 2, j = gi & 3;
+        constexpr uint32_t M32 = 0xE0E0E0E0u;  // -32 in every byte
 #pragma unroll
         for (int p = 0; p < 4; p++) {
             const int pos = 256 * b + 128 * n + 32 * p + 8 * j;
             const uint2 vh = *reinterpret_cast<const uint2 *>(xv.xh + pos);
+            const uint2 vm = *reinterpret_cast<const uint2 *>(xv.xm + pos);
             const uint2 vl = *reinterpret_cast<const uint2 *>(xv.xl + pos);
             x.h[2 * p] = vh.x; x.h[2 * p + 1] = vh.y;
+            x.m[2 * p] = vm.x; x.m[2 * p + 1] = vm.y;
             x.l[2 * p] = vl.x; x.l[2 * p + 1] = vl.y;
-            x.nS32[p] = -32 * xv.S8[pos >> 3];
+            x.nh[p] = digit_sum2(vh.x, vh.y, M32);
+            x.nml[p] = 256 * digit_sum2(vm.x, vm.y, M32) + digit_sum2(vl.x, vl.y, M32);
             x.s[p] = xv.s[pos >> 5];
         }
     }
@@ -211,8 +223,10 @@ template <> struct Q<kQ6_K> {
     }
     __device__ static float dot(const Raw &r, int g, const X &x) {
         const int jh = ((g & 7) & 3) >> 1;  // scale byte is scales[8n + jh + 2p]
-        // the low-digit sums start at -32 * S8: (hacc << 8) + lacc = sum (q - 32) x16
-        int hacc[4] = {0, 0, 0, 0}, lacc[4] = {x.nS32[0], x.nS32[1], x.nS32[2], x.nS32[3]};
+        // the accumulators start at -32 * (digit sums): the plane sums are then
+        // sum (q - 32) * digit, exact
+        int hacc[4] = {x.nh[0], x.nh[1], x.nh[2], x.nh[3]}, macc[4] = {0, 0, 0, 0},
+            lacc[4] = {x.nml[0], x.nml[1], x.nml[2], x.nml[3]};
         auto fun = [&](const uint32_t (&d)[3], int w) { return __builtin_amdgcn_alignbit(d[w + 1], d[w], r.sh); };
         const uint32_t A[2] = {fun(r.a, 0), fun(r.a, 1)}, B[2] = {fun(r.b, 0), fun(r.b, 1)},
                        H[2] = {fun(r.hq, 0), fun(r.hq, 1)};
@@ -227,6 +241,7 @@ template <> struct Q<kQ6_K> {
 #pragma unroll
             for (int p = 0; p < 4; p++) {
                 hacc[p] = dot4(qp[p], x.h[2 * p + w], hacc[p]);
+                macc[p] = dot4(qp[p], x.m[2 * p + w], macc[p]);
                 lacc[p] = dot4(qp[p], x.l[2 * p + w], lacc[p]);
             }
         }
@@ -235,8 +250,8 @@ template <> struct Q<kQ6_K> {
         for (int p = 0; p < 4; p++) {
             const uint32_t src = SC[p >> 1];
             const int sc = (int)(int8_t)((src >> (8 * (jh + 2 * (p & 1)))) & 0xFFu);
-            const int acc = (hacc[p] << 8) + lacc[p];  // sum (q - 32) x16, exact
-            tot = __builtin_fmaf((float)sc * x.s[p], (float)acc, tot);
+            // 256 * macc + lacc in int32: |macc| <= 63 * 128 * 8, |lacc| < 2^24
+            tot = __builtin_fmaf((float)sc * x.s[p], planes(hacc[p], macc[p], lacc[p]), tot);
         }
         return h2f((uint16_t)r.d) * tot;
     }
@@ -245,10 +260,11 @@ template <> struct Q<kQ6_K> {
 // ---- Q8_0 -------------------------------------------------------------------------
 template <> struct Q<kQ8_0> {
     static constexpr int GPB = 1;
-    struct X { uint32_t h[8], l[8]; float s; };
+    struct X { uint32_t h[8], m[8], l[8]; float s; };
     struct Raw { uint32_t q[9]; uint32_t sh, d; };
     __device__ static void load_x(const XView &xv, int g, X &x) {
         lds_words(xv.xh + 32 * g, x.h, 2);
+        lds_words(xv.xm + 32 * g, x.m, 2);
         lds_words(xv.xl + 32 * g, x.l, 2);
         x.s = xv.s[g];
     }
@@ -266,14 +282,15 @@ template <> struct Q<kQ8_0> {
         return r;
     }
     __device__ static float dot(const Raw &r, int, const X &x) {
-        int ah = 0, al = 0;
+        int ah = 0, am = 0, al = 0;
 #pragma unroll
         for (int w = 0; w < 8; w++) {
             const uint32_t v = __builtin_amdgcn_alignbit(r.q[w + 1], r.q[w], r.sh);
             ah = dot4(v, x.h[w], ah);
+            am = dot4(v, x.m[w], am);
             al = dot4(v, x.l[w], al);
         }
-        return h2f((uint16_t)r.d) * (x.s * (float)((ah << 8) + al));
+        return h2f((uint16_t)r.d) * (x.s * planes(ah, am, al));
     }
 };
 
@@ -457,7 +474,7 @@ __device__ __forceinline__ void stream_rows(const uint8_t *const (&w)[NM], int64
 }
 
 // Loads this lane's slices from the group-major staged copy (mx_stage.h):
-// nine 16-byte loads per group, each wave instruction 1 KB of consecutive bytes.
+// GM_CHUNKS 16-byte loads per group, each wave instruction 1 KB of consecutive bytes.
 template <int DT, int NG>
 __device__ __forceinline__ void load_xs_gm(const uint8_t *gm, int k, const Geo<DT> &geo,
                                            typename Q<DT>::X (&xs)[NG]) {
@@ -465,6 +482,7 @@ __device__ __forceinline__ void load_xs_gm(const uint8_t *gm, int k, const Geo<D
     const int G = k / 64;
     const uint4 *c = reinterpret_cast<const uint4 *>(gm);
     const int sub = (threadIdx.x & 63) & (geo.P - 1);
+    auto put = [](uint32_t *d, const uint4 v) { d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w; };
 #pragma unroll
     for (int jg = 0; jg < NG; jg++) {
         int g = sub + geo.P * jg;
@@ -472,11 +490,11 @@ __device__ __forceinline__ void load_xs_gm(const uint8_t *gm, int k, const Geo<D
         typename Q<DT>::X &x = xs[jg];
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-            const uint4 h = c[(size_t)q * G + g], l = c[(size_t)(4 + q) * G + g];
-            x.h[4 * q] = h.x; x.h[4 * q + 1] = h.y; x.h[4 * q + 2] = h.z; x.h[4 * q + 3] = h.w;
-            x.l[4 * q] = l.x; x.l[4 * q + 1] = l.y; x.l[4 * q + 2] = l.z; x.l[4 * q + 3] = l.w;
+            put(x.h + 4 * q, c[(size_t)q * G + g]);
+            put(x.m + 4 * q, c[(size_t)(4 + q) * G + g]);
+            put(x.l + 4 * q, c[(size_t)(8 + q) * G + g]);
         }
-        const uint4 sc = c[(size_t)8 * G + g];
+        const uint4 sc = c[(size_t)12 * G + g];
         x.sa = __uint_as_float(sc.x);
         x.sb = __uint_as_float(sc.y);
         x.ssa = __uint_as_float(sc.z);
@@ -612,10 +630,55 @@ static mx_status launch_mv_dt(const MvArgs &a, dim3 grid, hipStream_t s) {
     return MX_OK;
 }
 
+// ---- shape fits of the LDS-ring kernels (host) --------------------------------------
+// Each kernel holds NG <= NG_MAX activation groups per lane, copies a batch of rows
+// with at most DMA_MAX_INSTS wave instructions per matrix set, and needs its LDS.
+template <int DT> static int64_t row_bytes_of(int k) { return (int64_t)(k / block_size(DT)) * type_size(DT); }
+template <int DT> static bool geo_ok(int k, bool full_wave = false) {
+    return k > 0 && k % block_size(DT) == 0 && Geo<DT>(k, full_wave).NG <= NG_MAX;
+}
+template <int DT> static bool mv_fits_dt(int k) {
+    if (!geo_ok<DT>(k)) return false;
+    const Geo<DT> g(k);
+    const int nit = g.NG == 1 ? Batch<1>::NIT : Batch<2>::NIT;
+    const int ni = dma_insts(1, nit * g.RPI, row_bytes_of<DT>(k));
+    return ni <= DMA_MAX_INSTS && align16(xstage_bytes(k)) + (size_t)WAVES * RING_MV * ni * 1024 <= 160 * 1024;
+}
+template <int DT> static bool gu_fits_dt(int hidden, int64_t row_bytes) {
+    if (!geo_ok<DT>(hidden) || row_bytes != row_bytes_of<DT>(hidden)) return false;
+    const Geo<DT> g(hidden);
+    const int nit = g.NG == 1 ? Batch<1>::NIT : Batch<2>::NIT;
+    const int ni = dma_insts(2, nit * g.RPI, row_bytes);
+    return ni <= DMA_MAX_INSTS && (size_t)WAVES * RING_GU * ni * 1024 <= 160 * 1024;
+}
+template <int DT> static bool dn_fits_dt(int ff, int64_t row_bytes) {
+    if (!geo_ok<DT>(ff, DN_FULL) || row_bytes != row_bytes_of<DT>(ff)) return false;
+    const Geo<DT> g(ff, DN_FULL);
+    const int nit = g.NG == 1 ? BatchDn<1>::NIT : BatchDn<2>::NIT;
+    const int ni = dma_insts(1, nit * g.RPI, row_bytes);
+    return ni <= DMA_MAX_INSTS && align16(xstage_bytes(ff)) + (size_t)WAVES_DN * RING_DN * ni * 1024 <= 160 * 1024;
+}
+#define MX_DT_SWITCH(dtype, EXPR)                       \
+    switch (dtype) {                                    \
+    case kQ4_K: { constexpr int DT = kQ4_K; return EXPR; } \
+    case kQ5_K: { constexpr int DT = kQ5_K; return EXPR; } \
+    case kQ6_K: { constexpr int DT = kQ6_K; return EXPR; } \
+    case kQ8_0: { constexpr int DT = kQ8_0; return EXPR; } \
+    default: return false;                              \
+    }
+bool mv_ring_fits(int dtype, int k) { MX_DT_SWITCH(dtype, mv_fits_dt<DT>(k)) }
+bool decode_gate_up_fits(int dtype, int hidden, int64_t row_bytes) { MX_DT_SWITCH(dtype, gu_fits_dt<DT>(hidden, row_bytes)) }
+bool decode_down_fits(int dtype, int ff, int64_t row_bytes) { MX_DT_SWITCH(dtype, dn_fits_dt<DT>(ff, row_bytes)) }
+#undef MX_DT_SWITCH
+
 mx_status launch_mul_mv_id(int dtype, const MvArgs &a, hipStream_t s) {
     const dim3 grid((unsigned)((a.n_out + WAVES * RW_MV - 1) / (WAVES * RW_MV)), (unsigned)(a.t * a.top_k));
     if (grid.y == 0 || grid.x == 0) return MX_OK;
-    if (a.k % 32) return fail(MX_ERR_BLOCK, "mul_mv_id: k must be a multiple of 32");
+    if (!mv_ring_fits(dtype, a.k)) {  // any other row width: the f32 mat-vec
+        const MvfArgs f{a.w, a.expert_bytes, a.row_bytes, a.n_expert, a.n_out, a.k, a.x, a.x_per_row,
+                        a.ids, a.t, a.top_k, a.dst, a.top_k, 0};
+        return launch_mv_f32(dtype, f, s);
+    }
     switch (dtype) {
     case kQ4_K: MX_TRY(launch_mv_dt<kQ4_K>(a, grid, s)); break;
     case kQ5_K: MX_TRY(launch_mv_dt<kQ5_K>(a, grid, s)); break;
@@ -639,7 +702,7 @@ mx_status launch_mul_mv_id(int dtype, const MvArgs &a, hipStream_t s) {
 // are launched in the next kernel, which reads them.  The shared expert's
 // blocks need no routing, so they fill the machine while the selection runs.
 #ifndef MX_GU_WPE
-#define MX_GU_WPE 6
+#define MX_GU_WPE 5
 #endif
 template <int DT, int NG, bool GM>
 __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(MX_GU_WPE))) k_decode_gate_up(DecodeGateUpArgs a, int ni, int slot0, int nslot,
@@ -764,105 +827,64 @@ mx_status launch_decode_gate_up(int dtype, const DecodeGateUpArgs &a, int slot0,
     return MX_OK;
 }
 
-// ---- fused decode: down (one slot per block) + last-block weighted combine ---------------
-// grid (hidden / (WAVES_DN * RW_DN), n_slot_blocks, t).  Each block writes its slot's
-// down rows to part[tok, slot, :]; the last of the n_slot_blocks blocks of a
-// (tok, row tile) to finish (device-scope counter) combines them in slot order:
-//   out[c] = residual[c] + ( sum_k w[k] * part[k][c] + part[shared][c] )
-// (combine.metal:70-97, moe.rs:73-78, model.rs:351) and resets the counter.  When
-// the shared expert has another quant type than the routed experts, the host
-// computes it separately and passes it as a.shared_out (a.sh_down == NULL).
+// ---- fused decode: down (one slot per block), then the combine kernel ---------------------
+// grid (hidden / (WAVES_DN * RW_DN), n_slot_blocks, t), or (pairs in expert order,
+// row tiles).  Each block writes its slot's down rows to part[tok, slot, :]; the
+// combine kernel that follows on the stream (the kernel boundary orders the two)
+// forms out[c] = residual[c] + ( sum_k w[k] * part[k][c] + shared[c] )
+// (combine.metal:70-97, moe.rs:73-78, model.rs:351).  The shared expert is
+// part's last slot when it has the routed quant types, else a.shared_out.
 #ifndef MX_DN_WPE
 #define MX_DN_WPE 1
 #endif
 template <int DT, int NG>
 __global__ void __launch_bounds__(64 * WAVES_DN) __attribute__((amdgpu_waves_per_eu(MX_DN_WPE))) k_decode_down(DecodeDownArgs a, int ni) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    __shared__ int s_last;
     const int slots = a.top_k + (a.sh_down ? 1 : 0);
-    int slot, tok, tile, n_tiles;
+    int slot, tok, tile;
     if (a.order) {  // grid (t * slots pairs in expert order, row tiles)
         const int pair = a.order[blockIdx.x];
         tok = pair / slots;
         slot = pair % slots;
         tile = blockIdx.y;
-        n_tiles = gridDim.y;
     } else {  // grid (row tiles, slots, t)
         slot = blockIdx.y;
         tok = blockIdx.z;
         tile = blockIdx.x;
-        n_tiles = gridDim.x;
     }
     constexpr int ROWS_PER_WG = WAVES_DN * RW_DN;
-    const int tile0 = tile * ROWS_PER_WG;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (scalar)
-    const int r0 = tile0 + wave * RW_DN;
+    const int r0 = tile * ROWS_PER_WG + wave * RW_DN;
     const float *xrow = a.act + ((int64_t)tok * slots + slot) * a.ff;
     uint8_t *ring = lds + align16(xstage_bytes(a.ff)) + wave * (RING_DN * ni * 1024);
     XPre xp;
-    if (r0 < a.hidden) {  // wave-uniform; every wave takes part in the staging barrier
-        const uint8_t *wp;
-        int64_t rb;
-        if (slot < a.top_k) {
-            const uint32_t id = a.ids[tok * a.top_k + slot];
-            const int e = id < (uint32_t)a.n_expert ? (int)id : a.n_expert - 1;
-            wp = a.down + (int64_t)e * a.d_expert_bytes;
-            rb = a.d_row_bytes;
-        } else {
-            wp = a.sh_down;
-            rb = a.sh_row_bytes;
-        }
-        const uint8_t *const w[1] = {wp};
-        const Geo<DT> geo(a.ff, DN_FULL);
-        typename Q<DT>::X xs[NG];
-        float *part = a.part + ((int64_t)tok * slots + slot) * a.hidden;
-        stream_rows<DT, NG, BatchDn<NG>::NIT, 1, RING_DN>(w, rb, geo, xs, r0, min(r0 + RW_DN, a.hidden), ring, ni,
-                                                         [&] { stage_pre(xrow, a.ff, xp); },
-                                                         [&] {
-                                                             stage_post(xrow, a.ff, xp, lds);
-                                                             load_xs<DT, NG>(lds, a.ff, geo, xs);
-                                                         },
-                                                 [&](int row, const float (&s)[1]) { st_agent(part + row, s[0]); });
-    } else {
+    if (r0 >= a.hidden) {  // wave-uniform; every wave takes part in the staging barrier
         stage_pre(xrow, a.ff, xp);
         stage_post(xrow, a.ff, xp, lds);
+        return;
     }
-    // publish this block's partial rows (completed agent-coherent stores), then count in
-    drain_vmem();
-    __syncthreads();
-    unsigned *counter = a.counters + (int64_t)tok * n_tiles + tile;
-    if (threadIdx.x == 0) s_last = arrive_last(counter, (unsigned)slots);
-    __syncthreads();
-    if (!s_last) return;
-    const float *wt = a.w + tok * a.top_k;
-    for (int r = threadIdx.x; r < ROWS_PER_WG; r += blockDim.x) {
-        const int c = tile0 + r;
-        if (c >= a.hidden) break;
-        const float *pc = a.part + (int64_t)tok * slots * a.hidden + c;
-        const int64_t o = (int64_t)tok * a.hidden + c;
-        // shared-expert and residual terms are loaded up front with the first chunk
-        const float sh = a.sh_down ? ld_agent(pc + (int64_t)a.top_k * a.hidden) : a.shared_out ? a.shared_out[o] : 0.f;
-        const float res = a.residual ? a.residual[o] : 0.f;
-        float v = 0.f;
-        // slots in chunks of 8: the chunk's loads are all issued before the first
-        // is used (one L2 round trip per chunk instead of one per slot)
-        for (int s0 = 0; s0 < a.top_k; s0 += 8) {
-            float p[8], q[8];
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const int s = s0 + i;
-                p[i] = s < a.top_k ? ld_agent(pc + (int64_t)s * a.hidden) : 0.f;
-                q[i] = s < a.top_k ? wt[s] : 0.f;
-            }
-#pragma unroll
-            for (int i = 0; i < 8; i++)
-                if (s0 + i < a.top_k) v = v + p[i] * q[i];
-        }
-        if (a.sh_down || a.shared_out) v = v + sh;
-        if (a.residual) v = res + v;
-        a.out[o] = v;
+    const uint8_t *wp;
+    int64_t rb;
+    if (slot < a.top_k) {
+        const uint32_t id = a.ids[tok * a.top_k + slot];
+        const int e = id < (uint32_t)a.n_expert ? (int)id : a.n_expert - 1;
+        wp = a.down + (int64_t)e * a.d_expert_bytes;
+        rb = a.d_row_bytes;
+    } else {
+        wp = a.sh_down;
+        rb = a.sh_row_bytes;
     }
-    if (threadIdx.x == 0) reset_counter(counter);
+    const uint8_t *const w[1] = {wp};
+    const Geo<DT> geo(a.ff, DN_FULL);
+    typename Q<DT>::X xs[NG];
+    float *part = a.part + ((int64_t)tok * slots + slot) * a.hidden;
+    stream_rows<DT, NG, BatchDn<NG>::NIT, 1, RING_DN>(w, rb, geo, xs, r0, min(r0 + RW_DN, a.hidden), ring, ni,
+                                                     [&] { stage_pre(xrow, a.ff, xp); },
+                                                     [&] {
+                                                         stage_post(xrow, a.ff, xp, lds);
+                                                         load_xs<DT, NG>(lds, a.ff, geo, xs);
+                                                     },
+                                                     [&](int row, const float (&s)[1]) { part[row] = s[0]; });
 }
 
 // ---- fused decode down, one workgroup per (token, row tile) holding every slot ---------
@@ -883,6 +905,12 @@ constexpr int DN_SLOTS_MAX = 12;  // 3 waves per SIMD: 168 VGPRs
 #define MX_NIT_DNS 2
 #endif
 template <int NG> struct BatchDnSlots { static constexpr int NIT = NG == 1 ? BatchDn<1>::NIT : MX_NIT_DNS; };
+// LDS per slot (wave): the staged act row, then the wave's ring in the same bytes
+static_assert(RING_DN == 1, "k_decode_down_slots overlays its ring on the staged row: one batch in flight");
+__host__ __device__ inline size_t dn_slot_area(int ff, int ni) {
+    const size_t xs = align16(xstage_bytes(ff)), ring = (size_t)ni * 1024;
+    return xs > ring ? xs : ring;
+}
 constexpr int XPRE_W = 4;  // act quarters per lane held in registers before the weight copies
 template <int DT, int NG>
 __global__ void __launch_bounds__(64 * DN_SLOTS_MAX) k_decode_down_slots(DecodeDownArgs a, int ni) {
@@ -892,9 +920,10 @@ __global__ void __launch_bounds__(64 * DN_SLOTS_MAX) k_decode_down_slots(DecodeD
     const int slot = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int tok = blockIdx.y;
     const int r0 = blockIdx.x * RW_DN, r1 = min(r0 + RW_DN, a.hidden);
-    const int xs_bytes = (int)align16(xstage_bytes(a.ff));
-    uint8_t *xs_lds = lds + slot * (xs_bytes + RING_DN * ni * 1024);
-    uint8_t *ring = xs_lds + xs_bytes;
+    // the slot's staged row is read into registers before the first weight copy,
+    // so the ring reuses its LDS (dn_slot_area)
+    uint8_t *xs_lds = lds + (size_t)slot * dn_slot_area(a.ff, ni);
+    uint8_t *ring = xs_lds;
     const float *xrow = a.act + ((int64_t)tok * slots + slot) * a.ff;
     XPreT<XPRE_W> xp;
     const uint8_t *wp;
@@ -916,6 +945,7 @@ __global__ void __launch_bounds__(64 * DN_SLOTS_MAX) k_decode_down_slots(DecodeD
                                                      [&] {
                                                          stage_post_t(xrow, a.ff, xp, xs_lds, lane, 64);
                                                          load_xs<DT, NG>(xs_lds, a.ff, geo, xs);
+                                                         wait_lgkmcnt0();  // before the ring overwrites it
                                                      },
                                                      [&](int row, const float (&v)[1]) { s_part[slot][row - r0] = v[0]; });
     __syncthreads();
@@ -938,7 +968,7 @@ static mx_status launch_dn_slots_ng(const DecodeDownArgs &a, hipStream_t s) {
     const int ni = ring_insts<DT, NG>(1, a.ff, a.d_row_bytes, BatchDnSlots<NG>::NIT, DN_FULL);
     if (ni > DMA_MAX_INSTS) return fail(MX_ERR_SHAPE, "decode down: rows too long for the LDS ring");
     const int slots = a.top_k + (a.sh_down ? 1 : 0);
-    const size_t lds = (size_t)slots * (align16(xstage_bytes(a.ff)) + (size_t)RING_DN * ni * 1024);
+    const size_t lds = (size_t)slots * dn_slot_area(a.ff, ni);
     const dim3 grid((unsigned)((a.hidden + RW_DN - 1) / RW_DN), (unsigned)a.t);
     hipLaunchKernelGGL((k_decode_down_slots<DT, NG>), grid, dim3(64 * slots), lds, s, a, ni);
     return MX_OK;
@@ -949,7 +979,7 @@ static size_t dn_slots_lds(const DecodeDownArgs &a) {
     const int ni = ring_insts<DT, NG>(1, a.ff, a.d_row_bytes, BatchDnSlots<NG>::NIT, DN_FULL);
     if (ni > DMA_MAX_INSTS) return SIZE_MAX;
     const int slots = a.top_k + (a.sh_down ? 1 : 0);
-    return (size_t)slots * (align16(xstage_bytes(a.ff)) + (size_t)RING_DN * ni * 1024);
+    return (size_t)slots * dn_slot_area(a.ff, ni);
 }
 // true when the slot-per-wave kernel takes this launch
 template <int DT>
@@ -993,10 +1023,6 @@ static mx_status launch_dn_dt(const DecodeDownArgs &a, dim3 grid, hipStream_t s)
     return MX_OK;
 }
 
-size_t decode_down_counter_words(int t, int hidden) {
-    return (size_t)t * (size_t)((hidden + WAVES_DN * RW_DN - 1) / (WAVES_DN * RW_DN));
-}
-
 mx_status launch_decode_down(int dtype, const DecodeDownArgs &a, hipStream_t s) {
     const unsigned tiles = (unsigned)((a.hidden + WAVES_DN * RW_DN - 1) / (WAVES_DN * RW_DN));
     const unsigned slots = (unsigned)(a.top_k + (a.sh_down ? 1 : 0));
@@ -1029,7 +1055,8 @@ mx_status launch_decode_down(int dtype, const DecodeDownArgs &a, hipStream_t s) 
     default: MX_TRY(launch_dn_dt<kQ8_0>(a, grid, s)); break;
     }
     MX_LAUNCH("k_decode_down");
-    return MX_OK;
+    return launch_combine_prefill(a.part, a.w, a.residual, a.t, a.top_k, a.sh_down ? 1 : 0, a.hidden, a.out, s,
+                                  a.shared_out);
 }
 
 // ---- (token, slot) pairs in expert order (small-batch verify) --------------------------

@@ -1,14 +1,21 @@
 // Staged activations: the integer form in which the decode kernels consume an
 // activation row (x for gate/up, the SwiGLU output for down).
 //
-// Per 32-value group g of a k-vector (k % 32 == 0):
-//   s_g  = max|x| / 32000                      (f32)
-//   x16  = rint(x / s_g) in [-32000, 32000]    (exact integer grid)
-//   x16  = 256 * xh + xl, xh and xl signed int8 (xl in [-128, 127])
-// stored as two byte planes so four consecutive values form one dword for
-// v_dot4_i32_i8, plus the integer sums of x16 over every 8 and every 32 values
-// (the Q4_K "min" term and the Q6_K "-32" offset are applied from them).
-// Layout (bytes): xh[k] | xl[k] | s[k/32] f32 | S32[k/32] i32 | S8[k/8] i32.
+// Per 32-value group g of a k-vector (k % 32 == 0), with m = max|x| over g:
+//   s_g = 2^e, e = frexp_exp(m) - 23 (+1 if m / 2^e > X24_MAX), e >= -149
+//   x24 = rint(x / s_g), an integer in [-2^23, X24_MAX]
+//   x24 = 65536 * xh + 256 * xm + xl, three signed int8 digits in [-128, 127]
+// The scale is a power of two, so x / s_g is exact and s_g * x24 is the
+// represented value exactly; the only error is the rint:
+//   |s_g * x24 - x| <= s_g / 2 <= 2^-23 * (1 + 2^-8) * m
+// i.e. every value is carried to within ~2 f32 ulps of its group's largest
+// magnitude (a 24-bit grid, the width of an f32 significand).  Values whose
+// magnitude is within 2^-1 of m keep their f32 value to within one ulp of
+// their own; smaller values keep 24 bits below m.
+// Stored as three byte planes so four consecutive values form one dword for
+// v_dot4_i32_i8, plus the integer sum of x24 over every 32 values (the Q4_K
+// "min" term is applied from it).
+// Layout (bytes): xh[k] | xm[k] | xl[k] | s[k/32] f32 | S32[k/32] i32.
 // The same layout is used in LDS (per-workgroup staging) and in global memory
 // (staged once per layer by the router kernel).
 #pragma once
@@ -17,90 +24,119 @@
 
 namespace mx {
 
-constexpr float XQ_RANGE = 32000.0f;
+// largest x24 whose three balanced digits all fit int8: 127 * (65536 + 256 + 1)
+constexpr int X24_MAX = 8355711;
 
-__host__ __device__ constexpr int xstage_bytes(int k) { return 2 * k + (k / 32) * 8 + (k / 8) * 4; }
+__host__ __device__ constexpr int xstage_bytes(int k) { return 3 * k + (k / 32) * 8; }
 // distance between staged rows in a buffer of several (256-byte aligned, so
 // every row can be copied with aligned 16-byte pieces)
 __host__ __device__ constexpr int xstage_stride(int k) { return (xstage_bytes(k) + 255) & ~255; }
 
 struct XView {
-    const int8_t *xh, *xl;
+    const int8_t *xh, *xm, *xl;
     const float *s;
-    const int *S32, *S8;
+    const int *S32;
     __device__ XView(const uint8_t *base, int k)
-        : xh(reinterpret_cast<const int8_t *>(base)), xl(reinterpret_cast<const int8_t *>(base) + k),
-          s(reinterpret_cast<const float *>(base + 2 * k)),
-          S32(reinterpret_cast<const int *>(base + 2 * k) + k / 32),
-          S8(reinterpret_cast<const int *>(base + 2 * k) + 2 * (k / 32)) {}
+        : xh(reinterpret_cast<const int8_t *>(base)), xm(reinterpret_cast<const int8_t *>(base) + k),
+          xl(reinterpret_cast<const int8_t *>(base) + 2 * k), s(reinterpret_cast<const float *>(base + 3 * k)),
+          S32(reinterpret_cast<const int *>(base + 3 * k) + k / 32) {}
 };
 
 // Group-major copy for 64-value groups (the Q4_K / Q5_K decode geometry, in
-// which lane g of a row reads values 64g .. 64g+63): group g has 9 16-byte
+// which lane g of a row reads values 64g .. 64g+63): group g has 13 16-byte
 // chunks and chunk c of every group is stored together, at byte (c * G + g) * 16
-// with G = k / 64.  Chunks 0-3: xh[64g, 64g+64); 4-7: xl[64g, 64g+64); 8: f32
+// with G = k / 64.  Chunks 0-3: xh[64g, 64g+64); 4-7: xm; 8-11: xl; 12: f32
 // {s[2g], s[2g+1], s[2g] * S32[2g], s[2g+1] * S32[2g+1]}.  A wave then reads its
-// slices with 9 loads of 1 KB of consecutive bytes each, instead of 16-byte
+// slices with 13 loads of 1 KB of consecutive bytes each, instead of 16-byte
 // pieces 64 bytes apart (which made every load instruction touch ~32 lines).
-__host__ __device__ constexpr int xstage_gm_bytes(int k) { return (k / 64) * 144; }
+constexpr int GM_CHUNKS = 13;
+__host__ __device__ constexpr int xstage_gm_bytes(int k) { return (k / 64) * 16 * GM_CHUNKS; }
 __host__ __device__ constexpr int xstage_gm_stride(int k) { return (xstage_gm_bytes(k) + 255) & ~255; }
+
+// Exponent e of a group's power-of-two scale for its largest magnitude m
+// (m finite, > 0): m / 2^e lies in [2^22, X24_MAX].
+__device__ __forceinline__ int x24_exponent(float m) {
+    int e = __builtin_amdgcn_frexp_expf(m) - 23;  // m = f * 2^(e + 23), f in [0.5, 1)
+    if (e < -149) e = -149;                         // below: absolute error <= 2^-150
+    if (__builtin_amdgcn_ldexpf(m, -e) > (float)X24_MAX) e += 1;
+    return e;
+}
+
+// Splits x24 in [-2^23, X24_MAX] into balanced base-256 digits h, m, l.
+__device__ __forceinline__ void x24_digits(int v, int &h, int &m, int &l) {
+    l = ((v + 128) & 255) - 128;
+    const int r = (v - l) >> 8;
+    m = ((r + 128) & 255) - 128;
+    h = (r - m) >> 8;
+}
 
 // Quantises quarter-group q (values 8q .. 8q+7, given in v) into the staged
 // layout at `base` (and, when gm != NULL and k % 64 == 0, into the group-major
 // copy at gm).  The four quarters of a group must sit in four consecutive
 // lanes (4m .. 4m+3) of one wave, and all four lanes must call this together
 // (cross-lane max and sum); `valid` = false lanes contribute nothing and store
-// nothing.
+// nothing.  A group holding Inf or NaN gets a NaN scale, so it poisons the
+// rows that read it, as f32 arithmetic would.
 __device__ __forceinline__ void stage_quarter(const float (&v)[8], int q, bool valid, uint8_t *base, int k,
                                               uint8_t *gm = nullptr) {
     float mx = 0.f;
     if (valid) {
 #pragma unroll
         for (int i = 0; i < 8; i++) mx = fmaxf(mx, fabsf(v[i]));
+        // fmaxf drops NaN: carry it explicitly
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            if (v[i] != v[i]) mx = __builtin_inff();
     }
     mx = fmaxf(mx, lane_partner<1>(mx));
     mx = fmaxf(mx, lane_partner<2>(mx));
-    const float inv = mx > 0.f ? XQ_RANGE / mx : 0.f;
-    uint32_t h[2], l[2];
+    const bool finite = mx < __builtin_inff();
+    const bool nz = finite && mx > 0.f;
+    const int e = nz ? x24_exponent(mx) : 0;
+    uint32_t h[2], m[2], l[2];
     int s8 = 0;
 #pragma unroll
     for (int w = 0; w < 2; w++) {
-        uint32_t hw = 0, lw = 0;
+        uint32_t hw = 0, mw = 0, lw = 0;
 #pragma unroll
         for (int b = 0; b < 4; b++) {
-            const int xq = valid ? (int)rintf(v[4 * w + b] * inv) : 0;
-            const int hd = (xq + 128) >> 8;
-            const int ld = xq - (hd << 8);
+            const int xq = (valid && nz) ? (int)rintf(__builtin_amdgcn_ldexpf(v[4 * w + b], -e)) : 0;
+            int hd, md, ld;
+            x24_digits(xq, hd, md, ld);
             s8 += xq;
             hw |= ((uint32_t)hd & 0xFFu) << (8 * b);
+            mw |= ((uint32_t)md & 0xFFu) << (8 * b);
             lw |= ((uint32_t)ld & 0xFFu) << (8 * b);
         }
         h[w] = hw;
+        m[w] = mw;
         l[w] = lw;
     }
     int s32 = s8 + __float_as_int(lane_partner<1>(__int_as_float(s8)));
     s32 = s32 + __float_as_int(lane_partner<2>(__int_as_float(s32)));
+    const float sg = !finite ? __builtin_nanf("") : nz ? __builtin_amdgcn_ldexpf(1.0f, e) : 0.f;
     if (valid) {
         int8_t *xh = reinterpret_cast<int8_t *>(base);
-        int8_t *xl = xh + k;
-        float *s = reinterpret_cast<float *>(base + 2 * k);
+        int8_t *xm = xh + k;
+        int8_t *xl = xh + 2 * k;
+        float *s = reinterpret_cast<float *>(base + 3 * k);
         int *S32 = reinterpret_cast<int *>(s + k / 32);
-        int *S8 = S32 + k / 32;
         *reinterpret_cast<uint2 *>(xh + 8 * q) = make_uint2(h[0], h[1]);
+        *reinterpret_cast<uint2 *>(xm + 8 * q) = make_uint2(m[0], m[1]);
         *reinterpret_cast<uint2 *>(xl + 8 * q) = make_uint2(l[0], l[1]);
-        S8[q] = s8;
         if ((q & 3) == 0) {
-            s[q >> 2] = mx / XQ_RANGE;
+            s[q >> 2] = sg;
             S32[q >> 2] = s32;
         }
         if (gm) {
             const int G = k / 64, g = q >> 3, cq = q & 7;
-            *reinterpret_cast<uint2 *>(gm + ((size_t)(cq >> 1) * G + g) * 16 + (cq & 1) * 8) = make_uint2(h[0], h[1]);
-            *reinterpret_cast<uint2 *>(gm + ((size_t)(4 + (cq >> 1)) * G + g) * 16 + (cq & 1) * 8) = make_uint2(l[0], l[1]);
+            const size_t half = (size_t)(cq & 1) * 8;
+            *reinterpret_cast<uint2 *>(gm + ((size_t)(cq >> 1) * G + g) * 16 + half) = make_uint2(h[0], h[1]);
+            *reinterpret_cast<uint2 *>(gm + ((size_t)(4 + (cq >> 1)) * G + g) * 16 + half) = make_uint2(m[0], m[1]);
+            *reinterpret_cast<uint2 *>(gm + ((size_t)(8 + (cq >> 1)) * G + g) * 16 + half) = make_uint2(l[0], l[1]);
             if ((q & 3) == 0) {
-                float *sc = reinterpret_cast<float *>(gm + ((size_t)8 * G + g) * 16);
+                float *sc = reinterpret_cast<float *>(gm + ((size_t)12 * G + g) * 16);
                 const int par = (q >> 2) & 1;
-                const float sg = mx / XQ_RANGE;
                 sc[par] = sg;
                 sc[2 + par] = sg * (float)s32;
             }

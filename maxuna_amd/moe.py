@@ -128,7 +128,8 @@ class MoeBlock:
     def workspace(self, t: int, device) -> torch.Tensor:
         need = lib().mx_moe_workspace_bytes(C.byref(self._c), t)
         if self._ws is None or self._ws.numel() < need:
-            # zeroed once: the fused router keeps a self-resetting counter in it
+            # no state lives in the workspace between calls (every forward
+            # initialises what it reads); zeroed only for tidiness
             self._ws = torch.zeros(max(need, 256), dtype=torch.uint8, device=device)
         return self._ws
 

@@ -71,7 +71,28 @@ def _u32(t: torch.Tensor, name: str) -> torch.Tensor:
 
 def supported(dtype: GgmlDType, top_k: int) -> bool:
     """Whether the grouped-GEMM path has kernels for this dtype/top_k (mm_id.rs:48-50)."""
-    return dtype in (GgmlDType.Q4_K, GgmlDType.Q6_K, GgmlDType.Q8_0) and 1 <= top_k <= 64
+    return dtype in (GgmlDType.Q4_K, GgmlDType.Q5_K, GgmlDType.Q6_K, GgmlDType.Q8_0) and 1 <= top_k <= 64
+
+
+IDS_DUPLICATE = 1
+IDS_OUT_OF_RANGE = 2
+
+
+def check_ids(ids: torch.Tensor, n_expert: int, raise_on_error: bool = True) -> int:
+    """Device-side validation of routing ids (mx_check_ids): the flag word,
+    IDS_DUPLICATE | IDS_OUT_OF_RANGE.  Synchronises with the device; with
+    raise_on_error a non-zero flag raises MaxunaError (fail-closed, as the
+    reference's host validation is, dispatch.rs:812-847)."""
+    _u32(ids, "ids")
+    t, top_k = ids.shape
+    flags = torch.empty(1, dtype=torch.int32, device=ids.device)
+    check(lib().mx_check_ids(ids.data_ptr(), t, top_k, n_expert, flags.data_ptr(), _stream()))
+    f = int(flags.item())
+    if f and raise_on_error:
+        what = [n for b, n in ((IDS_DUPLICATE, "a token repeats an expert id"),
+                               (IDS_OUT_OF_RANGE, f"an expert id >= n_expert ({n_expert})")) if f & b]
+        raise MaxunaError(2, "invalid routing ids: " + "; ".join(what))
+    return f
 
 
 def mul_mv_id(stack: ExpertStack, x: torch.Tensor, ids: torch.Tensor) -> torch.Tensor:
