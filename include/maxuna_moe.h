@@ -235,6 +235,22 @@ mx_status mx_moe_forward(const mx_moe_layer *layer, const float *x, int64_t t,
                          const float *residual, float *out, uint32_t *ids_out, float *w_out,
                          void *workspace, size_t workspace_bytes, mx_stream_t stream);
 
+/* mx_moe_forward with no workspace argument and no allocation of any kind.  No
+ * counterpart in the reference: it is for callers that cannot allocate (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  The workspace is a device array inside the library,
+ * mx_moe_forward_noalloc_max_bytes() = 16 MiB per GPU, held by every GPU the
+ * library runs on until the process ends.  A call whose t needs more
+ * (mx_moe_workspace_bytes) fails with MX_ERR_SCRATCH before any launch; a
+ * C1-shaped layer (hidden 4096, 256 experts, top-10 + shared) fits up to
+ * t = 57.  Calls on one GPU share that array: calls that overlap on one GPU
+ * (different streams, or different host threads) race; order them on one
+ * stream.  Nothing in the array needs clearing between calls. */
+size_t mx_moe_forward_noalloc_max_bytes(void);
+mx_status mx_moe_forward_noalloc(const mx_moe_layer *layer, const float *x, int64_t t,
+                                 const float *residual, float *out, uint32_t *ids_out, float *w_out,
+                                 mx_stream_t stream);
+
 /* Same as mx_moe_forward, and additionally records a HIP event after each
  * stage on `stream`, waits for the last one and returns the stage durations
  * in milliseconds.  Decode (t < mm_min_seq): router logits, top-k (t <= 32;

@@ -109,6 +109,8 @@ SIGNATURES = {
     "mx_route_from_logits": (I32, [P, P, I64, I64, I64, F64, I32, P, P, P]),
     "mx_moe_workspace_bytes": (SZ, [C.POINTER(MoeLayerC), I64]),
     "mx_moe_forward": (I32, [C.POINTER(MoeLayerC), P, I64, P, P, P, P, P, SZ, P]),
+    "mx_moe_forward_noalloc": (I32, [C.POINTER(MoeLayerC), P, I64, P, P, P, P, P]),
+    "mx_moe_forward_noalloc_max_bytes": (SZ, []),
     "mx_moe_forward_profiled": (I32, [C.POINTER(MoeLayerC), P, I64, P, P, P, P, P, SZ, P, P, I32, P]),
     "mx_moe_forward_repeat": (I32, [C.POINTER(MoeLayerC), P, I64, P, P, P, P, P, SZ, P, I32, I32]),
     "mx_tensor_key": (U64, [U64, U32, U32]),

@@ -4,9 +4,15 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 
 #include "mx_launch.h"
 #include "mx_stage.h"
+
+// bytes of the device-resident workspace of mx_moe_forward_noalloc (per device)
+#ifndef MX_NOALLOC_SCRATCH_BYTES
+#define MX_NOALLOC_SCRATCH_BYTES (16u << 20)
+#endif
 
 // decode: the shared expert's gate/up rides in the top-k launch (1) or with the
 // routed slots (0)
@@ -732,6 +738,58 @@ mx_status mx_moe_forward_repeat(const mx_moe_layer *L, const float *x, int64_t t
     rep.times = times;
     return moe_forward_impl(L, x, t, residual, out, ids_out, w_out, workspace, workspace_bytes, (hipStream_t)stream,
                             nullptr, rep);
+}
+
+}  // extern "C"
+
+// ---- the forward that allocates nothing --------------------------------------------------
+// A file-scope device array serves as the workspace.  In host code its name is
+// only a stand-in: the device address comes from hipGetSymbolAddress, once per
+// device (each GPU holds its own copy at its own address), and only that address
+// is ever passed to kernels.  The forward keeps no state in its workspace (every
+// call initialises what it reads), so nothing needs clearing between calls.
+namespace {
+constexpr size_t kNoAllocScratchBytes = (size_t)MX_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+mx_status scratch_for_current_device(void **out) {
+    int dev = -1;
+    MX_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) return fail(MX_ERR_SHAPE, "no-alloc forward: device %d out of range", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        MX_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (!p) return fail(MX_ERR_HIP, "no-alloc forward: no device address for the scratch array");
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return MX_OK;
+}
+}  // namespace
+
+extern "C" {
+
+size_t mx_moe_forward_noalloc_max_bytes(void) { return kNoAllocScratchBytes; }
+
+mx_status mx_moe_forward_noalloc(const mx_moe_layer *L, const float *x, int64_t t, const float *residual, float *out,
+                                 uint32_t *ids_out, float *w_out, mx_stream_t stream) {
+    StackGeom gg, gu, gd, sg{}, su{}, sd{};
+    MX_TRY(check_layer(L, t, gg, gu, gd, sg, su, sd));
+    const size_t need = mx_moe_workspace_bytes(L, t);
+    if (need > kNoAllocScratchBytes)
+        return fail(MX_ERR_SCRATCH,
+                    "no-alloc forward: t = %lld needs %zu bytes of workspace, its scratch holds %zu "
+                    "(use mx_moe_forward with a caller workspace)",
+                    (long long)t, need, kNoAllocScratchBytes);
+    if (t == 0) return MX_OK;
+    void *ws = nullptr;
+    MX_TRY(scratch_for_current_device(&ws));
+    return moe_forward_impl(L, x, t, residual, out, ids_out, w_out, ws, kNoAllocScratchBytes, (hipStream_t)stream,
+                            nullptr);
 }
 
 uint64_t mx_tensor_key(uint64_t seed, uint32_t layer, uint32_t tensor_id) {

@@ -155,3 +155,21 @@ class MoeBlock:
                                    out.data_ptr(), ids.data_ptr(), w.data_ptr(), ws.data_ptr(),
                                    ws.numel(), ops._stream()))
         return (out, ids, w) if return_routing else out
+
+    def forward_noalloc(self, x: torch.Tensor, residual: torch.Tensor | None = None,
+                        out: torch.Tensor | None = None, return_routing: bool = False):
+        """`forward` through mx_moe_forward_noalloc: the library's own device-resident
+        scratch is the workspace (no allocation by the call, for callers that cannot
+        allocate); MaxunaError if this t needs more than that scratch holds.  Calls
+        that overlap on one GPU share the scratch and race."""
+        if x.dtype != torch.float32 or x.dim() != 2 or not x.is_contiguous():
+            raise ops.MaxunaError(2, "x must be a contiguous f32 [t, hidden] tensor")
+        t = x.shape[0]
+        if out is None:
+            out = torch.empty_like(x)
+        ids = torch.empty((t, self.cfg.n_expert_used), dtype=torch.uint32, device=x.device)
+        w = torch.empty((t, self.cfg.n_expert_used), dtype=torch.float32, device=x.device)
+        check(lib().mx_moe_forward_noalloc(C.byref(self._c), x.data_ptr(), t,
+                                           residual.data_ptr() if residual is not None else None,
+                                           out.data_ptr(), ids.data_ptr(), w.data_ptr(), ops._stream()))
+        return (out, ids, w) if return_routing else out

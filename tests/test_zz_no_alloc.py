@@ -1,0 +1,43 @@
+"""mx_moe_forward_noalloc (the forward whose workspace is the library's own
+device-resident scratch) against mx_moe_forward with a caller workspace: same
+kernels, so outputs, ids and weights must be identical bit for bit, on two
+calls in a row (the second with fewer tokens, so it reads scratch the first
+left behind), with and without an in-place residual."""
+import numpy as np
+import pytest
+import torch
+
+from maxuna_amd import ops
+from maxuna_amd._lib import lib
+from maxuna_amd.synth import CONFIGS, build_layer, make_x
+from tests.gpu_util import dev_f32, host
+
+pytestmark = pytest.mark.gpu
+
+
+def test_noalloc_forward_matches_workspace_forward(dev):
+    spec = CONFIGS["C2"]["spec"]
+    layer = build_layer(spec, seed=1303, rms=True)
+    blk = layer.block
+    for t, seed in ((16, 1), (3, 2), (1, 3)):
+        print(f"no-alloc t={t}", flush=True)
+        x = dev_f32(make_x(spec, 500 + seed, t))
+        want, wid, ww = blk.forward(x, return_routing=True)
+        got, gid, gw = blk.forward_noalloc(x, return_routing=True)
+        assert np.array_equal(host(got).view(np.uint32), host(want).view(np.uint32)), f"t={t}: out"
+        assert np.array_equal(host(gid), host(wid)), f"t={t}: ids"
+        assert np.array_equal(host(gw).view(np.uint32), host(ww).view(np.uint32)), f"t={t}: w"
+        # in-place residual update, as the decoder chain uses it
+        r1, r2 = x.clone(), x.clone()
+        blk.forward(x, residual=r1, out=r1)
+        blk.forward_noalloc(x, residual=r2, out=r2)
+        assert np.array_equal(host(r1).view(np.uint32), host(r2).view(np.uint32)), f"t={t}: residual"
+
+
+def test_noalloc_rejects_oversized_t(dev):
+    spec = CONFIGS["C3"]["spec"]
+    layer = build_layer(spec, seed=1304)
+    assert lib().mx_moe_forward_noalloc_max_bytes() == 16 << 20
+    x = dev_f32(make_x(spec, 600, 512))
+    with pytest.raises(ops.MaxunaError, match="no-alloc forward: t = 512 needs"):
+        layer.block.forward_noalloc(x)
