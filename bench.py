@@ -1,14 +1,14 @@
 """Benchmark of the quantized indexed-MoE hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps 400] [--warmup 40]
+    python bench.py [--gpus 1] [--steps 50] [--warmup 5]
 
 Workload (0-indexed):
   decode  C1: Laguna-shaped MoE layer, batch 1 (H=4096, FF=1536, 256 experts,
-          top-10 + shared, gate/up Q4_K, down Q6_K).  One step = one layer
-          forward (router + 10 routed experts + shared expert + combine).
-          Steps rotate over --layers distinct seeded layers (>= 1 GB of touched
-          weights per rotation) so the 256 MB Infinity Cache cannot serve
-          repeats; the rotation is captured once as a HIP graph and replayed.
+          top-10 + shared, gate/up Q4_K, down Q6_K).  One step = one forward
+          (router + 10 routed experts + shared expert + combine) of each of
+          --layers distinct seeded layers (>= 1 GB of touched weights per step,
+          so the 256 MB Infinity Cache cannot serve repeats); the step is
+          captured once as a HIP graph and replayed, exactly --steps times.
   prefill C3: the same layer at t = 2048 with a skewed selection bias (grouped
           expert GEMM), reported as TFLOP/s.
 `value` is decode HBM throughput: algorithmic bytes (each touched weight byte
@@ -129,29 +129,31 @@ def bench_decode(args):
         b, u = layer_bytes(spec, ids.view(torch.int32).cpu().numpy(), 1)
         tot_bytes += b
         uniq.append(u)
-    bytes_per_step = tot_bytes / L
-    # capture the rotation once; replay it
+    bytes_per_layer = tot_bytes / L
+    # capture the rotation once; one step = one replay (one forward of each of the
+    # L layers), so K steps time K * L layer forwards
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         for i in range(L):
             layers[i].block.forward(xs[i], out=outs[i])
-    for _ in range(3):
+    warm = max(args.warmup, -(-30 // L))  # at least 30 layer forwards before timing
+    for _ in range(warm):
         g.replay()
-    torch.cuda.synchronize()
-    replays = max(1, (args.steps + L - 1) // L)
-    steps = replays * L
+    steps = args.steps
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     start.record()
-    for _ in range(replays):
+    for _ in range(steps):
         g.replay()
     end.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    ms = start.elapsed_time(end) / steps
-    gbs = bytes_per_step / (ms * 1e-3) / 1e9
-    log(f"decode: {steps} steps, {ms * 1e3:.2f} us/layer, {gbs:.0f} GB/s (wall {wall * 1e3:.1f} ms)")
+    ms_step = start.elapsed_time(end) / steps
+    ms = ms_step / L
+    gbs = bytes_per_layer / (ms * 1e-3) / 1e9
+    log(f"decode: {steps} steps x {L} layers, {ms * 1e3:.2f} us/layer, {gbs:.0f} GB/s (wall {wall * 1e3:.1f} ms)")
+    replays = max(steps, 8)
     # per-kernel time inside the replayed pipeline: the plain rotation minus the
     # rotation with one stage's kernel left out (HIP events on the stream).  Leaving
     # a launch out, unlike launching it twice, keeps every weight byte an HBM read.
@@ -179,9 +181,9 @@ def bench_decode(args):
             "traffic": measured_traffic().get(dom), "bytes_per_launch": dbytes, "launch_us": round(dms * 1e3, 2)}
     stage_us = {"route_logits": st[0] * 1e3, "topk": st[1] * 1e3, "gate_up": st[2] * 1e3,
                 "down": st[3] * 1e3, "eager_events": [round(v * 1e3, 2) for v in eager]}
-    return dict(ms_per_step=ms, steps=steps, gbs=gbs, bytes_per_step=bytes_per_step, uniq=uniq,
-                stage_us=stage_us, roofline=roof,
-                layers=layers)
+    return dict(ms_per_layer=ms, ms_per_step=ms_step, steps=steps, warm_layers=warm * L, gbs=gbs,
+                bytes_per_layer=bytes_per_layer, bytes_per_step=bytes_per_layer * L, uniq=uniq,
+                stage_us=stage_us, roofline=roof, layers=layers)
 
 
 def bench_prefill(args):
@@ -246,7 +248,7 @@ def bench_verify(args, dec):
         tot += b
         uniq.append(u)
     us = graph_us(lambda: [layers[i].block.forward(xs[i], out=outs[i]) for i in range(L)],
-                  max(4, args.steps // (4 * L))) / L
+                  max(8, args.steps // 2)) / L
     gbs = tot / L / (us * 1e-6) / 1e9
     log(f"verify C2 (t={t}): {us:.1f} us/block, {gbs:.0f} GB/s, {sum(uniq) / L:.0f} unique experts")
     return {"workload": "C2 verify block, t=16, top-10 of 256 + shared", "us_per_block": round(us, 2),
@@ -278,7 +280,7 @@ def bench_chain(args):
         for lay in layers:
             lay.block.forward(x, residual=x, out=x)
 
-    us = graph_us(step, max(3, args.steps // 100))
+    us = graph_us(step, max(5, args.steps // 10))
     gbs = tot / (us * 1e-6) / 1e9
     log(f"chain C4: {us / 1e3:.3f} ms/step over {n} layers, {gbs:.0f} GB/s")
     del layers
@@ -300,12 +302,22 @@ def bench_lm_head(args):
     ws = [synth_stack(GgmlDType.Q6_K, 1, n_out, k, key=9000 + i) for i in range(copies)]
     x = torch.randn(1, k, device="cuda")
     us = graph_us(lambda: [ops.mul_mv(w.buffer, GgmlDType.Q6_K, n_out, k, x) for w in ws],
-                  max(4, args.steps // 16)) / copies
+                  max(16, args.steps)) / copies
     nbytes = ws[0].nbytes + k * 4 + n_out * 4
     gbs = nbytes / (us * 1e-6) / 1e9
     log(f"lm_head Q6_K [{n_out} x {k}]: {us:.1f} us, {gbs:.0f} GB/s")
     return {"workload": "plain mat-vec Q6_K [100352 x 3072], t=1 (mul_mv, lm_head shape)", "us": round(us, 2),
             "hbm_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": int(nbytes)}
+
+
+def cpu_model() -> str:
+    try:
+        for ln in open("/proc/cpuinfo"):
+            if ln.startswith("model name"):
+                return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def cpu_baseline(args, dec):
@@ -345,9 +357,10 @@ def cpu_baseline(args, dec):
         if el > args.cpu_seconds or reps >= 200:
             break
     s_per = el / reps
-    gbs = dec["bytes_per_step"] / s_per / 1e9
+    gbs = dec["bytes_per_layer"] / s_per / 1e9
     log(f"cpu baseline: {reps} layers in {el:.1f} s -> {s_per * 1e3:.1f} ms/layer, {gbs:.2f} GB/s")
     return {"value": round(gbs, 3), "unit": "GB/s", "cores": orc.lib().or_num_threads(), "kind": "port",
+            "cpu_model": cpu_model(),
             "sample": f"{reps} C1 decode layers (t=1; routing + 10 routed experts + shared; selected experts "
                       f"pre-generated), {s_per * 1e6:.0f} us/layer",
             "us_per_layer": round(s_per * 1e6, 1)}
@@ -356,8 +369,9 @@ def cpu_baseline(args, dec):
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=400)
-    ap.add_argument("--warmup", type=int, default=40)
+    ap.add_argument("--steps", type=int, default=50,
+                    help="timed steps; one step = one forward of each of the --layers decode layers")
+    ap.add_argument("--warmup", type=int, default=5, help="untimed steps first (at least 30 layer forwards)")
     ap.add_argument("--layers", type=int, default=8, help="distinct decode layers in the rotation")
     ap.add_argument("--prefill-steps", type=int, default=10)
     ap.add_argument("--profile-iters", type=int, default=32)
@@ -411,13 +425,20 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4_K/q6_K weights, f32 activations and accumulation",
+        "dtype": "q4_K/q6_K weight blocks; activations on a 24-bit grid per 32-value group (power-of-two scale, "
+                 "three int8 digit planes, exact int32 plane sums on v_dot4_i32_i8) recombined and scaled in f32, "
+                 "f32 accumulation",
         "data": "synthetic (seeded GGUF blocks generated on device; x, router ~ N(0,1), N(0,0.02))",
-        "config": {"workload": "C1 decode MoE layer, batch 1", "hidden": 4096, "expert_ff": 1536,
+        "config": {"workload": f"C1 decode MoE layer, batch 1; one step = one forward of each of {args.layers} "
+                               "distinct C1 layers (graph replay)",
+                   "hidden": 4096, "expert_ff": 1536,
                    "n_expert": 256, "top_k": 10, "shared_expert": True, "quant": "gate/up Q4_K, down Q6_K",
                    "rotation_layers": args.layers, "graph_replay": True},
-        "us_per_layer": round(dec["ms_per_step"] * 1e3, 2),
-        "tokens_per_s": round(1e3 / dec["ms_per_step"], 1),
+        "layer_forwards_timed": dec["steps"] * args.layers,
+        "warmup_layer_forwards": dec["warm_layers"],
+        "us_per_layer": round(dec["ms_per_layer"] * 1e3, 2),
+        "tokens_per_s": round(1e3 / dec["ms_per_layer"], 1),
+        "bytes_per_layer": int(dec["bytes_per_layer"]),
         "bytes_per_step": int(dec["bytes_per_step"]),
         "hbm_frac": round(dec["gbs"] / HBM_PEAK_GBS, 4),
         "decode_stage_us": {k: (round(v, 2) if isinstance(v, float) else v) for k, v in dec["stage_us"].items()},

@@ -69,6 +69,10 @@ def build(verbose: bool = True) -> Path:
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stderr}")
+    # every symbol must resolve (a kernel the host pass dropped leaves its launch
+    # stub undefined, which only the dynamic loader reports)
+    import ctypes
+    ctypes.CDLL(os.fspath(tmp), mode=os.RTLD_NOW)
     os.replace(tmp, out)
     if verbose:
         print(f"built {out}")

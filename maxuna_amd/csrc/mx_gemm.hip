@@ -11,12 +11,14 @@
 //    and copied straight into LDS with global_load_lds, 128 K-values per
 //    stage, double-buffered.  16-byte chunks are XOR-swizzled by row so the
 //    MFMA operand reads (16 consecutive rows, same chunk) hit distinct banks.
-//  * B (weights) are read from the raw GGUF blocks into registers, one stage
-//    ahead, and dequantised in registers directly into the MFMA B-operand
-//    layout: f32 dequantisation of the reference's formula, then one
-//    round-to-nearest f16 pack (the reference dequantises into half tiles).
-//    Each wave owns 64 output columns, so no weight is dequantised twice in a
-//    workgroup.
+//  * B (weights): each stage, the raw GGUF bytes the stage needs from every
+//    weight row of the tile are copied into LDS by buffer->LDS DMA (one slot
+//    per row; see WB), in flight with the A copy while the previous stage
+//    computes.  Each lane then reads its own row's slot and dequantises in
+//    registers directly into the MFMA B-operand layout: the reference's
+//    formula in packed f16 arithmetic, one rounding to f16 (the reference
+//    dequantises into half tiles).  Each wave owns 64 (or 32) output
+//    columns, so no weight is dequantised twice in a workgroup.
 //  * v_mfma_f32_32x32x16_f16, f32 accumulation: each wave holds 4 (pairs) x 2
 //    (columns) 32x32 accumulators.
 //
@@ -62,38 +64,11 @@ constexpr int BN = 256;  // weight rows (output columns) per block
 template <int DT, bool SWIGLU> struct GemmNb {
     static constexpr int nb = (SWIGLU || DT == kQ4_K) ? 2 : MX_GEMM_NB_PLAIN;
     // (Q6_K / Q8_0 SwiGLU keep 4 waves: at 8 a workgroup caps them at 256 VGPRs)
-    static constexpr int waves = nb == 2 ? ((DT == kQ4_K || DT == kQ5_K) ? MX_GEMM_WAVES2 : 4) : BN / (32 * nb);
+    static constexpr int waves = nb == 2 ? (DT == kQ4_K ? MX_GEMM_WAVES2 : 4) : BN / (32 * nb);
     static constexpr int bn = waves * 32 * nb;  // weight rows per workgroup
 };
 
-typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
 typedef float float2_t __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ uint4 ld16(const uint8_t *p) {  // 4-byte aligned p
-    const u32x4a4 v = *reinterpret_cast<const u32x4a4 *>(p);
-    return make_uint4(v.x, v.y, v.z, v.w);
-}
-
-// 16 bytes from a 2-byte aligned address: an aligned 16-byte load plus, when p
-// is not 4-byte aligned, the dword after it (funnel-shifted in `fix16`)
-struct Raw16 {
-    uint4 v;
-    uint32_t tail;
-    uint32_t sh;  // 0 or 16
-};
-__device__ __forceinline__ Raw16 ld16_a2(const uint8_t *p) {
-    Raw16 r;
-    const uintptr_t mis = reinterpret_cast<uintptr_t>(p) & 3;
-    const uint8_t *q = p - mis;
-    r.v = ld16(q);
-    r.tail = mis ? *reinterpret_cast<const uint32_t *>(q + 16) : 0u;
-    r.sh = (uint32_t)mis * 8;
-    return r;
-}
-__device__ __forceinline__ uint4 fix16(const Raw16 &r) {
-    return make_uint4(__builtin_amdgcn_alignbit(r.v.y, r.v.x, r.sh), __builtin_amdgcn_alignbit(r.v.z, r.v.y, r.sh),
-                      __builtin_amdgcn_alignbit(r.v.w, r.v.z, r.sh), __builtin_amdgcn_alignbit(r.tail, r.v.w, r.sh));
-}
 
 __device__ __forceinline__ half8_t pack8(const float (&f)[8]) {
     half8_t h;
@@ -106,13 +81,7 @@ __device__ __forceinline__ half8_t pack8(const float (&f)[8]) {
     return h;
 }
 
-// 4 unsigned bytes of w -> floats (v_cvt_f32_ubyte0..3)
-__device__ __forceinline__ void ubytes(uint32_t w, float *f) {
-#pragma unroll
-    for (int b = 0; b < 4; b++) f[b] = (float)((w >> (8 * b)) & 0xFFu);
-}
-
-// Packed-f16 dequantisation (MX_GEMM_PKDQ).  Bytes b < 1024 of two dwords become
+// Packed-f16 dequantisation.  Bytes b < 1024 of two dwords become
 // the f16 numbers 1024 + b by placing them under the exponent byte 0x64
 // (v_perm_b32); the rest is v_pk_*_f16 arithmetic on small integers, exact
 // except where noted:
@@ -123,9 +92,6 @@ __device__ __forceinline__ void ubytes(uint32_t w, float *f) {
 // d and dmin are the blocks' own f16 values, so against the f32 form (one f16
 // rounding of the f32 value) only fl16(dmin * m) adds an error.  About 1.5
 // VALU per weight instead of 3.
-#ifndef MX_GEMM_PKDQ
-#define MX_GEMM_PKDQ 1
-#endif
 __device__ __forceinline__ half2_t pk_bytes(uint32_t w, uint32_t sel) {
     return __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, w, sel));
 }
@@ -168,44 +134,54 @@ __device__ __forceinline__ half2_t h2bits(uint32_t bits16) {
     return __builtin_bit_cast(half2_t, (bits16 & 0xFFFFu) * 0x10001u);
 }
 
-// ---- per-type weight registers: one stage, one weight row, one lane half --------------
+// ---- per-type weight staging: LDS slots filled by DMA, lane registers read from them -----
+// Every stage, the workgroup copies the raw bytes of its weight rows for that
+// stage into LDS with buffer->LDS DMA (16-byte chunks, consecutive lanes take
+// consecutive chunks of a row, so each copy instruction reads a few whole row
+// spans instead of 64 scattered pieces).  Row R of the tile owns a slot of
+// CPR chunks at R * SLOT; the chunks are the 16-byte-aligned pieces covering
+// the fields the stage needs.  A lane then reads its own row's slot (slots are
+// SLOT bytes apart, chosen so 8 consecutive rows hit distinct LDS banks) and
+// dequantises in registers as before.
+//   Q4_K  5 chunks: block header (d, dmin, scales) | qs[64 par, +64)
+//   Q5_K  7 chunks: header | qh[0, 32) | qs[64 par, +64)
+//   Q6_K 11 chunks: ql[64 n, +64) | qh[32 n, +32) | scales + d, each span from its
+//        16-byte-aligned start (blocks are 2-byte aligned; m1 = the block's
+//        address mod 16 locates the fields), plus one spare
+//   Q8_0 11 chunks: the 4 blocks (136 bytes) of the stage from the aligned start
+// The buffer resource starts at the expert's 16-byte-aligned base, so every
+// chunk offset is aligned, and chunks past the expert's last byte read 0.
 template <int DT> struct WB;
+
+// one 16-byte buffer -> LDS copy per lane (lane i's bytes land at lds_dst + 16 i)
+__device__ __forceinline__ void dma16_buf(__amdgpu_buffer_rsrc_t rs, uint32_t off, uint8_t *lds_dst) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (MX_AS_LDS void *)lds_dst, 16, off, 0, 0, 0);
+}
 
 // Q4_K: stage = half `par` of super-block ks / 2; 64-value chunks i = 2 par + c.
 // Lane half kh holds qs bytes [32 i + 16 kh, +16) of both chunks; step p = 2c + nib
 // uses the low (nib 0) or high nibbles, sub-block 2 i + nib (mm_id.metal:95-113).
 template <> struct WB<kQ4_K> {
-    static constexpr int kMinLoads = 3;  // memory instructions load() always issues: header + 2 quant pieces
+    static constexpr int CPR = 5, SLOT = 80;
+    // byte offset (from the block start) of chunk c of stage parity par
+    __device__ static uint32_t chunk_off(int c, int par) { return c == 0 ? 0u : (uint32_t)(16 + 64 * par + 16 * (c - 1)); }
+    static constexpr int BLK = 144;
     uint4 h, q[2];
-    __device__ __forceinline__ void load(const uint8_t *base, __amdgpu_buffer_rsrc_t rs, uint32_t row, int ks, int kh) {
-        const uint8_t *blk = base + (row + (uint32_t)(ks >> 1) * 144u);
-        h = ld16(blk);
-        const uint8_t *qs = blk + 16 + 64 * (ks & 1) + 16 * kh;
-        q[0] = ld16(qs);
-        q[1] = ld16(qs + 32);
+    __device__ __forceinline__ void load_lds(const uint8_t *slot, int kh, uint32_t) {
+        h = *reinterpret_cast<const uint4 *>(slot);
+        q[0] = *reinterpret_cast<const uint4 *>(slot + 16 + 16 * kh);
+        q[1] = *reinterpret_cast<const uint4 *>(slot + 48 + 16 * kh);
     }
-#if MX_GEMM_PKDQ
     half2_t scm[4], d2;  // (sc, -fl16(dmin * m)) of each sub-block, packed
-#else
-    float d[4], m[4];
-#endif
     template <int PAR> __device__ __forceinline__ void prep(int kh) {
         (void)kh;
-        [[maybe_unused]] const float dd = h2f((uint16_t)(h.x & 0xFFFFu));
         const float dmin = h2f((uint16_t)(h.x >> 16));
-#if MX_GEMM_PKDQ
         d2 = h2bits(h.x);
-#endif
 #pragma unroll
         for (int p = 0; p < 4; p++) {
             uint32_t sc, mn;
             q4k_scale_min(4 * PAR + p, h.y, h.z, h.w, sc, mn);
-#if MX_GEMM_PKDQ
             scm[p] = half2_t{(_Float16)(float)sc, (_Float16)(-(dmin * (float)mn))};
-#else
-            d[p] = dd * (float)sc;
-            m[p] = dmin * (float)mn;
-#endif
         }
     }
     __device__ __forceinline__ half8_t step(int p, int hh) const {
@@ -213,55 +189,36 @@ template <> struct WB<kQ4_K> {
         const int sh = 4 * (p & 1);
         const uint32_t w0 = ((hh ? v.z : v.x) >> sh) & 0x0F0F0F0Fu;
         const uint32_t w1 = ((hh ? v.w : v.y) >> sh) & 0x0F0F0F0Fu;
-#if MX_GEMM_PKDQ
         return dq8_kmin(w0, w1, half2_t{scm[p][0], scm[p][0]}, d2, half2_t{scm[p][1], scm[p][1]});
-#else
-        float f[8];
-        ubytes(w0, f);
-        ubytes(w1, f + 4);
-#pragma unroll
-        for (int i = 0; i < 8; i++) f[i] = __builtin_fmaf(d[p], f[i], -m[p]);
-        return pack8(f);
-#endif
     }
 };
 
 // Q5_K: Q4_K's stage layout (qs at byte 48) plus lane half kh's 16 bytes of qh;
 // step p of half `par` adds bit 4 par + p of qh[l] as the fifth bit (mm_id.metal:113-134).
 template <> struct WB<kQ5_K> {
-    static constexpr int kMinLoads = 4;  // memory instructions load() always issues: header + qh + 2 quant pieces
-    uint4 h, q[2], qh;
-    __device__ __forceinline__ void load(const uint8_t *base, __amdgpu_buffer_rsrc_t rs, uint32_t row, int ks, int kh) {
-        const uint8_t *blk = base + (row + (uint32_t)(ks >> 1) * 176u);
-        h = ld16(blk);
-        qh = ld16(blk + 16 + 16 * kh);
-        const uint8_t *qs = blk + 48 + 64 * (ks & 1) + 16 * kh;
-        q[0] = ld16(qs);
-        q[1] = ld16(qs + 32);
+    static constexpr int CPR = 7, SLOT = 112;
+    __device__ static uint32_t chunk_off(int c, int par) {
+        return c < 3 ? (uint32_t)(16 * c) : (uint32_t)(48 + 64 * par + 16 * (c - 3));
     }
-#if MX_GEMM_PKDQ
-    half2_t scm[4], d2;  // (sc, -fl16(dmin * m)) of each sub-block, packed
-#else
-    float d[4], m[4];
-#endif
+    static constexpr int BLK = 176;
+    uint4 h, q[2], qh;
+    __device__ __forceinline__ void load_lds(const uint8_t *slot, int kh, uint32_t) {
+        h = *reinterpret_cast<const uint4 *>(slot);
+        qh = *reinterpret_cast<const uint4 *>(slot + 16 + 16 * kh);
+        q[0] = *reinterpret_cast<const uint4 *>(slot + 48 + 16 * kh);
+        q[1] = *reinterpret_cast<const uint4 *>(slot + 80 + 16 * kh);
+    }
+    half2_t scm[4], d2;
     int hsh;
     template <int PAR> __device__ __forceinline__ void prep(int kh) {
         (void)kh;
-        [[maybe_unused]] const float dd = h2f((uint16_t)(h.x & 0xFFFFu));
         const float dmin = h2f((uint16_t)(h.x >> 16));
-#if MX_GEMM_PKDQ
         d2 = h2bits(h.x);
-#endif
 #pragma unroll
         for (int p = 0; p < 4; p++) {
             uint32_t sc, mn;
             q4k_scale_min(4 * PAR + p, h.y, h.z, h.w, sc, mn);
-#if MX_GEMM_PKDQ
             scm[p] = half2_t{(_Float16)(float)sc, (_Float16)(-(dmin * (float)mn))};
-#else
-            d[p] = dd * (float)sc;
-            m[p] = dmin * (float)mn;
-#endif
         }
         hsh = 4 * PAR;
     }
@@ -271,79 +228,59 @@ template <> struct WB<kQ5_K> {
         const uint32_t hb = hsh + p;
         const uint32_t w0 = (((hh ? v.z : v.x) >> sh) & 0x0F0F0F0Fu) | ((((hh ? qh.z : qh.x) >> hb) & 0x01010101u) << 4);
         const uint32_t w1 = (((hh ? v.w : v.y) >> sh) & 0x0F0F0F0Fu) | ((((hh ? qh.w : qh.y) >> hb) & 0x01010101u) << 4);
-#if MX_GEMM_PKDQ
         return dq8_kmin(w0, w1, half2_t{scm[p][0], scm[p][0]}, d2, half2_t{scm[p][1], scm[p][1]});
-#else
-        float f[8];
-        ubytes(w0, f);
-        ubytes(w1, f + 4);
-#pragma unroll
-        for (int i = 0; i < 8; i++) f[i] = __builtin_fmaf(d[p], f[i], -m[p]);
-        return pack8(f);
-#endif
     }
 };
+
+// 16 bytes at slot + off (off even, the field's offset inside its 16-byte-aligned
+// span): an aligned-down dword run, funnel-shifted by the 2-byte phase
+__device__ __forceinline__ uint4 lds16_a2(const uint8_t *slot, uint32_t off) {
+    const uint32_t *w = reinterpret_cast<const uint32_t *>(slot + (off & ~3u));
+    const uint32_t sh = (off & 2u) * 8u;
+    const uint32_t d0 = w[0], d1 = w[1], d2 = w[2], d3 = w[3], d4 = w[4];
+    return make_uint4(__builtin_amdgcn_alignbit(d1, d0, sh), __builtin_amdgcn_alignbit(d2, d1, sh),
+                      __builtin_amdgcn_alignbit(d3, d2, sh), __builtin_amdgcn_alignbit(d4, d3, sh));
+}
 
 // Q6_K: stage = half n = par of super-block ks / 2 (128 values).  Lane half kh
 // holds ql[64n + 16kh, +16), ql[64n + 32 + 16kh, +16), qh[32n + 16kh, +16);
 // step p takes the 4-bit part from the low (p even) / high (p odd) ql piece,
 // nibble p / 2, and bits 2p of qh; scale 8n + 2p + kh (mm_id.metal:115-135).
 template <> struct WB<kQ6_K> {
-    static constexpr int kMinLoads = 11;  // buffer loads load() issues: 3 x (piece + next dword) + 3 scale words + d
-    // raw bytes, realigned in place by prep(): ql low piece, ql high piece, qh
-    uint4 lo, hi, qh;
-    uint32_t lo_t, hi_t, qh_t;  // the dword after each piece (2-byte aligned blocks)
-    uint32_t sc0, sc1, sc2w, dsh;  // 3 dwords covering scales[8n .. 8n+7]; d and the shift
-    // Buffer loads through the expert's resource: every word is loaded whatever
-    // the block's 4-byte phase (no branches, so exact wait counts), and the
-    // words past the end of the expert's rows read 0 instead of faulting.
-    __device__ __forceinline__ void load(const uint8_t *base, __amdgpu_buffer_rsrc_t rs, uint32_t row, int ks, int kh) {
-        const uint32_t blk = row + (uint32_t)(ks >> 1) * 210u;  // byte offset in the expert
-        const int n = ks & 1;
-        auto piece = [&](uint32_t off, uint4 &v, uint32_t &t) {
-            const uint32_t al = off & ~3u;
-            const auto q = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)al, 0, 0);
-            v = make_uint4(q[0], q[1], q[2], q[3]);
-            t = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(al + 16), 0, 0);
-        };
-        piece(blk + 64 * n + 16 * kh, lo, lo_t);
-        piece(blk + 64 * n + 32 + 16 * kh, hi, hi_t);
-        piece(blk + 128 + 32 * n + 16 * kh, qh, qh_t);
-        const uint32_t sa = (blk + 192 + 8 * n) & ~3u;
-        sc0 = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)sa, 0, 0);
-        sc1 = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(sa + 4), 0, 0);
-        sc2w = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(sa + 8), 0, 0);
-        // every field of a block shares its 4-byte phase
-        const uint32_t sh = (uint32_t)((reinterpret_cast<uintptr_t>(base) + blk) & 2) * 8;
-        dsh = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, (int)(blk + 208), 0, 0) | (sh << 16);
+    static constexpr int CPR = 11, SLOT = 176;
+    static constexpr int BLK = 210;
+    // chunk c (relative to the block's 16-byte-aligned address) of stage parity n:
+    // ql span 0-4, qh span 5-7, scales/d span 8-10 (10 is spare)
+    __device__ static uint32_t chunk_off(int c, int n) {
+        return c < 5 ? (uint32_t)(64 * n + 16 * c) : c < 8 ? (uint32_t)(128 + 32 * n + 16 * (c - 5))
+                                                           : (uint32_t)(192 + 16 * (c - 8));
     }
-#if MX_GEMM_PKDQ
+    uint4 lo, hi, qh;
+    uint32_t s0, s1;
+    uint16_t dbits;
+    __device__ __forceinline__ void load_lds(const uint8_t *slot, int kh, uint32_t m1, int n) {
+        lo = lds16_a2(slot, m1 + 16 * kh);
+        hi = lds16_a2(slot, m1 + 32 + 16 * kh);
+        qh = lds16_a2(slot + 80, m1 + 16 * kh);
+        // scales[8n .. 8n+7] and d: tail span at slot + 128, scales[0] at m1, d at m1 + 16
+        const uint32_t so = m1 + 8 * n;
+        const uint32_t *w = reinterpret_cast<const uint32_t *>(slot + 128 + (so & ~3u));
+        const uint32_t sh = (so & 2u) * 8u;
+        const uint32_t a0 = w[0], a1 = w[1], a2 = w[2];
+        s0 = __builtin_amdgcn_alignbit(a1, a0, sh);
+        s1 = __builtin_amdgcn_alignbit(a2, a1, sh);
+        dbits = *reinterpret_cast<const uint16_t *>(slot + 128 + m1 + 16);
+    }
     half2_t sc2[4], d2;
-#else
-    float ds[4];
-#endif
     template <int PAR> __device__ __forceinline__ void prep(int kh) {
-        const float d = h2f((uint16_t)(dsh & 0xFFFFu));
-        const uint32_t sh = dsh >> 16;
-#if MX_GEMM_PKDQ
-        d2 = h2bits(dsh);
-        (void)d;
-#endif
-        const uint32_t s0 = __builtin_amdgcn_alignbit(sc1, sc0, sh), s1 = __builtin_amdgcn_alignbit(sc2w, sc1, sh);
+        d2 = h2bits(dbits);
 #pragma unroll
         for (int p = 0; p < 4; p++) {
             const int j = 2 * p + kh;  // byte j of the stage's 8 scales
             const uint32_t word = j < 4 ? s0 : s1;
             const int8_t s8 = (int8_t)((word >> (8 * (j & 3))) & 0xFFu);
-#if MX_GEMM_PKDQ
             sc2[p] = h2splat((float)s8);
-#else
-            ds[p] = d * (float)s8;
-#endif
         }
-        lo = fix16(Raw16{lo, lo_t, sh});
-        hi = fix16(Raw16{hi, hi_t, sh});
-        qh = fix16(Raw16{qh, qh_t, sh});
     }
     __device__ __forceinline__ half8_t step(int p, int hh) const {
         const uint4 &ql = (p & 1) ? hi : lo;
@@ -352,42 +289,29 @@ template <> struct WB<kQ6_K> {
         const uint32_t a1 = ((hh ? ql.w : ql.y) >> shl) & 0x0F0F0F0Fu;
         const uint32_t b0 = (((hh ? qh.z : qh.x) >> shh) & 0x03030303u) << 4;
         const uint32_t b1 = (((hh ? qh.w : qh.y) >> shh) & 0x03030303u) << 4;
-#if MX_GEMM_PKDQ
         return dq8_q6(a0 | b0, a1 | b1, sc2[p], d2);
-#else
-        float f[8];
-        ubytes(a0 | b0, f);
-        ubytes(a1 | b1, f + 4);
-        const float off = -32.0f * ds[p];
-#pragma unroll
-        for (int i = 0; i < 8; i++) f[i] = __builtin_fmaf(ds[p], f[i], off);
-        return pack8(f);
-#endif
     }
 };
 
-// Q8_0: stage = blocks 4 ks + p; lane half kh holds quants [16 kh, +16) of each.
+// Q8_0: stage = blocks 4 ks + p (136 bytes from the aligned start); lane half kh
+// holds quants [16 kh, +16) of each.
 template <> struct WB<kQ8_0> {
-    static constexpr int kMinLoads = 8;  // memory instructions load() always issues: 4 x (piece + d)
-    Raw16 q[4];
+    static constexpr int CPR = 11, SLOT = 176;
+    __device__ static uint32_t chunk_off(int c, int) { return (uint32_t)(16 * c); }
+    uint4 v[4];
     uint16_t dh[4];
-    __device__ __forceinline__ void load(const uint8_t *base, __amdgpu_buffer_rsrc_t rs, uint32_t row, int ks, int kh) {
+    __device__ __forceinline__ void load_lds(const uint8_t *slot, int kh, uint32_t m1, int) {
 #pragma unroll
         for (int p = 0; p < 4; p++) {
-            const uint8_t *blk = base + (row + (uint32_t)(4 * ks + p) * 34u);
-            q[p] = ld16_a2(blk + 2 + 16 * kh);
-            dh[p] = ld_u16(blk);
+            v[p] = lds16_a2(slot, m1 + 34 * p + 2 + 16 * kh);
+            dh[p] = *reinterpret_cast<const uint16_t *>(slot + m1 + 34 * p);
         }
     }
     float d[4];
-    uint4 v[4];
     template <int PAR> __device__ __forceinline__ void prep(int kh) {
         (void)kh;
 #pragma unroll
-        for (int p = 0; p < 4; p++) {
-            d[p] = h2f(dh[p]);
-            v[p] = fix16(q[p]);
-        }
+        for (int p = 0; p < 4; p++) d[p] = h2f(dh[p]);
     }
     __device__ __forceinline__ half8_t step(int p, int hh) const {
         const uint32_t w0 = hh ? v[p].z : v[p].x, w1 = hh ? v[p].w : v[p].y;
@@ -403,26 +327,16 @@ template <> struct WB<kQ8_0> {
     }
 };
 
-#ifndef MX_GEMM_PIN_W
-#define MX_GEMM_PIN_W 1
-#endif
-// leave the next stage's weight loads outstanding across the stage barrier
-#ifndef MX_GEMM_WSLACK
-#define MX_GEMM_WSLACK 1
-#endif
-
-// Makes the compiler wait for every register of `v` here (an empty asm that
-// reads them).  Placed before a stage's A copies, the wait then covers weight
-// loads only: the compiler's counters cannot order weight loads against LDS
-// copies issued after them and would otherwise wait for everything.
-// The operands are in-out, so nothing computed from `v` can be hoisted above
-// this point either (the compiler would otherwise start the next stage's prep
-// inside this stage and wait for the loads just issued).
-template <class T> __device__ __forceinline__ void touch_regs(T &v) {
-    static_assert(sizeof(T) % 4 == 0, "touch_regs: whole dwords");
-    uint32_t *w = reinterpret_cast<uint32_t *>(&v);
-#pragma unroll
-    for (int i = 0; i < (int)(sizeof(T) / 4); i++) asm volatile("" : "+v"(w[i]));
+// byte offset of stage ks's data inside a weight row, and whether the type's
+// fields need the block's 16-byte phase (2-byte-aligned blocks)
+template <int DT> __device__ __forceinline__ uint32_t stage_block_off(int ks) {
+    if constexpr (DT == kQ8_0) return (uint32_t)(4 * ks) * 34u;
+    else return (uint32_t)(ks >> 1) * (uint32_t)WB<DT>::BLK;
+}
+template <int DT> constexpr bool kPhased = DT == kQ6_K || DT == kQ8_0;
+template <int DT> __device__ __forceinline__ void wb_load(WB<DT> &w, const uint8_t *slot, int kh, uint32_t m1, int par) {
+    if constexpr (kPhased<DT>) w.load_lds(slot, kh, m1, par);
+    else w.load_lds(slot, kh, m1);
 }
 
 struct Tile {
@@ -449,36 +363,39 @@ __device__ __forceinline__ bool tile_of(const GemmArgs &a, int nt_count, Tile &t
     return true;
 }
 
-// waves per SIMD the register allocation must allow, per weight type
-#ifndef MX_GEMM_WPE_Q4K
-#define MX_GEMM_WPE_Q4K 2
-#endif
-#ifndef MX_GEMM_WPE_Q6K
-#define MX_GEMM_WPE_Q6K 1
-#endif
-template <int DT> struct GemmWpe {
-    static constexpr int v = (DT == kQ4_K || DT == kQ5_K) ? MX_GEMM_WPE_Q4K : DT == kQ6_K ? MX_GEMM_WPE_Q6K : 1;
+// waves per SIMD the register allocation must allow: the LDS of one 8-wave
+// workgroup per CU holds 2 waves per SIMD; the 4-wave tiles run 1
+template <int DT, bool SWIGLU> struct GemmWpe {
+    static constexpr int v = GemmNb<DT, SWIGLU>::waves == 8 ? 2 : 1;
 };
 
 template <int DT, bool SWIGLU>
 __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
-    __attribute__((amdgpu_waves_per_eu(GemmWpe<DT>::v))) k_gemm(GemmArgs a) {
+    __attribute__((amdgpu_waves_per_eu(GemmWpe<DT, SWIGLU>::v))) k_gemm(GemmArgs a) {
     constexpr int NB = GemmNb<DT, SWIGLU>::nb;
     constexpr int NWAVE = GemmNb<DT, SWIGLU>::waves;
     constexpr int DMA_PER_WAVE = STAGE_BYTES / 1024 / NWAVE;
-    // two separate LDS objects (not one 2-D array): the compiler can then tell
-    // that a copy into one buffer does not feed reads of the other, and does
-    // not wait for the next stage's copies before this stage's reads
+    constexpr int BROWS = GemmNb<DT, SWIGLU>::bn;           // weight rows of the tile
+    constexpr int CPR = WB<DT>::CPR, SLOT = WB<DT>::SLOT;
+    constexpr int B_INSTS = BROWS * CPR / 64;                // B copy instructions per stage
+    constexpr int B_PER_MAT = SWIGLU ? B_INSTS / 2 : B_INSTS; // instructions per matrix (gate / up)
+    static_assert((BROWS * CPR) % 64 == 0 && (!SWIGLU || B_INSTS % 2 == 0), "B copies must not straddle matrices");
+    constexpr int B_PER_WAVE = (B_INSTS + NWAVE - 1) / NWAVE;
+    // separate LDS objects per buffer: the compiler can then tell that a copy into
+    // one buffer does not feed reads of the other
     __shared__ __attribute__((aligned(1024))) uint8_t sA0[STAGE_BYTES];
     __shared__ __attribute__((aligned(1024))) uint8_t sA1[STAGE_BYTES];
+    __shared__ __attribute__((aligned(1024))) uint8_t sB0[BROWS * SLOT];
+    __shared__ __attribute__((aligned(1024))) uint8_t sB1[BROWS * SLOT];
     __shared__ uint32_t s_src[GM_BM];  // byte offset of the A row from the tile's first row
     __shared__ float s_scale[GM_BM];
     __shared__ int s_out[GM_BM];      // output row
-    constexpr int NCOL = SWIGLU ? GemmNb<DT, SWIGLU>::bn / 2 : GemmNb<DT, SWIGLU>::bn;
+    constexpr int NCOL = SWIGLU ? BROWS / 2 : BROWS;
     const int nt_count = (a.n_out + NCOL - 1) / NCOL;
     Tile tl;
     if (!tile_of(a, nt_count, tl)) return;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int j = lane & 31, kh = lane >> 5;
     {
         const MapLayout L(a.n_map_expert, a.t, a.top_k);
@@ -495,25 +412,62 @@ __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
             s_out[tid] = SWIGLU ? pos : pair / a.top_k * a.out_stride + pair % a.top_k + a.out_add;
         }
     }
-    __syncthreads();
 
-    // this lane's two weight rows (one per 32-column MFMA block)
+    // the tile's weight matrices as buffers from their 16-byte-aligned base
     const bool shared = tl.e >= a.n_expert;
     const int64_t rb = shared ? a.sh_row_bytes : a.row_bytes;
-    const uint8_t *wbase[NB];  // wave-uniform expert base
-    __amdgpu_buffer_rsrc_t wres[NB];  // the expert's rows as a buffer (range-checked loads)
-    uint32_t wrow[NB];         // this lane's row offset from it (the launcher checks it fits)
+    constexpr int NMAT = SWIGLU ? 2 : 1;
+    __amdgpu_buffer_rsrc_t wres[NMAT];
+    uint32_t wphase[NMAT];  // base address mod 16
+#pragma unroll
+    for (int m = 0; m < NMAT; m++) {
+        const uint8_t *base = shared ? a.w_sh[m] : a.w[m] + (int64_t)tl.e * a.expert_bytes;
+        const uintptr_t ab = reinterpret_cast<uintptr_t>(base);
+        wphase[m] = (uint32_t)(ab & 15);
+        wres[m] = __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<uint8_t *>(ab & ~uintptr_t(15)), (short)0,
+                                                    (int)(a.n_out * rb + wphase[m]), 0x00020000);
+    }
+    // this lane's copy chunks: instruction q of the wave covers tile chunk
+    // (wave + NWAVE q) * 64 + lane = row R, chunk c; the row's offset in its matrix
+    uint32_t b_row[B_PER_WAVE];
+    int b_c[B_PER_WAVE];
+#pragma unroll
+    for (int q = 0; q < B_PER_WAVE; q++) {
+        const int inst = wave + NWAVE * q;
+        const int ch = inst * 64 + lane;
+        const int R = ch / CPR;
+        b_c[q] = ch - R * CPR;
+        const int rm = SWIGLU ? R % (BROWS / 2) : R;
+        const int colr = min(tl.nt * NCOL + rm, a.n_out - 1);
+        b_row[q] = (uint32_t)(colr * rb);
+    }
+    auto issue_b = [&](int ks, uint8_t *buf) {
+        const uint32_t so = stage_block_off<DT>(ks);
+#pragma unroll
+        for (int q = 0; q < B_PER_WAVE; q++) {
+            const int inst = wave + NWAVE * q;
+            if (inst < B_INSTS) {
+                const int m = SWIGLU ? (inst >= B_PER_MAT ? 1 : 0) : 0;
+                const uint32_t blk = wphase[m] + b_row[q] + so;  // block offset from the aligned base
+                const uint32_t off = kPhased<DT> ? (blk & ~15u) + WB<DT>::chunk_off(b_c[q], ks & 1)
+                                                 : blk + WB<DT>::chunk_off(b_c[q], ks & 1);
+                dma16_buf(wres[m], off, buf + inst * 1024);
+            }
+        }
+        asm volatile("" ::: "memory");
+    };
+
+    // this lane's B rows: tile row index, and (2-byte-aligned types) the block phase
+    int brow[NB];
+    uint32_t rowoff[NB];
     int col[NB];
 #pragma unroll
     for (int nb = 0; nb < NB; nb++) {
-        const int m = SWIGLU ? nb : 0;
-        const uint8_t *base = shared ? a.w_sh[m] : a.w[m] + (int64_t)tl.e * a.expert_bytes;
+        brow[nb] = SWIGLU ? nb * (BROWS / 2) + wave * 32 + j : wave * 32 * NB + nb * 32 + j;
         col[nb] = SWIGLU ? tl.nt * NCOL + wave * 32 + j : tl.nt * NCOL + wave * 32 * NB + nb * 32 + j;
-        wbase[nb] = base;
-        wres[nb] = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(base), (short)0, (int)(a.n_out * rb),
-                                                     0x00020000);
-        wrow[nb] = (uint32_t)(min(col[nb], a.n_out - 1) * rb);
+        rowoff[nb] = wphase[SWIGLU ? nb : 0] + (uint32_t)(min(col[nb], a.n_out - 1) * rb);
     }
+    __syncthreads();
 
     const MapLayout L0(a.n_map_expert, a.t, a.top_k);
     const int64_t arow0 = a.a_by_token ? a.map[L0.list + tl.pos0] / a.top_k : tl.pos0;
@@ -527,9 +481,6 @@ __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
             const int c = (lane & 15) ^ (row & 15);
             dma16(abase + (s_src[row] + (uint32_t)(ks * ROWB + c * 16)), buf + inst * 1024);
         }
-        // keep the copies at the start of the stage: without this the compiler
-        // sinks them behind the stage's LDS reads (the buffers are separate
-        // objects), which leaves the copy no time to land before the barrier
         asm volatile("" ::: "memory");
     };
 
@@ -565,56 +516,49 @@ __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
             }
         }
     };
+    // stage ks's B registers from LDS (the block phase of the lane's row for this stage)
+    WB<DT> wb[NB];
+    auto load_b = [&](int ks, const uint8_t *buf) {
+        const uint32_t so = stage_block_off<DT>(ks);
+#pragma unroll
+        for (int nb = 0; nb < NB; nb++)
+            wb_load<DT>(wb[nb], buf + brow[nb] * SLOT, kh, (rowoff[nb] + so) & 15u, ks & 1);
+    };
 
-    WB<DT> w0[NB], w1[NB];
     const int nks = a.k / KS;  // even
     issue_a(0, sA0);
-#pragma unroll
-    for (int nb = 0; nb < NB; nb++) w0[nb].load(wbase[nb], wres[nb], wrow[nb], 0, kh);
+    issue_b(0, sB0);
     wait_vmcnt(0);
     __syncthreads();
-    // Each stage: prep the weights loaded one stage ago, issue the next
-    // stage's A copy and weight loads, compute.  Stage ends wait for the A copy
-    // only and use a bare s_barrier: the copies are complete (vmcnt) and LDS
-    // needs no further fence between the waves of a workgroup.
-    // One-column tiles (NB = 1) have the registers to hold the next stage's
-    // weights through the compute: keep their loads at the stage start (the
-    // compiler would sink them next to their use).  The two-column tiles
-    // would spill, so their loads stay where the compiler puts them.
-    auto pin_weight_loads = [] {
-        if constexpr (NB == 1 && MX_GEMM_PIN_W) asm volatile("" ::: "memory");
-    };
+    // Each stage: issue the next stage's A and B copies, read this stage's B rows
+    // from LDS, dequantise, compute; stage ends wait for the copies and use a bare
+    // s_barrier (the copies are complete (vmcnt) and LDS needs no further fence
+    // between the waves of a workgroup).
     auto stage_end = [&] {
-        wait_vmcnt(MX_GEMM_WSLACK ? NB * WB<DT>::kMinLoads : 0);
+        wait_vmcnt(0);
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
     };
     for (int ks = 0; ks < nks; ks += 2) {
-#pragma unroll
-        for (int nb = 0; nb < NB; nb++) touch_regs(w0[nb]);
         issue_a(ks + 1, sA1);
+        issue_b(ks + 1, sB1);
+        load_b(ks, sB0);
 #pragma unroll
-        for (int nb = 0; nb < NB; nb++) w1[nb].load(wbase[nb], wres[nb], wrow[nb], ks + 1, kh);
-        pin_weight_loads();
-#pragma unroll
-        for (int nb = 0; nb < NB; nb++) w0[nb].template prep<0>(kh);
-        compute(sA0, w0);
+        for (int nb = 0; nb < NB; nb++) wb[nb].template prep<0>(kh);
+        compute(sA0, wb);
         stage_end();
-#pragma unroll
-        for (int nb = 0; nb < NB; nb++) touch_regs(w1[nb]);
         {
             // unconditional, clamped at the last stage (a harmless re-copy into
             // the buffer nobody reads next): no branch merge in front of the
             // next waits, so the compiler keeps exact memory counters
             const int kn = min(ks + 2, nks - 1);
             issue_a(kn, sA0);
-#pragma unroll
-            for (int nb = 0; nb < NB; nb++) w0[nb].load(wbase[nb], wres[nb], wrow[nb], kn, kh);
-            pin_weight_loads();
+            issue_b(kn, sB0);
         }
+        load_b(ks + 1, sB1);
 #pragma unroll
-        for (int nb = 0; nb < NB; nb++) w1[nb].template prep<1>(kh);
-        compute(sA1, w1);
+        for (int nb = 0; nb < NB; nb++) wb[nb].template prep<1>(kh);
+        compute(sA1, wb);
         stage_end();
     }
     __syncthreads();

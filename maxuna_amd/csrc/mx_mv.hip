@@ -773,6 +773,16 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
                                                      });
 }
 
+// The selection blocks alone (a launch with no expert slots): their own kernel,
+// so profiles tell the top-k from the expert rows.
+__global__ void __launch_bounds__(SEL_THREADS) k_decode_select(int top_k, DecodeSelArgs sel) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    SelShared &sh = *reinterpret_cast<SelShared *>(lds);
+    const int64_t o = (int64_t)blockIdx.x * sel.n_expert;
+    topk_from_keys(sel.keys + o, sel.probs + o, sel.n_expert, top_k, sel.scale, sel.apply_scale, sel.norm,
+                   sel.ids + (int64_t)blockIdx.x * top_k, sel.w + (int64_t)blockIdx.x * top_k, sh);
+}
+
 template <int DT, int NG>
 static mx_status launch_gu_ng(const DecodeGateUpArgs &a, unsigned blocks, int slot0, int nslot,
                               const DecodeSelArgs &sel, hipStream_t s) {
@@ -806,10 +816,17 @@ mx_status launch_decode_gate_up(int dtype, const DecodeGateUpArgs &a, int slot0,
     DecodeSelArgs none{};
     const DecodeSelArgs &sa = sel ? *sel : none;
     if (a.t == 0) return MX_OK;
-    if (sa.n_sel && (sa.n_expert > SEL_MAX_E || a.top_k > SEL_MAX_K || 64 * WAVES != SEL_THREADS))
+    if (sa.n_sel && (sa.n_expert > SEL_MAX_E || a.top_k > SEL_MAX_K || (nslot > 0 && 64 * WAVES != SEL_THREADS)))
         return fail(MX_ERR_SHAPE, "decode select: n_expert <= %d and top_k <= %d", SEL_MAX_E, SEL_MAX_K);
     if (a.order && (sa.n_sel || slot0 != 0 || nslot != a.top_k + (a.sh_gate ? 1 : 0)))
         return fail(MX_ERR_SHAPE, "decode gate/up: an expert-ordered launch covers every slot");
+    if (nslot == 0) {
+        if (sa.n_sel == 0) return MX_OK;
+        hipLaunchKernelGGL(k_decode_select, dim3((unsigned)sa.n_sel), dim3(SEL_THREADS), sizeof(SelShared), s,
+                           a.top_k, sa);
+        MX_LAUNCH("k_decode_select");
+        return MX_OK;
+    }
     const int64_t tiles = (a.ff + WAVES * RW_GU - 1) / (WAVES * RW_GU);
     const int64_t blocks = sa.n_sel + tiles * nslot * a.t;
     if (blocks == 0) return MX_OK;
