@@ -14,12 +14,6 @@
 #define MX_NOALLOC_SCRATCH_BYTES (16u << 20)
 #endif
 
-// decode: the shared expert's gate/up rides in the top-k launch (1) or with the
-// routed slots (0)
-#ifndef MX_SHARED_WITH_SELECT
-#define MX_SHARED_WITH_SELECT 0
-#endif
-
 namespace mx {
 
 static thread_local char g_err[512] = "";
@@ -312,7 +306,6 @@ struct Plan {
     bool generic;           // below the GEMM threshold, shapes the fused decode kernels cannot hold:
                             // router + f32 gather mat-vecs + SwiGLU + combine
     bool shared_in_decode;  // shared expert rides in the fused decode kernels (same quant types)
-    bool expert_order;      // decode kernels walk (token, slot) pairs in expert order (unfused router)
     int64_t min_seq;
 };
 
@@ -344,8 +337,6 @@ Plan plan_for(const mx_moe_layer *L, int64_t t) {
                              decode_down_fits(L->down.dtype, (int)L->expert_ff, stack_row_bytes(L->down));
     p.generic = !p.mm && !decode_fits;
     p.fused_router = !p.mm && !p.generic && t <= route_fused_max_t();
-    p.expert_order = !p.mm && !p.generic && !p.fused_router &&
-                     t * (L->top_k + (p.shared_in_decode ? 1 : 0)) <= SORT_PAIRS_MAX;
     return p;
 }
 
@@ -356,7 +347,7 @@ struct Layout {
     uint32_t *ids = nullptr, *zero_ids = nullptr;
     uint8_t *xstage = nullptr, *xstage_gm = nullptr;
     float *part = nullptr;
-    int32_t *map = nullptr, *map_sh = nullptr, *order = nullptr;
+    int32_t *map = nullptr, *map_sh = nullptr;
     uint32_t *ids_aug = nullptr;
     _Float16 *x16 = nullptr, *act16 = nullptr;
     float *x16s = nullptr, *act16s = nullptr, *down = nullptr, *act_u = nullptr;
@@ -391,7 +382,6 @@ Layout carve(const mx_moe_layer *L, int64_t t, const Plan &p, void *base) {
         if (H % 64 == 0) o.xstage_gm = ws.take<uint8_t>(t * xstage_gm_stride((int)H));
         o.act = ws.take<float>(t * slots * FF);
         o.part = ws.take<float>(t * slots * H);
-        if (p.expert_order) o.order = ws.take<int32_t>(t * slots);
         if (p.has_shared && !p.shared_in_decode) {
             o.sh_g = ws.take<float>(t * FF);
             o.sh_u = ws.take<float>(t * FF);
@@ -545,8 +535,7 @@ mx_status moe_forward_impl(const mx_moe_layer *L, const float *x, int64_t t, con
         MX_TRY(launch_route_select(o.logits, L->exp_probs_b, (int)t, (int)E, (int)K, scale, apply,
                                    L->weights_norm, ids, w, s));
         if (!p.mm && !p.generic) MX_TRY(launch_stage_rows(xin, (int)t, (int)H, o.xstage, o.xstage_gm, s));
-        if (p.expert_order)
-            MX_TRY(launch_sort_pairs(ids, (int)t, (int)K, p.shared_in_decode ? 1 : 0, (int)E, o.order, s));
+
     }
     MX_STAGE();
 
@@ -596,34 +585,22 @@ mx_status moe_forward_impl(const mx_moe_layer *L, const float *x, int64_t t, con
             shared_out = o.sh_out;
         }
         DecodeGateUpArgs ga{gg.w, gu.w, gg.expert_bytes, gg.row_bytes, shf ? sg.w : nullptr, shf ? su.w : nullptr,
-                            sg.row_bytes, (int)E, (int)FF, (int)H, o.xstage, ids, (int)t, (int)K, o.act, o.order,
+                            sg.row_bytes, (int)E, (int)FF, (int)H, o.xstage, ids, (int)t, (int)K, o.act,
                             o.xstage_gm};
+        DecodeDownArgs da{gd.w, gd.expert_bytes, gd.row_bytes, shf ? sd.w : nullptr, sd.row_bytes, shared_out,
+                          (int)E, (int)FF, (int)H, o.act, ids, w, residual, (int)t, (int)K, out, o.part};
         if (p.fused_router) {
-            // the top-k of every token, next to the shared expert's gate/up rows (which
-            // need no routing) -- then the routed slots, which read the selection
+            // the top-k of every token (its own launch), then the expert slots, which read it
             const uint8_t *keys = static_cast<const uint8_t *>(o.route_ws);
             DecodeSelArgs sel{reinterpret_cast<const uint64_t *>(keys),
                               reinterpret_cast<const float *>(keys + (size_t)t * E * sizeof(uint64_t)), (int)E,
                               (int)t, scale, apply, L->weights_norm, ids, w};
-#if MX_SHARED_WITH_SELECT
-            for (int r = 0; r < rep(1); r++)
-                MX_TRY(launch_decode_gate_up(L->gate.dtype, ga, (int)K, shf ? 1 : 0, &sel, s));
-            MX_STAGE();
-            for (int r = 0; r < rep(2); r++) MX_TRY(launch_decode_gate_up(L->gate.dtype, ga, 0, (int)K, nullptr, s));
-#else
             for (int r = 0; r < rep(1); r++) MX_TRY(launch_decode_gate_up(L->gate.dtype, ga, (int)K, 0, &sel, s));
-            MX_STAGE();
-            for (int r = 0; r < rep(2); r++)
-                MX_TRY(launch_decode_gate_up(L->gate.dtype, ga, 0, (int)K + (shf ? 1 : 0), nullptr, s));
-#endif
-        } else {
-            MX_STAGE();
-            MX_TRY(launch_decode_gate_up(L->gate.dtype, ga, 0, (int)K + (shf ? 1 : 0), nullptr, s));
         }
         MX_STAGE();
-        DecodeDownArgs da{gd.w, gd.expert_bytes, gd.row_bytes, shf ? sd.w : nullptr, sd.row_bytes, shared_out,
-                          (int)E, (int)FF, (int)H, o.act, ids, w, residual, (int)t, (int)K, out, o.part,
-                          o.order};
+        for (int r = 0; r < (p.fused_router ? rep(2) : 1); r++)
+            MX_TRY(launch_decode_gate_up(L->gate.dtype, ga, 0, (int)K + (shf ? 1 : 0), nullptr, s));
+        MX_STAGE();
         for (int r = 0; r < (p.fused_router ? rep(3) : 1); r++) MX_TRY(launch_decode_down(L->down.dtype, da, s));
         MX_STAGE();
         return MX_OK;

@@ -55,7 +55,6 @@ struct DecodeGateUpArgs {
     const uint32_t *ids;                 // [t, top_k]
     int t, top_k;
     float *act;                          // [t, slots, ff], slots = top_k + (sh_gate != NULL)
-    const int32_t *order;                // NULL, or the t * slots (token, slot) pairs sorted by expert
     const uint8_t *xstage_gm;            // NULL, or the group-major copy of xstage (Q4_K / Q5_K reads)
 };
 // Optional top-k blocks in front of the gate/up blocks (decode router split):
@@ -93,17 +92,8 @@ struct DecodeDownArgs {
     int t, top_k;
     float *out;                          // [t, hidden]
     float *part;                         // [t, top_k + (sh_down != NULL), hidden] scratch
-    const int32_t *order;                // NULL, or the t * slots (token, slot) pairs sorted by expert
 };
 mx_status launch_decode_down(int dtype, const DecodeDownArgs &a, hipStream_t s);
-// order[t * slots]: pair ids tok * slots + slot sorted by (expert, pair); slot
-// top_k (when has_shared) counts as expert n_expert.  One block; t * slots <= 1024.
-// The decode kernels walk the pairs in this order, pair index fastest, so all
-// tokens that picked an expert stream its rows at about the same time and the
-// repeats are served by the Infinity Cache instead of HBM.
-mx_status launch_sort_pairs(const uint32_t *ids, int t, int top_k, int has_shared, int n_expert, int32_t *order,
-                            hipStream_t s);
-constexpr int SORT_PAIRS_MAX = 1024;
 
 // mx_route.hip
 // router: [n_expert, hidden] (GGUF ffn_gate_inp layout)

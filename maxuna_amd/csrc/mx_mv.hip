@@ -722,13 +722,7 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
     const int tiles = (a.ff + WAVES * RW_GU - 1) / (WAVES * RW_GU);
     const int slots = a.top_k + (a.sh_gate ? 1 : 0);
     int tile, slot, tok;
-    if (a.order) {  // every slot of every token, pairs in expert order, pair index fastest
-        const int npair = a.t * slots;
-        const int pair = a.order[bid % npair];
-        tile = bid / npair;
-        tok = pair / slots;
-        slot = pair % slots;
-    } else if (sel.n_sel == 0) {  // grid (tiles, nslot, t)
+    if (sel.n_sel == 0) {  // grid (tiles, nslot, t)
         tile = blockIdx.x;
         slot = slot0 + blockIdx.y;
         tok = blockIdx.z;
@@ -787,7 +781,7 @@ template <int DT, int NG>
 static mx_status launch_gu_ng(const DecodeGateUpArgs &a, unsigned blocks, int slot0, int nslot,
                               const DecodeSelArgs &sel, hipStream_t s) {
     const unsigned tiles = (unsigned)((a.ff + WAVES * RW_GU - 1) / (WAVES * RW_GU));
-    const dim3 grid = (sel.n_sel == 0 && !a.order) ? dim3(tiles, (unsigned)nslot, (unsigned)a.t) : dim3(blocks);
+    const dim3 grid = sel.n_sel == 0 ? dim3(tiles, (unsigned)nslot, (unsigned)a.t) : dim3(blocks);
     constexpr bool GM_OK = DT == kQ4_K || DT == kQ5_K;
     const int ni = ring_insts<DT, NG>(2, a.hidden, a.gu_row_bytes);
     if (ni > DMA_MAX_INSTS) return fail(MX_ERR_SHAPE, "decode gate/up: rows too long for the LDS ring");
@@ -818,8 +812,6 @@ mx_status launch_decode_gate_up(int dtype, const DecodeGateUpArgs &a, int slot0,
     if (a.t == 0) return MX_OK;
     if (sa.n_sel && (sa.n_expert > SEL_MAX_E || a.top_k > SEL_MAX_K || (nslot > 0 && 64 * WAVES != SEL_THREADS)))
         return fail(MX_ERR_SHAPE, "decode select: n_expert <= %d and top_k <= %d", SEL_MAX_E, SEL_MAX_K);
-    if (a.order && (sa.n_sel || slot0 != 0 || nslot != a.top_k + (a.sh_gate ? 1 : 0)))
-        return fail(MX_ERR_SHAPE, "decode gate/up: an expert-ordered launch covers every slot");
     if (nslot == 0) {
         if (sa.n_sel == 0) return MX_OK;
         hipLaunchKernelGGL(k_decode_select, dim3((unsigned)sa.n_sel), dim3(SEL_THREADS), sizeof(SelShared), s,
@@ -845,8 +837,7 @@ mx_status launch_decode_gate_up(int dtype, const DecodeGateUpArgs &a, int slot0,
 }
 
 // ---- fused decode: down (one slot per block), then the combine kernel ---------------------
-// grid (hidden / (WAVES_DN * RW_DN), n_slot_blocks, t), or (pairs in expert order,
-// row tiles).  Each block writes its slot's down rows to part[tok, slot, :]; the
+// grid (hidden / (WAVES_DN * RW_DN), n_slot_blocks, t).  Each block writes its slot's down rows to part[tok, slot, :]; the
 // combine kernel that follows on the stream (the kernel boundary orders the two)
 // forms out[c] = residual[c] + ( sum_k w[k] * part[k][c] + shared[c] )
 // (combine.metal:70-97, moe.rs:73-78, model.rs:351).  The shared expert is
@@ -858,17 +849,7 @@ template <int DT, int NG>
 __global__ void __launch_bounds__(64 * WAVES_DN) __attribute__((amdgpu_waves_per_eu(MX_DN_WPE))) k_decode_down(DecodeDownArgs a, int ni) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int slots = a.top_k + (a.sh_down ? 1 : 0);
-    int slot, tok, tile;
-    if (a.order) {  // grid (t * slots pairs in expert order, row tiles)
-        const int pair = a.order[blockIdx.x];
-        tok = pair / slots;
-        slot = pair % slots;
-        tile = blockIdx.y;
-    } else {  // grid (row tiles, slots, t)
-        slot = blockIdx.y;
-        tok = blockIdx.z;
-        tile = blockIdx.x;
-    }
+    const int slot = blockIdx.y, tok = blockIdx.z, tile = blockIdx.x;  // grid (row tiles, slots, t)
     constexpr int ROWS_PER_WG = WAVES_DN * RW_DN;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (scalar)
     const int r0 = tile * ROWS_PER_WG + wave * RW_DN;
@@ -1001,7 +982,7 @@ static size_t dn_slots_lds(const DecodeDownArgs &a) {
 // true when the slot-per-wave kernel takes this launch
 template <int DT>
 static bool dn_slots_fit(const DecodeDownArgs &a) {
-    if (!MX_DN_SLOTS || a.order || a.t > MX_DN_SLOTS_MAX_T) return false;
+    if (!MX_DN_SLOTS || a.t > MX_DN_SLOTS_MAX_T) return false;
     if (a.top_k + (a.sh_down ? 1 : 0) > DN_SLOTS_MAX) return false;
     const int ng = ng_variant(Geo<DT>(a.ff, DN_FULL).NG);
     size_t lds = SIZE_MAX;
@@ -1043,7 +1024,7 @@ static mx_status launch_dn_dt(const DecodeDownArgs &a, dim3 grid, hipStream_t s)
 mx_status launch_decode_down(int dtype, const DecodeDownArgs &a, hipStream_t s) {
     const unsigned tiles = (unsigned)((a.hidden + WAVES_DN * RW_DN - 1) / (WAVES_DN * RW_DN));
     const unsigned slots = (unsigned)(a.top_k + (a.sh_down ? 1 : 0));
-    const dim3 grid = a.order ? dim3(slots * (unsigned)a.t, tiles) : dim3(tiles, slots, (unsigned)a.t);
+    const dim3 grid(tiles, slots, (unsigned)a.t);
     if (grid.x == 0 || a.t == 0) return MX_OK;
     if (a.ff % 32) return fail(MX_ERR_BLOCK, "decode down: expert_ff must be a multiple of 32");
     if (a.sh_down && a.sh_row_bytes != a.d_row_bytes)
@@ -1074,39 +1055,6 @@ mx_status launch_decode_down(int dtype, const DecodeDownArgs &a, hipStream_t s) 
     MX_LAUNCH("k_decode_down");
     return launch_combine_prefill(a.part, a.w, a.residual, a.t, a.top_k, a.sh_down ? 1 : 0, a.hidden, a.out, s,
                                   a.shared_out);
-}
-
-// ---- (token, slot) pairs in expert order (small-batch verify) --------------------------
-__global__ void __launch_bounds__(SORT_PAIRS_MAX) k_sort_pairs(const uint32_t *__restrict__ ids, int t, int top_k,
-                                                               int has_shared, int n_expert,
-                                                               int32_t *__restrict__ order) {
-    __shared__ uint32_t s_key[SORT_PAIRS_MAX];
-    const int slots = top_k + has_shared;
-    const int n = t * slots;
-    const int p = threadIdx.x;
-    uint32_t key = 0xFFFFFFFFu;
-    if (p < n) {
-        const int tok = p / slots, slot = p % slots;
-        uint32_t e = slot < top_k ? ids[tok * top_k + slot] : (uint32_t)n_expert;
-        if (e > (uint32_t)n_expert) e = (uint32_t)n_expert;  // out-of-range ids sort with the shared expert
-        key = (e << 10) | (uint32_t)p;                      // n_expert <= 32767, p < 1024: distinct keys
-    }
-    s_key[p] = key;
-    __syncthreads();
-    if (p >= n) return;
-    int rank = 0;
-    for (int i = 0; i < n; i++) rank += s_key[i] < key;
-    order[rank] = p;
-}
-
-mx_status launch_sort_pairs(const uint32_t *ids, int t, int top_k, int has_shared, int n_expert, int32_t *order,
-                            hipStream_t s) {
-    if ((int64_t)t * (top_k + has_shared) > SORT_PAIRS_MAX) return fail(MX_ERR_SHAPE, "sort_pairs: too many pairs");
-    if (t == 0) return MX_OK;
-    hipLaunchKernelGGL(k_sort_pairs, dim3(1), dim3(SORT_PAIRS_MAX), 0, s, ids, t, top_k, has_shared, n_expert,
-                       order);
-    MX_LAUNCH("k_sort_pairs");
-    return MX_OK;
 }
 
 }  // namespace mx
