@@ -595,11 +595,11 @@ mx_status moe_forward_impl(const mx_moe_layer *L, const float *x, int64_t t, con
             DecodeSelArgs sel{reinterpret_cast<const uint64_t *>(keys),
                               reinterpret_cast<const float *>(keys + (size_t)t * E * sizeof(uint64_t)), (int)E,
                               (int)t, scale, apply, L->weights_norm, ids, w};
-            for (int r = 0; r < rep(1); r++) MX_TRY(launch_decode_gate_up(L->gate.dtype, ga, (int)K, 0, &sel, s));
+            for (int r = 0; r < rep(1); r++) MX_TRY(launch_decode_select((int)K, sel, s));
         }
         MX_STAGE();
         for (int r = 0; r < (p.fused_router ? rep(2) : 1); r++)
-            MX_TRY(launch_decode_gate_up(L->gate.dtype, ga, 0, (int)K + (shf ? 1 : 0), nullptr, s));
+            MX_TRY(launch_decode_gate_up(L->gate.dtype, ga, 0, (int)K + (shf ? 1 : 0), s));
         MX_STAGE();
         for (int r = 0; r < (p.fused_router ? rep(3) : 1); r++) MX_TRY(launch_decode_down(L->down.dtype, da, s));
         MX_STAGE();

@@ -57,9 +57,9 @@ struct DecodeGateUpArgs {
     float *act;                          // [t, slots, ff], slots = top_k + (sh_gate != NULL)
     const uint8_t *xstage_gm;            // NULL, or the group-major copy of xstage (Q4_K / Q5_K reads)
 };
-// Optional top-k blocks in front of the gate/up blocks (decode router split):
-// block i < n_sel selects token i from keys/probs [n_sel, n_expert] (written by
-// launch_route_fused) into ids/w [n_sel, top_k].
+// Decode top-k (decode router split): block i < n_sel selects token i from
+// keys/probs [n_sel, n_expert] (written by launch_route_fused) into ids/w
+// [n_sel, top_k].
 struct DecodeSelArgs {
     const uint64_t *keys;
     const float *probs;
@@ -69,10 +69,10 @@ struct DecodeSelArgs {
     uint32_t *ids;
     float *w;
 };
+mx_status launch_decode_select(int top_k, const DecodeSelArgs &sel, hipStream_t s);
 // Slots slot0 .. slot0 + nslot - 1 of every token (slot top_k = the shared
-// expert, which must have the routed experts' quant type); sel may be NULL.
-mx_status launch_decode_gate_up(int dtype, const DecodeGateUpArgs &a, int slot0, int nslot,
-                                const DecodeSelArgs *sel, hipStream_t s);
+// expert, which must have the routed experts' quant type).
+mx_status launch_decode_gate_up(int dtype, const DecodeGateUpArgs &a, int slot0, int nslot, hipStream_t s);
 // true when the fused decode kernels take a layer of these shapes (their DMA
 // batches and LDS fit); checked before any launch of a forward
 bool decode_gate_up_fits(int dtype, int hidden, int64_t row_bytes);

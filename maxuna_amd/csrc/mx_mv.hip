@@ -305,8 +305,10 @@ constexpr int NG_MAX = MX_NG_MAX;
 // full_wave: a row whose groups fit one wave takes the whole wave (one group per
 // lane, lanes past G idle) instead of P = the largest power of two dividing G;
 // fewer activation registers per lane at the cost of idle lanes.
+// Built on the host and passed to the kernels as an argument (so no wave spends
+// scalar instructions on its divisions); lp = log2 P, lrpi = log2 RPI.
 template <int DT> struct Geo {
-    int G, P, NG, RPI;
+    int G, P, NG, RPI, lp, lrpi;
     __host__ __device__ explicit Geo(int k, bool full_wave = false) {
         G = (k / block_size(DT)) * Q<DT>::GPB;
         int p = G & (-G);
@@ -316,6 +318,9 @@ template <int DT> struct Geo {
         P = p;
         NG = (G + p - 1) / p;
         RPI = 64 / p;
+        lp = 0;
+        while ((1 << lp) < P) lp++;
+        lrpi = 6 - lp;
     }
 };
 
@@ -379,12 +384,14 @@ template <int DT, int NG, int NIT, int NM, int RING, class XPreF, class XPostF, 
 __device__ __forceinline__ void stream_rows(const uint8_t *const (&w)[NM], int64_t row_bytes, const Geo<DT> &geo,
                                             typename Q<DT>::X (&xs)[NG], int r_begin, int r_end, uint8_t *ring,
                                             int ni, XPreF &&pre, XPostF &&post, Sink &&sink) {
+    static_assert((NIT & (NIT - 1)) == 0, "NIT: a power of two");
+    constexpr int LNIT = NIT == 1 ? 0 : NIT == 2 ? 1 : NIT == 4 ? 2 : NIT == 8 ? 3 : 4;
     const int lane = threadIdx.x & 63;
     const int sub = lane & (geo.P - 1);
-    const int rsub = lane / geo.P;
-    const int step = NIT * geo.RPI;
+    const int rsub = lane >> geo.lp;
+    const int step = NIT << geo.lrpi;
     const int bstride = ni * 1024;
-    const int nbatch = (r_end - r_begin + step - 1) / step;
+    const int nbatch = (r_end - r_begin + step - 1) >> (LNIT + geo.lrpi);
     // the chunk range [base_m, base_m + 16 * nch_m) of matrix m's span for the batch at r0
     auto span = [&](int m, int r0, uintptr_t &base, int &nch) {
         const int r1 = min(r0 + step, r_end);
@@ -569,7 +576,7 @@ __host__ __device__ inline size_t align16(size_t v) { return (v + 15) & ~size_t(
 // grid (row tiles, t * top_k); one (token, slot) pair per block, its activation
 // row staged into LDS by the whole block, then one LDS ring per wave.
 template <int DT, int NG>
-__global__ void __launch_bounds__(64 * WAVES) k_mul_mv_id(MvArgs a, int ni) {
+__global__ void __launch_bounds__(64 * WAVES) k_mul_mv_id(MvArgs a, int ni, Geo<DT> geo) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int pair = blockIdx.y;  // token * top_k + slot
     const int tok = pair / a.top_k, slot = pair % a.top_k;
@@ -582,7 +589,6 @@ __global__ void __launch_bounds__(64 * WAVES) k_mul_mv_id(MvArgs a, int ni) {
     const uint8_t *const w[1] = {a.w + (int64_t)e * a.expert_bytes};
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (scalar)
     const int r0 = blockIdx.x * (WAVES * RW_MV) + wave * RW_MV;
-    const Geo<DT> geo(a.k);
     typename Q<DT>::X xs[NG];
     XPre xp;
     uint8_t *ring = lds + align16(xstage_bytes(a.k)) + wave * (RING_MV * ni * 1024);
@@ -617,7 +623,7 @@ static mx_status launch_mv_ng(const MvArgs &a, dim3 grid, hipStream_t s) {
     if (ni > DMA_MAX_INSTS) return fail(MX_ERR_SHAPE, "mul_mv_id: rows of %lld bytes are too long", (long long)a.row_bytes);
     const size_t lds = align16(xstage_bytes(a.k)) + (size_t)WAVES * RING_MV * ni * 1024;
     if (lds > 160 * 1024) return fail(MX_ERR_SHAPE, "mul_mv_id: k = %d needs %zu bytes of LDS", a.k, lds);
-    hipLaunchKernelGGL((k_mul_mv_id<DT, NG>), grid, dim3(64 * WAVES), lds, s, a, ni);
+    hipLaunchKernelGGL((k_mul_mv_id<DT, NG>), grid, dim3(64 * WAVES), lds, s, a, ni, Geo<DT>(a.k));
     return MX_OK;
 }
 
@@ -690,47 +696,23 @@ mx_status launch_mul_mv_id(int dtype, const MvArgs &a, hipStream_t s) {
 }
 
 // ---- fused decode: gate/up + SwiGLU ---------------------------------------------------
-// Flattened grid: sel.n_sel selection blocks, then (ff / (WAVES * RW_GU)) row
-// tiles x nslot slots x t tokens.  Slots slot0 .. slot0 + nslot - 1; slot
-// top_k (if present) is the shared expert, which then has the routed experts'
-// quant type and shape.
+// grid (ff / (WAVES * RW_GU) row tiles, nslot slots, t tokens): slots slot0 ..
+// slot0 + nslot - 1; slot top_k (if present) is the shared expert, which then has
+// the routed experts' quant type and shape.
 // act[tok, slot, r] = silu(gate_r . x) * (up_r . x), silu(g) = g / (1 + exp(-g)),
 // the product rounded on its own (silu_mul.metal:57-72).  The token row comes
 // staged from the router kernel (global memory).  Expert waves are independent.
-// Selection block i (decode router split, mx_route.hip) runs the top-k of
-// token i from the router's keys and writes ids / weights; the routed slots
-// are launched in the next kernel, which reads them.  The shared expert's
-// blocks need no routing, so they fill the machine while the selection runs.
+// The routed slots read the ids the selection kernel (k_decode_select, the
+// previous launch) wrote.
 #ifndef MX_GU_WPE
 #define MX_GU_WPE 5
 #endif
 template <int DT, int NG, bool GM>
-__global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(MX_GU_WPE))) k_decode_gate_up(DecodeGateUpArgs a, int ni, int slot0, int nslot,
-                                                               DecodeSelArgs sel) {
+__global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(MX_GU_WPE)))
+k_decode_gate_up(DecodeGateUpArgs a, int ni, int slot0, Geo<DT> geo) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    int bid = blockIdx.x;
-    if (bid < sel.n_sel) {
-        // the selection state lives in the dynamic LDS (a static __shared__ would be
-        // reserved by every block of the launch and cut the expert blocks' occupancy)
-        SelShared &sh = *reinterpret_cast<SelShared *>(lds);
-        const int64_t o = (int64_t)bid * sel.n_expert;
-        topk_from_keys(sel.keys + o, sel.probs + o, sel.n_expert, a.top_k, sel.scale, sel.apply_scale, sel.norm,
-                       sel.ids + (int64_t)bid * a.top_k, sel.w + (int64_t)bid * a.top_k, sh);
-        return;
-    }
-    bid -= sel.n_sel;
-    const int tiles = (a.ff + WAVES * RW_GU - 1) / (WAVES * RW_GU);
     const int slots = a.top_k + (a.sh_gate ? 1 : 0);
-    int tile, slot, tok;
-    if (sel.n_sel == 0) {  // grid (tiles, nslot, t)
-        tile = blockIdx.x;
-        slot = slot0 + blockIdx.y;
-        tok = blockIdx.z;
-    } else {
-        tile = bid % tiles;
-        slot = slot0 + (bid / tiles) % nslot;
-        tok = bid / (tiles * nslot);
-    }
+    const int tile = blockIdx.x, slot = slot0 + blockIdx.y, tok = blockIdx.z;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (scalar)
     const int r0 = tile * (WAVES * RW_GU) + wave * RW_GU;
     if (r0 >= a.ff) return;  // wave-uniform; no block barrier below
@@ -749,7 +731,6 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
         rb = a.sh_row_bytes;
     }
     const uint8_t *const w[2] = {gw, uw};
-    const Geo<DT> geo(a.hidden);
     typename Q<DT>::X xs[NG];
     const uint8_t *staged = a.xstage + (int64_t)tok * xstage_stride(a.hidden);
     uint8_t *ring = lds + wave * (RING_GU * ni * 1024);
@@ -778,59 +759,50 @@ __global__ void __launch_bounds__(SEL_THREADS) k_decode_select(int top_k, Decode
 }
 
 template <int DT, int NG>
-static mx_status launch_gu_ng(const DecodeGateUpArgs &a, unsigned blocks, int slot0, int nslot,
-                              const DecodeSelArgs &sel, hipStream_t s) {
+static mx_status launch_gu_ng(const DecodeGateUpArgs &a, int slot0, int nslot, hipStream_t s) {
     const unsigned tiles = (unsigned)((a.ff + WAVES * RW_GU - 1) / (WAVES * RW_GU));
-    const dim3 grid = sel.n_sel == 0 ? dim3(tiles, (unsigned)nslot, (unsigned)a.t) : dim3(blocks);
+    const dim3 grid(tiles, (unsigned)nslot, (unsigned)a.t);
     constexpr bool GM_OK = DT == kQ4_K || DT == kQ5_K;
     const int ni = ring_insts<DT, NG>(2, a.hidden, a.gu_row_bytes);
-    if (ni > DMA_MAX_INSTS) return fail(MX_ERR_SHAPE, "decode gate/up: rows too long for the LDS ring");
-    size_t lds = (size_t)WAVES * RING_GU * ni * 1024;
-    if (sel.n_sel && lds < sizeof(SelShared)) lds = sizeof(SelShared);
-    if (lds > 160 * 1024) return fail(MX_ERR_SHAPE, "decode gate/up: hidden = %d needs %zu bytes of LDS", a.hidden, lds);
+    const size_t lds = (size_t)WAVES * RING_GU * ni * 1024;
+    const Geo<DT> geo(a.hidden);
     if (GM_OK && a.xstage_gm)
-        hipLaunchKernelGGL((k_decode_gate_up<DT, NG, GM_OK>), grid, dim3(64 * WAVES), lds, s, a, ni, slot0, nslot, sel);
+        hipLaunchKernelGGL((k_decode_gate_up<DT, NG, GM_OK>), grid, dim3(64 * WAVES), lds, s, a, ni, slot0, geo);
     else
-        hipLaunchKernelGGL((k_decode_gate_up<DT, NG, false>), grid, dim3(64 * WAVES), lds, s, a, ni, slot0, nslot, sel);
+        hipLaunchKernelGGL((k_decode_gate_up<DT, NG, false>), grid, dim3(64 * WAVES), lds, s, a, ni, slot0, geo);
     return MX_OK;
 }
 
 template <int DT>
-static mx_status launch_gu_dt(const DecodeGateUpArgs &a, unsigned blocks, int slot0, int nslot,
-                              const DecodeSelArgs &sel, hipStream_t s) {
+static mx_status launch_gu_dt(const DecodeGateUpArgs &a, int slot0, int nslot, hipStream_t s) {
     const int ng = ng_variant(Geo<DT>(a.hidden).NG);
-#define MX_L(N) return launch_gu_ng<DT, N>(a, blocks, slot0, nslot, sel, s)
+#define MX_L(N) return launch_gu_ng<DT, N>(a, slot0, nslot, s)
     MX_NG_SWITCH(ng, MX_L)
 #undef MX_L
     return MX_OK;
 }
 
-mx_status launch_decode_gate_up(int dtype, const DecodeGateUpArgs &a, int slot0, int nslot,
-                                const DecodeSelArgs *sel, hipStream_t s) {
-    DecodeSelArgs none{};
-    const DecodeSelArgs &sa = sel ? *sel : none;
-    if (a.t == 0) return MX_OK;
-    if (sa.n_sel && (sa.n_expert > SEL_MAX_E || a.top_k > SEL_MAX_K || (nslot > 0 && 64 * WAVES != SEL_THREADS)))
+mx_status launch_decode_select(int top_k, const DecodeSelArgs &sel, hipStream_t s) {
+    if (sel.n_sel == 0) return MX_OK;
+    if (sel.n_expert > SEL_MAX_E || top_k > SEL_MAX_K)
         return fail(MX_ERR_SHAPE, "decode select: n_expert <= %d and top_k <= %d", SEL_MAX_E, SEL_MAX_K);
-    if (nslot == 0) {
-        if (sa.n_sel == 0) return MX_OK;
-        hipLaunchKernelGGL(k_decode_select, dim3((unsigned)sa.n_sel), dim3(SEL_THREADS), sizeof(SelShared), s,
-                           a.top_k, sa);
-        MX_LAUNCH("k_decode_select");
-        return MX_OK;
-    }
-    const int64_t tiles = (a.ff + WAVES * RW_GU - 1) / (WAVES * RW_GU);
-    const int64_t blocks = sa.n_sel + tiles * nslot * a.t;
-    if (blocks == 0) return MX_OK;
-    if (blocks > INT32_MAX) return fail(MX_ERR_OVERFLOW, "decode gate/up: grid too large");
+    hipLaunchKernelGGL(k_decode_select, dim3((unsigned)sel.n_sel), dim3(SEL_THREADS), sizeof(SelShared), s, top_k,
+                       sel);
+    MX_LAUNCH("k_decode_select");
+    return MX_OK;
+}
+
+mx_status launch_decode_gate_up(int dtype, const DecodeGateUpArgs &a, int slot0, int nslot, hipStream_t s) {
+    if (a.t == 0 || nslot == 0) return MX_OK;
+    if ((int64_t)a.t > 65535 || nslot > 65535) return fail(MX_ERR_OVERFLOW, "decode gate/up: grid too large");
     if (a.hidden % 32) return fail(MX_ERR_BLOCK, "decode gate/up: hidden must be a multiple of 32");
     if (a.sh_gate && a.sh_row_bytes != a.gu_row_bytes)
         return fail(MX_ERR_SHAPE, "decode gate/up: shared expert rows must match the routed rows");
     switch (dtype) {
-    case kQ4_K: MX_TRY(launch_gu_dt<kQ4_K>(a, (unsigned)blocks, slot0, nslot, sa, s)); break;
-    case kQ5_K: MX_TRY(launch_gu_dt<kQ5_K>(a, (unsigned)blocks, slot0, nslot, sa, s)); break;
-    case kQ6_K: MX_TRY(launch_gu_dt<kQ6_K>(a, (unsigned)blocks, slot0, nslot, sa, s)); break;
-    default: MX_TRY(launch_gu_dt<kQ8_0>(a, (unsigned)blocks, slot0, nslot, sa, s)); break;
+    case kQ4_K: MX_TRY(launch_gu_dt<kQ4_K>(a, slot0, nslot, s)); break;
+    case kQ5_K: MX_TRY(launch_gu_dt<kQ5_K>(a, slot0, nslot, s)); break;
+    case kQ6_K: MX_TRY(launch_gu_dt<kQ6_K>(a, slot0, nslot, s)); break;
+    default: MX_TRY(launch_gu_dt<kQ8_0>(a, slot0, nslot, s)); break;
     }
     MX_LAUNCH("k_decode_gate_up");
     return MX_OK;
@@ -846,7 +818,7 @@ mx_status launch_decode_gate_up(int dtype, const DecodeGateUpArgs &a, int slot0,
 #define MX_DN_WPE 1
 #endif
 template <int DT, int NG>
-__global__ void __launch_bounds__(64 * WAVES_DN) __attribute__((amdgpu_waves_per_eu(MX_DN_WPE))) k_decode_down(DecodeDownArgs a, int ni) {
+__global__ void __launch_bounds__(64 * WAVES_DN) __attribute__((amdgpu_waves_per_eu(MX_DN_WPE))) k_decode_down(DecodeDownArgs a, int ni, Geo<DT> geo) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int slots = a.top_k + (a.sh_down ? 1 : 0);
     const int slot = blockIdx.y, tok = blockIdx.z, tile = blockIdx.x;  // grid (row tiles, slots, t)
@@ -873,7 +845,6 @@ __global__ void __launch_bounds__(64 * WAVES_DN) __attribute__((amdgpu_waves_per
         rb = a.sh_row_bytes;
     }
     const uint8_t *const w[1] = {wp};
-    const Geo<DT> geo(a.ff, DN_FULL);
     typename Q<DT>::X xs[NG];
     float *part = a.part + ((int64_t)tok * slots + slot) * a.hidden;
     stream_rows<DT, NG, BatchDn<NG>::NIT, 1, RING_DN>(w, rb, geo, xs, r0, min(r0 + RW_DN, a.hidden), ring, ni,
@@ -911,7 +882,7 @@ __host__ __device__ inline size_t dn_slot_area(int ff, int ni) {
 }
 constexpr int XPRE_W = 4;  // act quarters per lane held in registers before the weight copies
 template <int DT, int NG>
-__global__ void __launch_bounds__(64 * DN_SLOTS_MAX) k_decode_down_slots(DecodeDownArgs a, int ni) {
+__global__ void __launch_bounds__(64 * DN_SLOTS_MAX) k_decode_down_slots(DecodeDownArgs a, int ni, Geo<DT> geo) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     __shared__ float s_part[DN_SLOTS_MAX][RW_DN];
     const int slots = a.top_k + (a.sh_down ? 1 : 0);
@@ -936,7 +907,6 @@ __global__ void __launch_bounds__(64 * DN_SLOTS_MAX) k_decode_down_slots(DecodeD
         rb = a.sh_row_bytes;
     }
     const uint8_t *const w[1] = {wp};
-    const Geo<DT> geo(a.ff, DN_FULL);
     typename Q<DT>::X xs[NG];
     stream_rows<DT, NG, BatchDnSlots<NG>::NIT, 1, RING_DN>(w, rb, geo, xs, r0, r1, ring, ni,
                                                      [&] { stage_pre_t(xrow, a.ff, xp, lane, 64); },
@@ -968,7 +938,7 @@ static mx_status launch_dn_slots_ng(const DecodeDownArgs &a, hipStream_t s) {
     const int slots = a.top_k + (a.sh_down ? 1 : 0);
     const size_t lds = (size_t)slots * dn_slot_area(a.ff, ni);
     const dim3 grid((unsigned)((a.hidden + RW_DN - 1) / RW_DN), (unsigned)a.t);
-    hipLaunchKernelGGL((k_decode_down_slots<DT, NG>), grid, dim3(64 * slots), lds, s, a, ni);
+    hipLaunchKernelGGL((k_decode_down_slots<DT, NG>), grid, dim3(64 * slots), lds, s, a, ni, Geo<DT>(a.ff, DN_FULL));
     return MX_OK;
 }
 // LDS bytes of the slot-per-wave kernel (SIZE_MAX: its DMA batch does not fit)
@@ -1008,7 +978,7 @@ static mx_status launch_dn_ng(const DecodeDownArgs &a, dim3 grid, hipStream_t s)
     if (ni > DMA_MAX_INSTS) return fail(MX_ERR_SHAPE, "decode down: rows too long for the LDS ring");
     const size_t lds = align16(xstage_bytes(a.ff)) + (size_t)WAVES_DN * RING_DN * ni * 1024;
     if (lds > 160 * 1024) return fail(MX_ERR_SHAPE, "decode down: expert_ff = %d needs %zu bytes of LDS", a.ff, lds);
-    hipLaunchKernelGGL((k_decode_down<DT, NG>), grid, dim3(64 * WAVES_DN), lds, s, a, ni);
+    hipLaunchKernelGGL((k_decode_down<DT, NG>), grid, dim3(64 * WAVES_DN), lds, s, a, ni, Geo<DT>(a.ff, DN_FULL));
     return MX_OK;
 }
 
