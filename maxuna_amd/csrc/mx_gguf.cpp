@@ -268,7 +268,14 @@ mx_status parse(mx_gguf *g) {
         t.ggml_type = (int32_t)type;
         t.offset = off;  // relative for now
         const TypeGeom tg = ggml_geom(type);
-        const unsigned __int128 n = (unsigned __int128)t.ne[0] * t.ne[1] * t.ne[2] * t.ne[3];
+        // element count, dimension by dimension, rejected as soon as it passes 2^62
+        // (four 2^40 dimensions would overflow even a 128-bit product)
+        unsigned __int128 n = 1;
+        for (int d = 0; d < 4; d++) {
+            n *= (uint64_t)t.ne[d];
+            if (n > ((unsigned __int128)1 << 62))
+                return fail(MX_ERR_FORMAT, "gguf: tensor %s has more than 2^62 elements", g->names[i].c_str());
+        }
         if (tg.block) {
             if (t.ne[0] % tg.block)
                 return fail(MX_ERR_FORMAT, "gguf: tensor %s row of %lld is not a multiple of its block size %lld",

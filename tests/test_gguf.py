@@ -124,3 +124,17 @@ def test_malformed_files_fail_cleanly(tmp_path):
     with pytest.raises(MaxunaError) as e:
         G.GgufFile(tmp_path / "absent.gguf")
     assert e.value.code == 11
+
+
+def test_element_count_overflow_rejected(tmp_path):
+    """Four dimensions of 2^40 each multiply past any 128-bit product: the
+    reader rejects the tensor as soon as its running element count passes 2^62
+    instead of wrapping to a small size."""
+    raw = b"GGUF" + struct.pack("<IQQ", 3, 1, 0)
+    raw += _s(b"huge") + struct.pack("<I", 4) + struct.pack("<QQQQ", 2**40, 2**40, 2**40, 2**40)
+    raw += struct.pack("<IQ", 0, 0)
+    raw += b"\0" * ((len(raw) + 31) // 32 * 32 - len(raw)) + b"\0" * 64
+    p = tmp_path / "huge.gguf"
+    p.write_bytes(raw)
+    with pytest.raises(MaxunaError, match="more than 2\\^62 elements"):
+        G.GgufFile(p)
