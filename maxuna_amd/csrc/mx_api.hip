@@ -520,8 +520,7 @@ mx_status moe_forward_impl(const mx_moe_layer *L, const float *x, int64_t t, con
     // routing (+ the RMSNorm of the FFN half when requested)
     if (p.fused_router) {
         // logits -> keys/probs; the router also stages the (normalised) rows for the
-        // decode expert kernels.  The top-k runs in the selection blocks of the next
-        // launch (below).
+        // decode expert kernels.  The top-k is its own launch (k_decode_select, below).
         for (int r = 0; r < rep(0); r++)
             MX_TRY(launch_route_fused(x, L->rms_alpha, L->rms_eps, o.x_normed, L->router, L->exp_probs_b, (int)t,
                                       (int)H, (int)E, o.route_ws, o.xstage, o.xstage_gm, s));
