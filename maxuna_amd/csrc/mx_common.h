@@ -79,6 +79,19 @@ __device__ __forceinline__ void q4k_scale_min(int j, uint32_t s0, uint32_t s1, u
     }
 }
 
+// The scales and mins of sub-blocks 2i and 2i + 1 (i in 0..3, may differ per
+// lane) without a branch: byte 0 of sc / m is sub-block 2i's 6-bit value, byte 1
+// sub-block 2i + 1's -- the same bits as q4k_scale_min(2i) and (2i + 1).
+__device__ __forceinline__ void q4k_pair_scale_min(int i, uint32_t s0, uint32_t s1, uint32_t s2,
+                                                   uint32_t &sc, uint32_t &m) {
+    const uint32_t b = 16u * (uint32_t)(i & 1);  // bit offset of byte (2i) mod 4
+    const uint32_t a0 = __builtin_amdgcn_ubfe(s0, b, 16), a1 = __builtin_amdgcn_ubfe(s1, b, 16);
+    const uint32_t a2 = __builtin_amdgcn_ubfe(s2, b, 16);
+    const bool upper = i >= 2;  // sub-blocks 4..7: low nibbles in scales[8..11], top bits in scales[0..3]
+    sc = upper ? (a2 & 0x0F0Fu) | ((a0 >> 2) & 0x3030u) : a0 & 0x3F3Fu;
+    m = upper ? ((a2 >> 4) & 0x0F0Fu) | ((a1 >> 2) & 0x3030u) : a1 & 0x3F3Fu;
+}
+
 // The value held by this lane's partner for O in {1, 2, 4, 8, 16, 32}, exchanged
 // without LDS (DPP / permlane).  The partner differs from the lane in bit log2(O)
 // and possibly in lower bits, never in higher ones: lane ^ 1, ^ 2, ^ 7

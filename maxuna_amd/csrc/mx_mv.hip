@@ -128,14 +128,14 @@ template <> struct Q<kQ4_K> {
             bl = dot4(hi, x.l[8 + w], bl);
         }
         const float A = planes(ah, am, al), B = planes(bh, bm, bl);
-        uint32_t sc0, m0, sc1, m1;
-        q4k_scale_min(2 * i, s0, s1, s2, sc0, m0);
-        q4k_scale_min(2 * i + 1, s0, s1, s2, sc1, m1);
+        uint32_t sc, mn;
+        q4k_pair_scale_min(i, s0, s1, s2, sc, mn);
         const float d = h2f((uint16_t)(hd0 & 0xFFFFu));
         const float dmin = h2f((uint16_t)(hd0 >> 16));
-        // sa, sb are powers of two: (float)sc * sa is exact
-        const float p = __builtin_fmaf((float)sc0 * x.sa, A, (float)sc1 * x.sb * B);
-        const float m = __builtin_fmaf((float)m0, x.ssa, (float)m1 * x.ssb);
+        const float sc0 = (float)(sc & 0xFFu), sc1 = (float)(sc >> 8), m0 = (float)(mn & 0xFFu), m1 = (float)(mn >> 8);
+        // sa, sb are powers of two: sc * sa is exact
+        const float p = __builtin_fmaf(sc0 * x.sa, A, sc1 * x.sb * B);
+        const float m = __builtin_fmaf(m0, x.ssa, m1 * x.ssb);
         return __builtin_fmaf(d, p, -dmin * m);
     }
     __device__ static float dot(const Raw &r, int g, const X &x) {
@@ -380,7 +380,11 @@ __device__ __forceinline__ void reduce_tuples(float (&v)[NB][NM], int P, int sub
 // as the aligned 16-byte chunks covering it, packed back to back.  `pre`
 // issues the activation loads before the first copies, `post` finishes filling
 // `xs`.  sink(row, sums[NM]) runs once per row with the fully reduced sums.
-template <int DT, int NG, int NIT, int NM, int RING, class XPreF, class XPostF, class Sink>
+// EARLY (RING == 1): a batch's weight words are read from LDS into registers
+// first, then the next batch's copy is issued into the same buffer, then the
+// batch is computed from registers -- the copy overlaps the compute without a
+// second buffer.
+template <int DT, int NG, int NIT, int NM, int RING, class XPreF, class XPostF, class Sink, bool EARLY = false>
 __device__ __forceinline__ void stream_rows(const uint8_t *const (&w)[NM], int64_t row_bytes, const Geo<DT> &geo,
                                             typename Q<DT>::X (&xs)[NG], int r_begin, int r_end, uint8_t *ring,
                                             int ni, XPreF &&pre, XPostF &&post, Sink &&sink) {
@@ -435,6 +439,39 @@ __device__ __forceinline__ void stream_rows(const uint8_t *const (&w)[NM], int64
         }
         const int rb32 = (int)row_bytes;
         float acc[NIT][NM];
+        if constexpr (EARLY) {
+            typename Q<DT>::Raw raw[NIT][NM][NG];
+#pragma unroll
+            for (int ib = 0; ib < NIT; ib++) {
+                const int row = min(r0 + rsub + geo.RPI * ib, r_end - 1);
+#pragma unroll
+                for (int m = 0; m < NM; m++) {
+                    const uint8_t *rl = ring + moff[m] + (row - r0) * rb32;
+#pragma unroll
+                    for (int jg = 0; jg < NG; jg++) {
+                        const int g = sub + geo.P * jg;
+                        raw[ib][m][jg] = Q<DT>::load(rl, g < geo.G ? g : 0);
+                    }
+                }
+            }
+            // the buffer's words are in registers: the next batch may overwrite it
+            wait_lgkmcnt0();
+            if (bi + 1 < nbatch) issue(bi + 1);
+#pragma unroll
+            for (int ib = 0; ib < NIT; ib++) {
+                const bool ok = r0 + rsub + geo.RPI * ib < r_end;
+#pragma unroll
+                for (int m = 0; m < NM; m++) {
+                    float a = 0.f;
+#pragma unroll
+                    for (int jg = 0; jg < NG; jg++) {
+                        const int g = sub + geo.P * jg;
+                        if (ok && g < geo.G) a += Q<DT>::dot(raw[ib][m][jg], g, xs[jg]);
+                    }
+                    acc[ib][m] = a;
+                }
+            }
+        } else
 #pragma unroll
         for (int ib = 0; ib < NIT; ib++) {
             const int row = r0 + rsub + geo.RPI * ib;
@@ -469,6 +506,17 @@ __device__ __forceinline__ void stream_rows(const uint8_t *const (&w)[NM], int64
             }
         }
     };
+    if constexpr (EARLY) {
+        static_assert(RING == 1, "EARLY re-issues into the one buffer");
+        pre();
+        if (nbatch > 0) issue(0);
+        post();
+        for (int bi = 0; bi < nbatch; bi++) {
+            wait_vmcnt(0);
+            process(bi);
+        }
+        return;
+    }
     pre();
     for (int bi = 0; bi < RING - 1 && bi < nbatch; bi++) issue(bi);
     post();
@@ -532,6 +580,10 @@ __device__ __forceinline__ void load_xs(const uint8_t *staged, int k, const Geo<
 #ifndef MX_RING_GU
 #define MX_RING_GU 1
 #endif
+#ifndef MX_GU_EARLY
+#define MX_GU_EARLY 0
+#endif
+constexpr bool GU_EARLY = MX_GU_EARLY != 0;
 #ifndef MX_RW_DN
 #define MX_RW_DN 16
 #endif
@@ -740,12 +792,110 @@ k_decode_gate_up(DecodeGateUpArgs a, int ni, int slot0, Geo<DT> geo) {
         if constexpr (GM) load_xs_gm<DT, NG>(a.xstage_gm + (int64_t)tok * xstage_gm_stride(a.hidden), a.hidden, geo, xs);
         else load_xs<DT, NG>(staged, a.hidden, geo, xs);
     };
-    stream_rows<DT, NG, Batch<NG>::NIT, 2, RING_GU>(w, rb, geo, xs, r0, min(r0 + RW_GU, a.ff), ring, ni, pre, [] {},
-                                                     [&](int row, const float (&s)[2]) {
-                                                         const float g = s[0];
-                                                         const float sg = g / (1.0f + expf(-g));
-                                                         act[row] = sg * s[1];
-                                                     });
+    auto sink = [&](int row, const float (&s)[2]) {
+        const float g = s[0];
+        const float sg = g / (1.0f + expf(-g));
+        act[row] = sg * s[1];
+    };
+    auto nopost = [] {};
+    stream_rows<DT, NG, Batch<NG>::NIT, 2, RING_GU, decltype(pre) &, decltype(nopost) &, decltype(sink) &, GU_EARLY>(
+        w, rb, geo, xs, r0, min(r0 + RW_GU, a.ff), ring, ni, pre, nopost, sink);
+}
+
+// Gate/up rows of exactly 64 groups (Q4_K / Q5_K at hidden 4096, 16-byte-aligned
+// rows): the geometry is compile-time -- one group per lane, one row pair per
+// iteration, no masked lanes -- and each wave takes R consecutive row pairs of its
+// (slot, token).  The wave's one LDS buffer holds a gate row and an up row; as
+// soon as the current pair's words are in registers the next pair's copy is
+// issued into it, so the copy overlaps the dot products.  Sums and SwiGLU are the
+// generic kernel's, operation for operation (the 64-lane sums in the same order).
+#ifndef MX_GU64_R
+#define MX_GU64_R 2
+#endif
+constexpr int GU64_R = MX_GU64_R;
+template <int DT> struct Row64 {
+    static_assert(DT == kQ4_K || DT == kQ5_K, "64-group rows: the K-quants with 64-weight groups");
+    static constexpr int RB = 16 * (DT == kQ4_K ? 144 : 176);  // row bytes (16 super-blocks)
+    static constexpr int CH = RB / 16, NI = (CH + 63) / 64;     // 16-byte chunks, copy instructions
+};
+template <int DT, int R>
+__global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(MX_GU_WPE)))
+k_decode_gate_up64(DecodeGateUpArgs a, int slot0, Geo<DT> geo) {
+    constexpr int RB = Row64<DT>::RB, CH = Row64<DT>::CH, NI = Row64<DT>::NI;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const int slots = a.top_k + (a.sh_gate ? 1 : 0);
+    const int slot = slot0 + blockIdx.y, tok = blockIdx.z;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int r0 = (blockIdx.x * WAVES + wave) * R;
+    if (r0 >= a.ff) return;  // wave-uniform; no block barrier below
+    const int n = min(R, a.ff - r0);
+    typename Q<DT>::X xs[1];
+    load_xs_gm<DT, 1>(a.xstage_gm + (int64_t)tok * xstage_gm_stride(a.hidden), a.hidden, geo, xs);
+    const uint8_t *gw, *uw;
+    if (slot < a.top_k) {
+        const uint32_t id = a.ids[tok * a.top_k + slot];
+        const int e = id < (uint32_t)a.n_expert ? (int)id : a.n_expert - 1;
+        gw = a.gate + (int64_t)e * a.gu_expert_bytes;
+        uw = a.up + (int64_t)e * a.gu_expert_bytes;
+    } else {
+        gw = a.sh_gate;
+        uw = a.sh_up;
+    }
+    gw += (int64_t)r0 * RB;
+    uw += (int64_t)r0 * RB;
+    uint8_t *buf = lds + wave * (2 * RB);
+    // row r of matrix m (0 gate, 1 up) into the matrix's half of the buffer; every
+    // address a scalar base plus a 32-bit lane offset
+    auto issue = [&](int m, int r) {
+        const uint8_t *src = (m ? uw : gw) + r * RB;
+#pragma unroll
+        for (int q = 0; q < NI; q++) {
+            const int ci = 64 * q + lane;
+            if (q < NI - 1 || ci < CH) dma16(src + (uint32_t)(16 * ci), buf + m * RB + 1024 * q);
+        }
+        asm volatile("" ::: "memory");
+    };
+    float res[R];
+    issue(0, 0);
+    issue(1, 0);
+    // Only the copies count in vmcnt inside the loop (the act stores come after it):
+    // when row r's gate copy is waited for, at most row r's up copy is younger; when
+    // its up copy is, at most row r + 1's gate copy.
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        if (r < n) {
+            float v2[2];
+#pragma unroll
+            for (int m = 0; m < 2; m++) {
+                if (m == 0 || r + 1 >= n) wait_vmcnt(m == 0 ? NI : 0);
+                else wait_vmcnt(NI);
+                const typename Q<DT>::Raw rw = Q<DT>::load(buf + m * RB, lane);
+                if (r + 1 < n) {
+                    wait_lgkmcnt0();  // the words are in registers: the half may be overwritten
+                    issue(m, r + 1);
+                }
+                v2[m] = Q<DT>::dot(rw, lane, xs[0]);
+            }
+            // 64-lane sums of g and u: lanes 0-31 keep g, 32-63 keep u after the first step
+            const bool hi = (lane & 32) != 0;
+            float v = (hi ? v2[1] : v2[0]) + lane_partner<32>(hi ? v2[0] : v2[1]);
+            v += lane_partner<16>(v);
+            v += lane_partner<8>(v);
+            v += lane_partner<4>(v);
+            v += lane_partner<2>(v);
+            v += lane_partner<1>(v);
+            const float G = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+            const float U = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+            res[r] = G / (1.0f + expf(-G)) * U;
+        }
+    }
+    float *act = a.act + ((int64_t)tok * slots + slot) * a.ff + r0;
+    if (lane < n) {
+#pragma unroll
+        for (int r = 0; r < R; r++)
+            if (r == lane) act[r] = res[r];
+    }
 }
 
 // The selection blocks alone (a launch with no expert slots): their own kernel,
@@ -773,8 +923,33 @@ static mx_status launch_gu_ng(const DecodeGateUpArgs &a, int slot0, int nslot, h
     return MX_OK;
 }
 
+// the 64-group kernel's conditions: Q4_K / Q5_K, 64 groups per row, 16-byte-aligned
+// rows and experts, and the group-major staged activation
+template <int DT>
+static bool gu64_ok(const DecodeGateUpArgs &a) {
+    if constexpr (DT != kQ4_K) {  // (Q5_K's extra high-bit words spill at this occupancy)
+        (void)a;
+        return false;
+    } else {
+        auto al = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+        return GU64_R > 0 && Geo<DT>(a.hidden).G == 64 && a.gu_row_bytes == Row64<DT>::RB &&
+               a.gu_expert_bytes % 16 == 0 && al(a.gate) && al(a.up) && a.xstage_gm &&
+               (!a.sh_gate || (al(a.sh_gate) && al(a.sh_up)));
+    }
+}
+
 template <int DT>
 static mx_status launch_gu_dt(const DecodeGateUpArgs &a, int slot0, int nslot, hipStream_t s) {
+    if constexpr (DT == kQ4_K || DT == kQ5_K) {
+        if (gu64_ok<DT>(a)) {
+            const unsigned tiles = (unsigned)((a.ff + WAVES * GU64_R - 1) / (WAVES * GU64_R));
+            const dim3 grid(tiles, (unsigned)nslot, (unsigned)a.t);
+            const size_t lds = (size_t)WAVES * 2 * Row64<DT>::RB;
+            hipLaunchKernelGGL((k_decode_gate_up64<DT, (GU64_R > 0 ? GU64_R : 1)>), grid, dim3(64 * WAVES), lds, s, a, slot0,
+                               Geo<DT>(a.hidden));
+            return MX_OK;
+        }
+    }
     const int ng = ng_variant(Geo<DT>(a.hidden).NG);
 #define MX_L(N) return launch_gu_ng<DT, N>(a, slot0, nslot, s)
     MX_NG_SWITCH(ng, MX_L)
