@@ -31,10 +31,12 @@
 // act = silu(g) * u is lane-local; act is written f32 at the pair's bucket
 // position) or plain (f32 rows scattered to the pair's output row).
 //
-// Work items are (m-tile, n-tile) pairs, m-tile fastest; blocks are dealt to
-// the 8 XCDs round-robin by the hardware, so block b takes item
-// (b % 8) * per + b / 8: each XCD works through a contiguous run of items, and
-// the m-tiles of one expert that share a weight slice run together on one L2.
+// Work items are (m-tile, n-tile) pairs, ordered expert by expert (within an
+// expert n-tile-major, m-tile fastest); blocks are dealt to the 8 XCDs
+// round-robin by the hardware, so block b takes item (b % 8) * per + b / 8: each
+// XCD works through a contiguous run of items, so the m-tiles of one expert that
+// share a weight slice, and the n-tiles that share its A rows, run together on
+// one L2.
 #include "mx_launch.h"
 #include "mx_dma.h"
 
@@ -339,6 +341,13 @@ template <int DT> __device__ __forceinline__ void wb_load(WB<DT> &w, const uint8
     else w.load_lds(slot, kh, m1);
 }
 
+#ifndef MX_GEMM_BPAD
+#define MX_GEMM_BPAD 2
+#endif
+#ifndef MX_GEMM_EXPERT_ORDER
+#define MX_GEMM_EXPERT_ORDER 1
+#endif
+
 struct Tile {
     int e, pos0, mrows, nt;
 };
@@ -353,11 +362,27 @@ __device__ __forceinline__ bool tile_of(const GemmArgs &a, int nt_count, Tile &t
     if (local >= per) return false;
     const int item = xcd * per + local;
     if (item >= n_items) return false;
+#if MX_GEMM_EXPERT_ORDER
+    // expert-major items: an expert's T m-tiles x nt_count n-tiles are consecutive,
+    // n-tile-major, so an XCD works through one expert's A rows and weight slices
+    // together (its L2 serves the repeats).  Tiles list each expert's m-tiles in
+    // order, so item / nt_count falls on one of the item's expert's tiles.
+    const int j0 = item / nt_count;
+    const int w0 = a.map[L.tiles + j0];
+    t.e = w0 >> 16;
+    const int first = j0 - (w0 & 0xFFFF);  // the expert's first tile
+    const int cnt = a.map[L.tpe + t.e];
+    const int T = (cnt + GM_BM - 1) / GM_BM;
+    const int loc = item - first * nt_count;
+    t.nt = loc / T;
+    const int mt = loc - t.nt * T;
+#else
     t.nt = item / n_mt;
     const int word = a.map[L.tiles + item % n_mt];
     t.e = word >> 16;
     const int mt = word & 0xFFFF;
     const int cnt = a.map[L.tpe + t.e];
+#endif
     t.mrows = min(GM_BM, cnt - mt * GM_BM);
     t.pos0 = a.map[L.off + t.e] + mt * GM_BM;
     return true;
@@ -369,6 +394,23 @@ template <int DT, bool SWIGLU> struct GemmWpe {
     static constexpr int v = GemmNb<DT, SWIGLU>::waves == 8 ? 2 : 1;
 };
 
+// B slot layout in LDS.  Row R's slot starts at byte R * SLOT, plus PAD spare
+// 16-byte chunks after every 16 rows.  With SLOT = 176 (44 dwords) rows j and
+// j + 16 of a wave's 32 lanes would otherwise start on the same LDS bank
+// (44 * 16 = 704 = 11 * 64 dwords): a two-way conflict on every dword read of the
+// 2-byte-aligned types.  Two spare chunks shift row j + 16 by 8 banks, which also
+// keeps the other lane half (16 bytes further on) and the four row phases of the
+// 2-byte-aligned blocks on distinct banks.  Only the plain tiles pad (a SwiGLU
+// tile's copies must not straddle its two matrices).
+template <int DT, bool SWIGLU> struct BSlots {
+    static constexpr int CPR = WB<DT>::CPR, SLOT = WB<DT>::SLOT;
+    static constexpr int PAD = (!SWIGLU && (DT == kQ6_K || DT == kQ8_0)) ? MX_GEMM_BPAD : 0;
+    static constexpr int GROUP = 16 * CPR + PAD;  // positions per 16 rows
+    __device__ static int row_off(int R) { return R * SLOT + 16 * PAD * (R >> 4); }
+    static constexpr int bytes(int rows) { return rows * SLOT + 16 * PAD * (rows / 16); }
+    static constexpr int positions(int rows) { return rows * CPR + PAD * (rows / 16); }
+};
+
 template <int DT, bool SWIGLU>
 __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
     __attribute__((amdgpu_waves_per_eu(GemmWpe<DT, SWIGLU>::v))) k_gemm(GemmArgs a) {
@@ -376,17 +418,21 @@ __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
     constexpr int NWAVE = GemmNb<DT, SWIGLU>::waves;
     constexpr int DMA_PER_WAVE = STAGE_BYTES / 1024 / NWAVE;
     constexpr int BROWS = GemmNb<DT, SWIGLU>::bn;           // weight rows of the tile
-    constexpr int CPR = WB<DT>::CPR, SLOT = WB<DT>::SLOT;
-    constexpr int B_INSTS = BROWS * CPR / 64;                // B copy instructions per stage
+    using BS = BSlots<DT, SWIGLU>;
+    constexpr int CPR = BS::CPR;
+    constexpr int B_POS = BS::positions(BROWS);
+    constexpr int B_INSTS = (B_POS + 63) / 64;                 // B copy instructions per stage
     constexpr int B_PER_MAT = SWIGLU ? B_INSTS / 2 : B_INSTS; // instructions per matrix (gate / up)
-    static_assert((BROWS * CPR) % 64 == 0 && (!SWIGLU || B_INSTS % 2 == 0), "B copies must not straddle matrices");
+    static_assert(BS::PAD ? !SWIGLU : ((BROWS * CPR) % 64 == 0 && (!SWIGLU || B_INSTS % 2 == 0)),
+                  "B copies must not straddle matrices");
+    static_assert(BROWS % 16 == 0, "whole 16-row slot groups");
     constexpr int B_PER_WAVE = (B_INSTS + NWAVE - 1) / NWAVE;
     // separate LDS objects per buffer: the compiler can then tell that a copy into
     // one buffer does not feed reads of the other
     __shared__ __attribute__((aligned(1024))) uint8_t sA0[STAGE_BYTES];
     __shared__ __attribute__((aligned(1024))) uint8_t sA1[STAGE_BYTES];
-    __shared__ __attribute__((aligned(1024))) uint8_t sB0[BROWS * SLOT];
-    __shared__ __attribute__((aligned(1024))) uint8_t sB1[BROWS * SLOT];
+    __shared__ __attribute__((aligned(1024))) uint8_t sB0[BS::bytes(BROWS)];
+    __shared__ __attribute__((aligned(1024))) uint8_t sB1[BS::bytes(BROWS)];
     __shared__ uint32_t s_src[GM_BM];  // byte offset of the A row from the tile's first row
     __shared__ float s_scale[GM_BM];
     __shared__ int s_out[GM_BM];      // output row
@@ -431,12 +477,15 @@ __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
     // (wave + NWAVE q) * 64 + lane = row R, chunk c; the row's offset in its matrix
     uint32_t b_row[B_PER_WAVE];
     int b_c[B_PER_WAVE];
+    bool b_on[B_PER_WAVE];  // false: a spare position (or past the last one), no copy
 #pragma unroll
     for (int q = 0; q < B_PER_WAVE; q++) {
         const int inst = wave + NWAVE * q;
-        const int ch = inst * 64 + lane;
-        const int R = ch / CPR;
-        b_c[q] = ch - R * CPR;
+        const int ch = inst * 64 + lane;  // LDS position
+        const int grp = ch / BS::GROUP, w = ch - grp * BS::GROUP;
+        b_on[q] = ch < B_POS && w < 16 * CPR;
+        const int R = min(16 * grp + w / CPR, BROWS - 1);
+        b_c[q] = w % CPR;
         const int rm = SWIGLU ? R % (BROWS / 2) : R;
         const int colr = min(tl.nt * NCOL + rm, a.n_out - 1);
         b_row[q] = (uint32_t)(colr * rb);
@@ -451,7 +500,7 @@ __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
                 const uint32_t blk = wphase[m] + b_row[q] + so;  // block offset from the aligned base
                 const uint32_t off = kPhased<DT> ? (blk & ~15u) + WB<DT>::chunk_off(b_c[q], ks & 1)
                                                  : blk + WB<DT>::chunk_off(b_c[q], ks & 1);
-                dma16_buf(wres[m], off, buf + inst * 1024);
+                if (!BS::PAD || b_on[q]) dma16_buf(wres[m], off, buf + inst * 1024);
             }
         }
         asm volatile("" ::: "memory");
@@ -522,7 +571,7 @@ __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
         const uint32_t so = stage_block_off<DT>(ks);
 #pragma unroll
         for (int nb = 0; nb < NB; nb++)
-            wb_load<DT>(wb[nb], buf + brow[nb] * SLOT, kh, (rowoff[nb] + so) & 15u, ks & 1);
+            wb_load<DT>(wb[nb], buf + BS::row_off(brow[nb]), kh, (rowoff[nb] + so) & 15u, ks & 1);
     };
 
     const int nks = a.k / KS;  // even

@@ -70,15 +70,15 @@ __device__ __forceinline__ void x24_digits(int v, int &h, int &m, int &l) {
     h = (r - m) >> 8;
 }
 
-// Quantises quarter-group q (values 8q .. 8q+7, given in v) into the staged
-// layout at `base` (and, when gm != NULL and k % 64 == 0, into the group-major
-// copy at gm).  The four quarters of a group must sit in four consecutive
-// lanes (4m .. 4m+3) of one wave, and all four lanes must call this together
-// (cross-lane max and sum); `valid` = false lanes contribute nothing and store
-// nothing.  A group holding Inf or NaN gets a NaN scale, so it poisons the
-// rows that read it, as f32 arithmetic would.
-__device__ __forceinline__ void stage_quarter(const float (&v)[8], int q, bool valid, uint8_t *base, int k,
-                                              uint8_t *gm = nullptr) {
+// The staged form of quarter-group values v (8 consecutive values of one 32-value
+// group): digit words h, m, l (4 values per word), the group scale sg and the
+// group's sum of x24 (s32).  The four quarters of a group must sit in four
+// consecutive lanes (4m .. 4m+3) of one wave, and all four lanes must call this
+// together (cross-lane max and sum); `valid` = false lanes contribute zeros.  A
+// group holding Inf or NaN gets a NaN scale, so it poisons the rows that read it,
+// as f32 arithmetic would.
+__device__ __forceinline__ void quarter_digits(const float (&v)[8], bool valid, uint32_t (&h)[2], uint32_t (&m)[2],
+                                               uint32_t (&l)[2], float &sg, int &s32) {
     float mx = 0.f;
     if (valid) {
 #pragma unroll
@@ -93,7 +93,6 @@ __device__ __forceinline__ void stage_quarter(const float (&v)[8], int q, bool v
     const bool finite = mx < __builtin_inff();
     const bool nz = finite && mx > 0.f;
     const int e = nz ? x24_exponent(mx) : 0;
-    uint32_t h[2], m[2], l[2];
     int s8 = 0;
 #pragma unroll
     for (int w = 0; w < 2; w++) {
@@ -112,9 +111,21 @@ __device__ __forceinline__ void stage_quarter(const float (&v)[8], int q, bool v
         m[w] = mw;
         l[w] = lw;
     }
-    int s32 = s8 + __float_as_int(lane_partner<1>(__int_as_float(s8)));
+    s32 = s8 + __float_as_int(lane_partner<1>(__int_as_float(s8)));
     s32 = s32 + __float_as_int(lane_partner<2>(__int_as_float(s32)));
-    const float sg = !finite ? __builtin_nanf("") : nz ? __builtin_amdgcn_ldexpf(1.0f, e) : 0.f;
+    sg = !finite ? __builtin_nanf("") : nz ? __builtin_amdgcn_ldexpf(1.0f, e) : 0.f;
+}
+
+// Quantises quarter-group q (values 8q .. 8q+7, given in v) into the staged
+// layout at `base` (and, when gm != NULL and k % 64 == 0, into the group-major
+// copy at gm), under quarter_digits' lane rules; `valid` = false lanes store
+// nothing.
+__device__ __forceinline__ void stage_quarter(const float (&v)[8], int q, bool valid, uint8_t *base, int k,
+                                              uint8_t *gm = nullptr) {
+    uint32_t h[2], m[2], l[2];
+    float sg;
+    int s32;
+    quarter_digits(v, valid, h, m, l, sg, s32);
     if (valid) {
         int8_t *xh = reinterpret_cast<int8_t *>(base);
         int8_t *xm = xh + k;
