@@ -106,7 +106,7 @@ mx_status launch_route_select(const float *logits, const float *bias, int t, int
 // probabilities and selection sort keys for t tokens (ws: keys u64 [t, E] |
 // probs f32 [t, E]); also stages the (normalised) rows into `xstage`
 // (mx_stage.h layout) and/or writes them to `x_normed` when non-NULL.  The
-// top-k runs in the selection blocks of launch_decode_gate_up.
+// top-k runs in k_decode_select (launch_decode_select).
 size_t route_fused_ws_bytes(int t, int hidden, int n_expert);
 int route_fused_max_t();
 mx_status launch_route_fused(const float *x, const float *rms_alpha, float rms_eps,
