@@ -550,19 +550,26 @@ __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
             for (int r = 0; r < 16; r++) acc[mb][nb][r] = 0.f;
 
     auto compute = [&](const uint8_t *buf, WB<DT>(&wb)[NB]) {
+        // the A fragments of step s + 1 are read while step s computes
+        half8_t af[2][4];
+#pragma unroll
+        for (int mb = 0; mb < 4; mb++) af[0][mb] = *reinterpret_cast<const half8_t *>(buf + mb * 32 * ROWB + aoff[0]);
 #pragma unroll
         for (int s = 0; s < 8; s++) {
-            const int p = s >> 1, hh = s & 1;
+            const int p = s >> 1, hh = s & 1, cur = s & 1;
+            if (s + 1 < 8) {
+#pragma unroll
+                for (int mb = 0; mb < 4; mb++)
+                    af[cur ^ 1][mb] = *reinterpret_cast<const half8_t *>(buf + mb * 32 * ROWB + aoff[s + 1]);
+            }
             half8_t bf[NB];
 #pragma unroll
             for (int nb = 0; nb < NB; nb++) bf[nb] = wb[nb].step(p, hh);
 #pragma unroll
-            for (int mb = 0; mb < 4; mb++) {
-                const half8_t af = *reinterpret_cast<const half8_t *>(buf + mb * 32 * ROWB + aoff[s]);
+            for (int mb = 0; mb < 4; mb++)
 #pragma unroll
                 for (int nb = 0; nb < NB; nb++)
-                    acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[nb], acc[mb][nb], 0, 0, 0);
-            }
+                    acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[cur][mb], bf[nb], acc[mb][nb], 0, 0, 0);
         }
     };
     // stage ks's B registers from LDS (the block phase of the lane's row for this stage)
