@@ -228,3 +228,32 @@ def test_chain_full_depth_48_layers(dev, orc):
         del L
     assert flips <= 1
     assert_close(host(xd), x, what="48-layer chain")
+
+
+def test_decode_down_compiled_shape_matches_generic(dev):
+    """The C1 shape's down rows (Q6_K, expert_ff 1536, 16-byte-aligned stacks) run
+    a kernel with compile-time geometry; the same weights placed 2 bytes off
+    16-byte alignment (Q6_K needs 2) take the generic slot-per-wave kernel.  Both
+    perform the same operations in the same order, so the outputs must be
+    bit-identical (t = 1 and 3: the slot-per-wave path)."""
+    from maxuna_amd.gguf import ExpertStack
+    from maxuna_amd.moe import MoeBlock, SharedExpert
+
+    spec = CONFIGS["C1"]["spec"]
+    layer = build_layer(spec, seed=1077)
+    blk = layer.block
+
+    def shifted(st):
+        buf = torch.empty(st.nbytes + 16, dtype=torch.uint8, device=st.buffer.device)
+        buf[2:2 + st.nbytes].copy_(st.buffer[st.base_off:st.base_off + st.nbytes])
+        return ExpertStack(buf, st.dtype, st.n_expert, st.n_out, st.k, base_off=2)
+
+    e, sh = blk.experts, blk.shared
+    other = MoeBlock(blk.router, blk.exp_probs_b, e.gate, e.up, shifted(e.down), blk.cfg,
+                     shared=SharedExpert(sh.gate, sh.up, shifted(sh.down)))
+    for t in (1, 3):
+        x = dev_f32(make_x(spec, 300 + t, t))
+        a = host(blk.forward(x))
+        b = host(other.forward(x))
+        _log(f"down compiled vs generic t={t}: max |diff| {np.abs(a - b).max()}")
+        assert np.array_equal(a, b), f"t={t}: compiled-shape down kernel differs from the generic kernel"
