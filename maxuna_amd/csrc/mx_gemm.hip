@@ -549,24 +549,27 @@ __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[mb][nb][r] = 0.f;
 
-    auto compute = [&](const uint8_t *buf, WB<DT>(&wb)[NB]) {
+    // MB: 32-row blocks of the tile that hold rows (a partly filled last m-tile of
+    // an expert skips the MFMAs and A reads of its empty blocks)
+    auto compute = [&](auto mbc, const uint8_t *buf, WB<DT>(&wb)[NB]) {
+        constexpr int MB = decltype(mbc)::value;
         // the A fragments of step s + 1 are read while step s computes
         half8_t af[2][4];
 #pragma unroll
-        for (int mb = 0; mb < 4; mb++) af[0][mb] = *reinterpret_cast<const half8_t *>(buf + mb * 32 * ROWB + aoff[0]);
+        for (int mb = 0; mb < MB; mb++) af[0][mb] = *reinterpret_cast<const half8_t *>(buf + mb * 32 * ROWB + aoff[0]);
 #pragma unroll
         for (int s = 0; s < 8; s++) {
             const int p = s >> 1, hh = s & 1, cur = s & 1;
             if (s + 1 < 8) {
 #pragma unroll
-                for (int mb = 0; mb < 4; mb++)
+                for (int mb = 0; mb < MB; mb++)
                     af[cur ^ 1][mb] = *reinterpret_cast<const half8_t *>(buf + mb * 32 * ROWB + aoff[s + 1]);
             }
             half8_t bf[NB];
 #pragma unroll
             for (int nb = 0; nb < NB; nb++) bf[nb] = wb[nb].step(p, hh);
 #pragma unroll
-            for (int mb = 0; mb < 4; mb++)
+            for (int mb = 0; mb < MB; mb++)
 #pragma unroll
                 for (int nb = 0; nb < NB; nb++)
                     acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[cur][mb], bf[nb], acc[mb][nb], 0, 0, 0);
@@ -595,27 +598,56 @@ __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
     };
-    for (int ks = 0; ks < nks; ks += 2) {
-        issue_a(ks + 1, sA1);
-        issue_b(ks + 1, sB1);
-        load_b(ks, sB0);
+    auto k_loop = [&](auto mbc) {
+        for (int ks = 0; ks < nks; ks += 2) {
+            issue_a(ks + 1, sA1);
+            issue_b(ks + 1, sB1);
+            load_b(ks, sB0);
 #pragma unroll
-        for (int nb = 0; nb < NB; nb++) wb[nb].template prep<0>(kh);
-        compute(sA0, wb);
-        stage_end();
-        {
-            // unconditional, clamped at the last stage (a harmless re-copy into
-            // the buffer nobody reads next): no branch merge in front of the
-            // next waits, so the compiler keeps exact memory counters
-            const int kn = min(ks + 2, nks - 1);
-            issue_a(kn, sA0);
-            issue_b(kn, sB0);
+            for (int nb = 0; nb < NB; nb++) wb[nb].template prep<0>(kh);
+            compute(mbc, sA0, wb);
+            stage_end();
+            {
+                // unconditional, clamped at the last stage (a harmless re-copy into
+                // the buffer nobody reads next): no branch merge in front of the
+                // next waits, so the compiler keeps exact memory counters
+                const int kn = min(ks + 2, nks - 1);
+                issue_a(kn, sA0);
+                issue_b(kn, sB0);
+            }
+            load_b(ks + 1, sB1);
+#pragma unroll
+            for (int nb = 0; nb < NB; nb++) wb[nb].template prep<1>(kh);
+            compute(mbc, sA1, wb);
+            stage_end();
         }
-        load_b(ks + 1, sB1);
+    };
+    // block-uniform: the tile's filled 32-row blocks (the SwiGLU tiles; the plain
+    // tiles keep the single loop, which the compiler schedules better there)
+    if constexpr (SWIGLU) {
+        if (tl.mrows > 64) k_loop(std::integral_constant<int, 4>{});
+        else if (tl.mrows > 32) k_loop(std::integral_constant<int, 2>{});
+        else k_loop(std::integral_constant<int, 1>{});
+    } else {
+        for (int ks = 0; ks < nks; ks += 2) {
+            issue_a(ks + 1, sA1);
+            issue_b(ks + 1, sB1);
+            load_b(ks, sB0);
 #pragma unroll
-        for (int nb = 0; nb < NB; nb++) wb[nb].template prep<1>(kh);
-        compute(sA1, wb);
-        stage_end();
+            for (int nb = 0; nb < NB; nb++) wb[nb].template prep<0>(kh);
+            compute(std::integral_constant<int, 4>{}, sA0, wb);
+            stage_end();
+            {
+                const int kn = min(ks + 2, nks - 1);  // clamped, unconditional (see k_loop)
+                issue_a(kn, sA0);
+                issue_b(kn, sB0);
+            }
+            load_b(ks + 1, sB1);
+#pragma unroll
+            for (int nb = 0; nb < NB; nb++) wb[nb].template prep<1>(kh);
+            compute(std::integral_constant<int, 4>{}, sA1, wb);
+            stage_end();
+        }
     }
     __syncthreads();
 
