@@ -200,6 +200,22 @@ def test_wide_rows(dev, orc):
         oracle_check(orc, layer, x, out, ids, w, f"wide rows t={t}", max_flips=1)
 
 
+def test_laguna_geometry(dev, orc):
+    """The shipped Laguna layer geometry (reference/config.json: hidden 3072,
+    moe_intermediate_size 1024, shared_expert_intermediate_size 1024, 256 experts,
+    top-10) with the GGUF's expert_weights_scale 2.5 and norm on.  ff = 1024 has 32
+    Q4_K groups per gate/up row and 4 Q6_K blocks per down row, so decode takes the
+    generic slot kernels (not the ff = 1536 compile-time forms); t = 6 and 16 are
+    verify blocks and t = 64 the grouped GEMM."""
+    spec = LayerSpec(3072, 1024, 256, 10, GgmlDType.Q4_K, GgmlDType.Q6_K, shared=True, weights_scale=2.5)
+    layer = build_layer(spec, seed=1051)
+    for t in (1, 6, 16, 64):
+        _log(f"laguna geometry t={t}")
+        x = make_x(spec, 61 + t, t)
+        out, ids, w = run_block(layer, x)
+        oracle_check(orc, layer, x, out, ids, w, f"laguna t={t}", max_flips=2)
+
+
 def test_chain_full_depth_48_layers(dev, orc):
     """C4 at its stated depth: 48 C1-shaped layers, x <- x + MoE(RMSNorm(x))
     (model.rs:340-351), each layer built, run and freed in turn on the GPU while
