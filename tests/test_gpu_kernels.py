@@ -188,7 +188,8 @@ def _distinct_ids(rng, t, k, E):
 def test_map0_matches_oracle(dev, orc):
     rng = np.random.default_rng(6)
     # E = 2000 takes the scan fallback of the fill pass (slot table too large for LDS)
-    for t, k, E in [(1, 4, 64), (48, 10, 32), (300, 10, 256), (2048, 10, 256), (100, 4, 2000)]:
+    for t, k, E in [(1, 4, 64), (48, 10, 32), (300, 10, 256), (2048, 10, 256), (8192, 2, 296), (9000, 3, 64),
+                    (70, 8, 300), (50, 20, 64), (100, 4, 2000)]:
         _log(f"map0 t={t} k={k} E={E}")
         ids = _distinct_ids(rng, t, k, E)
         m = ops.prepare_map0(E, dev_u32(ids))
@@ -200,8 +201,13 @@ def test_map0_matches_oracle(dev, orc):
         for e in range(E):
             assert np.array_equal(lst[offs[e]:offs[e + 1]], hids[e, :tpe[e]]), e
         assert m.dup_flag() == 0
-    ids = np.array([[1, 1, 2]], np.uint32)
-    assert ops.prepare_map0(4, dev_u32(ids)).dup_flag() & 1
+    for E in (4, 2000):  # both fill passes flag a repeated id (1) and an out-of-range id (2)
+        ids = np.array([[1, 1, 2]], np.uint32)
+        assert ops.prepare_map0(E, dev_u32(ids)).dup_flag() == 1
+        ids = np.array([[0, 2], [3, E]], np.uint32)
+        m = ops.prepare_map0(E, dev_u32(ids))
+        assert m.dup_flag() == 2
+        assert np.array_equal(host(m.pair_list())[:3], [0, 1, 2])  # the bad pair (token 1, slot 1) is dropped
 
 
 @pytest.mark.parametrize("dt", DTYPES, ids=lambda d: d.name)

@@ -200,6 +200,17 @@ def test_wide_rows(dev, orc):
         oracle_check(orc, layer, x, out, ids, w, f"wide rows t={t}", max_flips=1)
 
 
+def test_prefill_ragged_router_tiles(dev, orc):
+    """Prefill at t = 300 with 96 experts: the MFMA router's 32-token and
+    64-expert tiles and the GEMM's m-tiles are all left partly filled."""
+    spec = LayerSpec(1024, 512, 96, 6, GgmlDType.Q4_K, GgmlDType.Q4_K, shared=False)
+    layer = build_layer(spec, seed=1061)
+    _log("ragged prefill t=300")
+    x = make_x(spec, 71, 300)
+    out, ids, w = run_block(layer, x)
+    oracle_check(orc, layer, x, out, ids, w, "ragged prefill t=300", max_flips=2)
+
+
 def test_laguna_geometry(dev, orc):
     """The shipped Laguna layer geometry (reference/config.json: hidden 3072,
     moe_intermediate_size 1024, shared_expert_intermediate_size 1024, 256 experts,
