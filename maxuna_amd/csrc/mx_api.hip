@@ -340,11 +340,17 @@ Plan plan_for(const mx_moe_layer *L, int64_t t) {
     return p;
 }
 
+// Verify blocks on the decode kernels launch their gate/up pairs in expert order.
+bool pair_order_used(int64_t t, int64_t slots, int64_t n_expert) {
+    return t > 1 && t * slots <= PAIR_ORDER_MAX && n_expert <= 1024;  // the top-k kernels' limit
+}
+
 // Carves the workspace; with base == nullptr it only measures.
 struct Layout {
     uint8_t *route_ws = nullptr;
     float *x_normed = nullptr, *logits = nullptr, *w = nullptr, *act = nullptr;
     uint32_t *ids = nullptr, *zero_ids = nullptr;
+    int32_t *perm = nullptr;  // expert-ordered (token, slot) pairs of a verify block
     uint8_t *xstage = nullptr, *xstage_gm = nullptr;
     float *part = nullptr;
     int32_t *map = nullptr, *map_sh = nullptr;
@@ -382,6 +388,7 @@ Layout carve(const mx_moe_layer *L, int64_t t, const Plan &p, void *base) {
         if (H % 64 == 0) o.xstage_gm = ws.take<uint8_t>(t * xstage_gm_stride((int)H));
         o.act = ws.take<float>(t * slots * FF);
         o.part = ws.take<float>(t * slots * H);
+        if (pair_order_used(t, slots, E)) o.perm = ws.take<int32_t>(t * slots);
         if (p.has_shared && !p.shared_in_decode) {
             o.sh_g = ws.take<float>(t * FF);
             o.sh_u = ws.take<float>(t * FF);
@@ -585,7 +592,7 @@ mx_status moe_forward_impl(const mx_moe_layer *L, const float *x, int64_t t, con
         }
         DecodeGateUpArgs ga{gg.w, gu.w, gg.expert_bytes, gg.row_bytes, shf ? sg.w : nullptr, shf ? su.w : nullptr,
                             sg.row_bytes, (int)E, (int)FF, (int)H, o.xstage, ids, (int)t, (int)K, o.act,
-                            o.xstage_gm};
+                            o.xstage_gm, o.perm};
         DecodeDownArgs da{gd.w, gd.expert_bytes, gd.row_bytes, shf ? sd.w : nullptr, sd.row_bytes, shared_out,
                           (int)E, (int)FF, (int)H, o.act, ids, w, residual, (int)t, (int)K, out, o.part};
         if (p.fused_router) {
@@ -596,6 +603,7 @@ mx_status moe_forward_impl(const mx_moe_layer *L, const float *x, int64_t t, con
                               (int)t, scale, apply, L->weights_norm, ids, w};
             for (int r = 0; r < rep(1); r++) MX_TRY(launch_decode_select((int)K, sel, s));
         }
+        if (o.perm) MX_TRY(launch_pair_order(ids, (int)t, (int)K, (int)E, (int)K + (shf ? 1 : 0), o.perm, s));
         MX_STAGE();
         for (int r = 0; r < (p.fused_router ? rep(2) : 1); r++)
             MX_TRY(launch_decode_gate_up(L->gate.dtype, ga, 0, (int)K + (shf ? 1 : 0), s));

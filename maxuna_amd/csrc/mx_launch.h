@@ -56,7 +56,18 @@ struct DecodeGateUpArgs {
     int t, top_k;
     float *act;                          // [t, slots, ff], slots = top_k + (sh_gate != NULL)
     const uint8_t *xstage_gm;            // NULL, or the group-major copy of xstage (Q4_K / Q5_K reads)
+    // NULL, or the launch order of the (token, slot) pairs, [t * slots] of
+    // (tok * slots + slot) | expert << 16 (the shared slot: n_expert), pairs of
+    // one expert adjacent (launch_pair_order)
+    const int32_t *perm;
 };
+// Verify blocks (t > 1): orders the t * slots (token, slot) pairs by expert (the
+// shared slot as expert n_expert) into perm, so the gate/up blocks of pairs that
+// share an expert run back to back on one XCD and the repeats read its L2.
+// t * slots <= PAIR_ORDER_MAX; the order within an expert is unspecified.
+constexpr int PAIR_ORDER_MAX = 1024;
+mx_status launch_pair_order(const uint32_t *ids, int t, int top_k, int n_expert, int slots, int32_t *perm,
+                            hipStream_t s);
 // Decode top-k (decode router split): block i < n_sel selects token i from
 // keys/probs [n_sel, n_expert] (written by launch_route_fused) into ids/w
 // [n_sel, top_k].

@@ -764,7 +764,15 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
 k_decode_gate_up(DecodeGateUpArgs a, int ni, int slot0, Geo<DT> geo) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int slots = a.top_k + (a.sh_gate ? 1 : 0);
-    const int tile = blockIdx.x, slot = slot0 + blockIdx.y, tok = blockIdx.z;
+    const int tile = blockIdx.x;
+    int slot = slot0 + blockIdx.y, tok = blockIdx.z;
+    int pe = -1;  // the pair's expert, from the expert-ordered launch list
+    if (a.perm) {  // (all slots launched: slot0 == 0)
+        const int v = a.perm[blockIdx.z * slots + blockIdx.y];
+        tok = (v & 0xFFFF) / slots;
+        slot = (v & 0xFFFF) % slots;
+        pe = v >> 16;
+    }
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (scalar)
     const int r0 = tile * (WAVES * RW_GU) + wave * RW_GU;
     if (r0 >= a.ff) return;  // wave-uniform; no block barrier below
@@ -772,7 +780,7 @@ k_decode_gate_up(DecodeGateUpArgs a, int ni, int slot0, Geo<DT> geo) {
     const uint8_t *gw, *uw;
     int64_t rb;
     if (slot < a.top_k) {
-        const uint32_t id = a.ids[tok * a.top_k + slot];
+        const uint32_t id = pe >= 0 ? (uint32_t)pe : a.ids[tok * a.top_k + slot];
         const int e = id < (uint32_t)a.n_expert ? (int)id : a.n_expert - 1;
         gw = a.gate + (int64_t)e * a.gu_expert_bytes;
         uw = a.up + (int64_t)e * a.gu_expert_bytes;
@@ -824,7 +832,14 @@ k_decode_gate_up64(DecodeGateUpArgs a, int slot0, Geo<DT> geo) {
     constexpr int RB = Row64<DT>::RB, CH = Row64<DT>::CH, NI = Row64<DT>::NI;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int slots = a.top_k + (a.sh_gate ? 1 : 0);
-    const int slot = slot0 + blockIdx.y, tok = blockIdx.z;
+    int slot = slot0 + blockIdx.y, tok = blockIdx.z;
+    int pe = -1;  // the pair's expert, from the expert-ordered launch list
+    if (a.perm) {  // (all slots launched: slot0 == 0)
+        const int v = a.perm[blockIdx.z * slots + blockIdx.y];
+        tok = (v & 0xFFFF) / slots;
+        slot = (v & 0xFFFF) % slots;
+        pe = v >> 16;
+    }
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int r0 = (blockIdx.x * WAVES + wave) * R;
@@ -834,7 +849,7 @@ k_decode_gate_up64(DecodeGateUpArgs a, int slot0, Geo<DT> geo) {
     load_xs_gm<DT, 1>(a.xstage_gm + (int64_t)tok * xstage_gm_stride(a.hidden), a.hidden, geo, xs);
     const uint8_t *gw, *uw;
     if (slot < a.top_k) {
-        const uint32_t id = a.ids[tok * a.top_k + slot];
+        const uint32_t id = pe >= 0 ? (uint32_t)pe : a.ids[tok * a.top_k + slot];
         const int e = id < (uint32_t)a.n_expert ? (int)id : a.n_expert - 1;
         gw = a.gate + (int64_t)e * a.gu_expert_bytes;
         uw = a.up + (int64_t)e * a.gu_expert_bytes;
@@ -908,6 +923,58 @@ __global__ void __launch_bounds__(SEL_THREADS) k_decode_select(int top_k, Decode
                    sel.ids + (int64_t)blockIdx.x * top_k, sel.w + (int64_t)blockIdx.x * top_k, sh);
 }
 
+__global__ void __launch_bounds__(PAIR_ORDER_MAX) k_pair_order(const uint32_t *__restrict__ ids, int t, int top_k,
+                                                                int n_expert, int slots,
+                                                                int32_t *__restrict__ perm) {
+    __shared__ int cnt[SEL_MAX_E + 2];
+    __shared__ int s_scan[PAIR_ORDER_MAX];
+    const int tid = threadIdx.x, n = t * slots, ne = n_expert + 1;  // expert n_expert: the shared slot
+    for (int i = tid; i < ne; i += PAIR_ORDER_MAX) cnt[i] = 0;
+    __syncthreads();
+    int e = 0, rank = 0;
+    if (tid < n) {
+        const int tok = tid / slots, slot = tid % slots;
+        if (slot < top_k) {
+            const uint32_t id = ids[tok * top_k + slot];
+            e = id < (uint32_t)n_expert ? (int)id : n_expert - 1;  // as the expert kernels clamp it
+        } else {
+            e = n_expert;
+        }
+        rank = atomicAdd(&cnt[e], 1);
+    }
+    __syncthreads();
+    // exclusive scan of the counts: each thread sums a run of `per` experts
+    const int per = (ne + PAIR_ORDER_MAX - 1) / PAIR_ORDER_MAX;
+    const int e0 = min(tid * per, ne), e1 = min(e0 + per, ne);
+    int sum = 0;
+    for (int i = e0; i < e1; i++) sum += cnt[i];
+    s_scan[tid] = sum;
+    __syncthreads();
+    for (int d = 1; d < PAIR_ORDER_MAX; d <<= 1) {
+        const int v = tid >= d ? s_scan[tid - d] : 0;
+        __syncthreads();
+        s_scan[tid] += v;
+        __syncthreads();
+    }
+    int run = s_scan[tid] - sum;
+    for (int i = e0; i < e1; i++) {
+        const int c = cnt[i];
+        cnt[i] = run;
+        run += c;
+    }
+    __syncthreads();
+    if (tid < n) perm[cnt[e] + rank] = tid | (e << 16);  // the expert rides along: no ids load downstream
+}
+
+mx_status launch_pair_order(const uint32_t *ids, int t, int top_k, int n_expert, int slots, int32_t *perm,
+                            hipStream_t s) {
+    if ((int64_t)t * slots > PAIR_ORDER_MAX || n_expert > SEL_MAX_E)
+        return fail(MX_ERR_SHAPE, "pair order: t * slots <= %d and n_expert <= %d", PAIR_ORDER_MAX, SEL_MAX_E);
+    hipLaunchKernelGGL(k_pair_order, dim3(1), dim3(PAIR_ORDER_MAX), 0, s, ids, t, top_k, n_expert, slots, perm);
+    MX_LAUNCH("k_pair_order");
+    return MX_OK;
+}
+
 template <int DT, int NG>
 static mx_status launch_gu_ng(const DecodeGateUpArgs &a, int slot0, int nslot, hipStream_t s) {
     const unsigned tiles = (unsigned)((a.ff + WAVES * RW_GU - 1) / (WAVES * RW_GU));
@@ -973,6 +1040,8 @@ mx_status launch_decode_gate_up(int dtype, const DecodeGateUpArgs &a, int slot0,
     if (a.hidden % 32) return fail(MX_ERR_BLOCK, "decode gate/up: hidden must be a multiple of 32");
     if (a.sh_gate && a.sh_row_bytes != a.gu_row_bytes)
         return fail(MX_ERR_SHAPE, "decode gate/up: shared expert rows must match the routed rows");
+    if (a.perm && (slot0 != 0 || nslot != a.top_k + (a.sh_gate ? 1 : 0)))
+        return fail(MX_ERR_SHAPE, "decode gate/up: an expert-ordered launch covers every slot");
     switch (dtype) {
     case kQ4_K: MX_TRY(launch_gu_dt<kQ4_K>(a, slot0, nslot, s)); break;
     case kQ5_K: MX_TRY(launch_gu_dt<kQ5_K>(a, slot0, nslot, s)); break;
