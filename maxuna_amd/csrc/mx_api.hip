@@ -594,7 +594,8 @@ mx_status moe_forward_impl(const mx_moe_layer *L, const float *x, int64_t t, con
                             sg.row_bytes, (int)E, (int)FF, (int)H, o.xstage, ids, (int)t, (int)K, o.act,
                             o.xstage_gm, o.perm};
         DecodeDownArgs da{gd.w, gd.expert_bytes, gd.row_bytes, shf ? sd.w : nullptr, sd.row_bytes, shared_out,
-                          (int)E, (int)FF, (int)H, o.act, ids, w, residual, (int)t, (int)K, out, o.part};
+                          (int)E, (int)FF, (int)H, o.act, ids, w, residual, (int)t, (int)K, out, o.part,
+                          o.perm};
         if (p.fused_router) {
             // the top-k of every token (its own launch), then the expert slots, which read it
             const uint8_t *keys = static_cast<const uint8_t *>(o.route_ws);

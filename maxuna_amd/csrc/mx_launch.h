@@ -103,6 +103,7 @@ struct DecodeDownArgs {
     int t, top_k;
     float *out;                          // [t, hidden]
     float *part;                         // [t, top_k + (sh_down != NULL), hidden] scratch
+    const int32_t *perm;                 // NULL, or the expert-ordered pair list (DecodeGateUpArgs::perm)
 };
 mx_status launch_decode_down(int dtype, const DecodeDownArgs &a, hipStream_t s);
 

@@ -1065,7 +1065,14 @@ template <int DT, int NG>
 __global__ void __launch_bounds__(64 * WAVES_DN) __attribute__((amdgpu_waves_per_eu(MX_DN_WPE))) k_decode_down(DecodeDownArgs a, int ni, Geo<DT> geo) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int slots = a.top_k + (a.sh_down ? 1 : 0);
-    const int slot = blockIdx.y, tok = blockIdx.z, tile = blockIdx.x;  // grid (row tiles, slots, t)
+    const int tile = blockIdx.x;  // grid (row tiles, slots, t)
+    int slot = blockIdx.y, tok = blockIdx.z, pe = -1;
+    if (a.perm) {  // expert-ordered pairs: an expert's repeats run back to back (its rows in L2)
+        const int v = a.perm[blockIdx.z * slots + blockIdx.y];
+        tok = (v & 0xFFFF) / slots;
+        slot = (v & 0xFFFF) % slots;
+        pe = v >> 16;
+    }
     constexpr int ROWS_PER_WG = WAVES_DN * RW_DN;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (scalar)
     const int r0 = tile * ROWS_PER_WG + wave * RW_DN;
@@ -1080,7 +1087,7 @@ __global__ void __launch_bounds__(64 * WAVES_DN) __attribute__((amdgpu_waves_per
     const uint8_t *wp;
     int64_t rb;
     if (slot < a.top_k) {
-        const uint32_t id = a.ids[tok * a.top_k + slot];
+        const uint32_t id = pe >= 0 ? (uint32_t)pe : a.ids[tok * a.top_k + slot];
         const int e = id < (uint32_t)a.n_expert ? (int)id : a.n_expert - 1;
         wp = a.down + (int64_t)e * a.d_expert_bytes;
         rb = a.d_row_bytes;
