@@ -255,8 +255,9 @@ mx_status mx_moe_forward_noalloc(const mx_moe_layer *layer, const float *x, int6
  * stage on `stream`, waits for the last one and returns the stage durations
  * in milliseconds.  Decode (t < mm_min_seq): router (fused router: logits,
  * sort keys and activation staging; else logits + top-k), top-k (fused router:
- * k_decode_select; empty otherwise), routed + shared gate/up + SwiGLU, down +
- * combine.
+ * k_decode_select, and for a verify block the expert-ordered pair list; empty
+ * otherwise, and at t = 1 when the 64-group gate/up kernel runs the top-k in its
+ * own blocks), routed + shared gate/up + SwiGLU, down + combine.
  * Grouped path: route, map0, x -> f16, then per bucket map gate/up GEMM +
  * SwiGLU, act -> f16, down GEMM (one map when the shared expert has the
  * routed quant types, else a second map for it), then combine.  For profiling
@@ -268,7 +269,8 @@ mx_status mx_moe_forward_profiled(const mx_moe_layer *layer, const float *x, int
                                   int32_t *n_stages);
 
 /* Same as mx_moe_forward, with the kernels of decode stage `stage` (0 router
- * logits + staging, 1 top-k, 2 routed + shared gate/up, 3 down + combine; the
+ * logits + staging, 1 top-k (nothing at t = 1 when gate/up selects in its own
+ * blocks), 2 routed + shared gate/up, 3 down + combine; the
  * fused-router decode path, t < mm_min_seq <= 32) launched `times` times (0..16).  times = 0 skips
  * the stage: the later stages then read what the workspace holds from the
  * previous forward of the same layer (valid inputs, stale results) -- a graph

@@ -287,7 +287,11 @@ mx_status mx_route_from_logits(const float *logits, const float *bias, int64_t t
 // ---- whole MoE block --------------------------------------------------------------------
 namespace {
 
-constexpr int64_t kDefaultMmMinSeq = 32;  // ops/mod.rs:31 MM_ID_MIN_SEQ
+constexpr int64_t kDefaultMmMinSeq = 32;
+#ifndef MX_FUSE_SELECT
+#define MX_FUSE_SELECT 1
+#endif
+constexpr bool kFuseSelect = MX_FUSE_SELECT != 0;  // ops/mod.rs:31 MM_ID_MIN_SEQ
 
 struct Ws {
     uint8_t *base;
@@ -597,12 +601,23 @@ mx_status moe_forward_impl(const mx_moe_layer *L, const float *x, int64_t t, con
                           (int)E, (int)FF, (int)H, o.act, ids, w, residual, (int)t, (int)K, out, o.part,
                           o.perm};
         if (p.fused_router) {
-            // the top-k of every token (its own launch), then the expert slots, which read it
             const uint8_t *keys = static_cast<const uint8_t *>(o.route_ws);
             DecodeSelArgs sel{reinterpret_cast<const uint64_t *>(keys),
                               reinterpret_cast<const float *>(keys + (size_t)t * E * sizeof(uint64_t)), (int)E,
                               (int)t, scale, apply, L->weights_norm, ids, w};
-            for (int r = 0; r < rep(1); r++) MX_TRY(launch_decode_select((int)K, sel, s));
+            // one token: the gate/up blocks run the top-k themselves where they can
+            // (no launch boundary between router and experts); else its own launch
+            ga.sel_keys = sel.keys;
+            ga.sel_probs = sel.probs;
+            ga.sel_scale = scale;
+            ga.sel_apply = apply;
+            ga.sel_norm = L->weights_norm;
+            ga.sel_ids = ids;
+            ga.sel_w = w;
+            if (!(kFuseSelect && decode_gate_up_selects(L->gate.dtype, ga))) {
+                ga.sel_keys = nullptr;
+                for (int r = 0; r < rep(1); r++) MX_TRY(launch_decode_select((int)K, sel, s));
+            }
         }
         if (o.perm) MX_TRY(launch_pair_order(ids, (int)t, (int)K, (int)E, (int)K + (shf ? 1 : 0), o.perm, s));
         MX_STAGE();

@@ -60,7 +60,19 @@ struct DecodeGateUpArgs {
     // (tok * slots + slot) | expert << 16 (the shared slot: n_expert), pairs of
     // one expert adjacent (launch_pair_order)
     const int32_t *perm;
+    // t == 1 with the 64-group kernel: the top-k runs in every routed block from
+    // the router's keys/probs [n_expert] (NULL: ids come from k_decode_select),
+    // and block (0, 0) writes ids/w for the down kernel and the caller
+    const uint64_t *sel_keys;
+    const float *sel_probs;
+    float sel_scale;
+    int sel_apply, sel_norm;
+    uint32_t *sel_ids;
+    float *sel_w;
 };
+// Whether launch_decode_gate_up can run the top-k itself for these arguments
+// (t == 1, the 64-group kernel, n_expert <= 256).
+bool decode_gate_up_selects(int dtype, const DecodeGateUpArgs &a);
 // Verify blocks (t > 1): orders the t * slots (token, slot) pairs by expert (the
 // shared slot as expert n_expert) into perm, so the gate/up blocks of pairs that
 // share an expert run back to back on one XCD and the repeats read its L2.

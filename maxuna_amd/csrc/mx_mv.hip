@@ -826,6 +826,8 @@ template <int DT> struct Row64 {
     static constexpr int RB = 16 * (DT == kQ4_K ? 144 : 176);  // row bytes (16 super-blocks)
     static constexpr int CH = RB / 16, NI = (CH + 63) / 64;     // 16-byte chunks, copy instructions
 };
+constexpr int GU_SEL_E = 256;  // experts of the in-block top-k
+static_assert(64 * WAVES == SEL_THREADS, "the in-block top-k needs SEL_THREADS threads");
 template <int DT, int R>
 __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(MX_GU_WPE)))
 k_decode_gate_up64(DecodeGateUpArgs a, int slot0, Geo<DT> geo) {
@@ -843,10 +845,17 @@ k_decode_gate_up64(DecodeGateUpArgs a, int slot0, Geo<DT> geo) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int r0 = (blockIdx.x * WAVES + wave) * R;
+    typename Q<DT>::X xs[1];
+    if (r0 < a.ff) load_xs_gm<DT, 1>(a.xstage_gm + (int64_t)tok * xstage_gm_stride(a.hidden), a.hidden, geo, xs);
+    if (a.sel_keys && slot < a.top_k) {  // block-uniform: the whole block selects (t == 1)
+        auto &sh = *reinterpret_cast<SelSharedT<GU_SEL_E> *>(lds + WAVES * 2 * RB);
+        const bool writer = blockIdx.x == 0 && blockIdx.y == 0;
+        topk_from_keys<GU_SEL_E>(a.sel_keys, a.sel_probs, a.n_expert, a.top_k, a.sel_scale, a.sel_apply,
+                                 a.sel_norm, writer ? a.sel_ids : nullptr, a.sel_w, sh);
+        pe = sh.pick[slot];
+    }
     if (r0 >= a.ff) return;  // wave-uniform; no block barrier below
     const int n = min(R, a.ff - r0);
-    typename Q<DT>::X xs[1];
-    load_xs_gm<DT, 1>(a.xstage_gm + (int64_t)tok * xstage_gm_stride(a.hidden), a.hidden, geo, xs);
     const uint8_t *gw, *uw;
     if (slot < a.top_k) {
         const uint32_t id = pe >= 0 ? (uint32_t)pe : a.ids[tok * a.top_k + slot];
@@ -1011,7 +1020,7 @@ static mx_status launch_gu_dt(const DecodeGateUpArgs &a, int slot0, int nslot, h
         if (gu64_ok<DT>(a)) {
             const unsigned tiles = (unsigned)((a.ff + WAVES * GU64_R - 1) / (WAVES * GU64_R));
             const dim3 grid(tiles, (unsigned)nslot, (unsigned)a.t);
-            const size_t lds = (size_t)WAVES * 2 * Row64<DT>::RB;
+            const size_t lds = (size_t)WAVES * 2 * Row64<DT>::RB + (a.sel_keys ? sizeof(SelSharedT<GU_SEL_E>) : 0);
             hipLaunchKernelGGL((k_decode_gate_up64<DT, (GU64_R > 0 ? GU64_R : 1)>), grid, dim3(64 * WAVES), lds, s, a, slot0,
                                Geo<DT>(a.hidden));
             return MX_OK;
@@ -1034,6 +1043,11 @@ mx_status launch_decode_select(int top_k, const DecodeSelArgs &sel, hipStream_t 
     return MX_OK;
 }
 
+bool decode_gate_up_selects(int dtype, const DecodeGateUpArgs &a) {
+    return dtype == kQ4_K && gu64_ok<kQ4_K>(a) && a.t == 1 && a.n_expert <= GU_SEL_E && a.top_k <= SEL_MAX_K &&
+           !a.perm;
+}
+
 mx_status launch_decode_gate_up(int dtype, const DecodeGateUpArgs &a, int slot0, int nslot, hipStream_t s) {
     if (a.t == 0 || nslot == 0) return MX_OK;
     if ((int64_t)a.t > 65535 || nslot > 65535) return fail(MX_ERR_OVERFLOW, "decode gate/up: grid too large");
@@ -1042,6 +1056,8 @@ mx_status launch_decode_gate_up(int dtype, const DecodeGateUpArgs &a, int slot0,
         return fail(MX_ERR_SHAPE, "decode gate/up: shared expert rows must match the routed rows");
     if (a.perm && (slot0 != 0 || nslot != a.top_k + (a.sh_gate ? 1 : 0)))
         return fail(MX_ERR_SHAPE, "decode gate/up: an expert-ordered launch covers every slot");
+    if (a.sel_keys && (!decode_gate_up_selects(dtype, a) || slot0 != 0))
+        return fail(MX_ERR_SHAPE, "decode gate/up: the in-block top-k needs t == 1 and the 64-group kernel");
     switch (dtype) {
     case kQ4_K: MX_TRY(launch_gu_dt<kQ4_K>(a, slot0, nslot, s)); break;
     case kQ5_K: MX_TRY(launch_gu_dt<kQ5_K>(a, slot0, nslot, s)); break;

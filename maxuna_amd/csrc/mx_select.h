@@ -42,29 +42,37 @@ template <int O> __device__ __forceinline__ uint64_t lane_partner_u64(uint64_t v
     return ((uint64_t)hi << 32) | lo;
 }
 
-struct SelShared {
-    uint64_t gmax[SEL_MAX_E / 8];
-    uint64_t ckey[SEL_MAX_E];
-    float cprob[SEL_MAX_E];
+// LDS of one top-k for up to MAXE experts.
+template <int MAXE = SEL_MAX_E> struct SelSharedT {
+    static_assert(MAXE % SEL_THREADS == 0 && MAXE <= SEL_MAX_E, "MAXE: a multiple of SEL_THREADS");
+    uint64_t gmax[MAXE / 8];
+    uint64_t ckey[MAXE];
+    float cprob[MAXE];
     float prob[SEL_MAX_K];
     int pick[SEL_MAX_K];
     uint64_t thresh;
     int ncand;
     float sum;
 };
+using SelShared = SelSharedT<>;
 
 // key[j], prob[j]: expert e = threadIdx.x + SEL_THREADS * j (key 0 for e >=
 // n_expert).  All SEL_THREADS threads of the block must call; blockDim.x must
-// be SEL_THREADS.  Writes ids_out[0..top_k), w_out[0..top_k).
-__device__ __forceinline__ void topk_select(const uint64_t (&key)[SEL_PER], const float (&prob)[SEL_PER],
-                                            int n_expert, int top_k, float scale, int apply_scale, int norm,
-                                            uint32_t *__restrict__ ids_out, float *__restrict__ w_out,
-                                            SelShared &sh) {
+// be SEL_THREADS.  Writes ids_out[0..top_k), w_out[0..top_k) (ids_out NULL: neither;
+// the picks stay in sh.pick).
+// MAXE: the largest n_expert the caller allows (the key arrays hold MAXE /
+// SEL_THREADS entries per thread).
+template <int MAXE = SEL_MAX_E>
+__device__ __forceinline__ void topk_select(const uint64_t (&key)[MAXE / SEL_THREADS],
+                                            const float (&prob)[MAXE / SEL_THREADS], int n_expert, int top_k,
+                                            float scale, int apply_scale, int norm, uint32_t *__restrict__ ids_out,
+                                            float *__restrict__ w_out, SelSharedT<MAXE> &sh) {
+    constexpr int PER = MAXE / SEL_THREADS;
     const int tid = threadIdx.x;
     const int G = (n_expert + 7) >> 3;
     // 1. group maxima (8 consecutive experts = 8 consecutive lanes)
 #pragma unroll
-    for (int j = 0; j < SEL_PER; j++) {
+    for (int j = 0; j < PER; j++) {
         if (j * SEL_THREADS < n_expert) {  // block-uniform
             // partners lane ^ 1, lane ^ 2, then the mirror lane of the 8: the
             // maximum of all 8 lanes reaches every lane of the group
@@ -97,7 +105,7 @@ __device__ __forceinline__ void topk_select(const uint64_t (&key)[SEL_PER], cons
     // 3. candidates, ranked among themselves
     const uint64_t T = sh.thresh;
 #pragma unroll
-    for (int j = 0; j < SEL_PER; j++) {
+    for (int j = 0; j < PER; j++) {
         const int e = tid + SEL_THREADS * j;
         if (e < n_expert && key[j] >= T) {
             const int c = atomicAdd(&sh.ncand, 1);
@@ -123,7 +131,7 @@ __device__ __forceinline__ void topk_select(const uint64_t (&key)[SEL_PER], cons
         sh.sum = sum < 6.103515625e-5f ? 6.103515625e-5f : sum;
     }
     __syncthreads();
-    if (tid < top_k) {
+    if (tid < top_k && ids_out) {  // (NULL: the caller reads sh.pick)
         float wk = sh.prob[tid];
         if (norm) wk = wk / sh.sum;
         if (apply_scale) wk = wk * scale;
@@ -135,19 +143,21 @@ __device__ __forceinline__ void topk_select(const uint64_t (&key)[SEL_PER], cons
 
 // Top-k from keys and probabilities in global memory (written by an earlier
 // kernel on the stream).
+template <int MAXE = SEL_MAX_E>
 __device__ __forceinline__ void topk_from_keys(const uint64_t *__restrict__ keys, const float *__restrict__ probs,
                                                int n_expert, int top_k, float scale, int apply_scale, int norm,
                                                uint32_t *__restrict__ ids_out, float *__restrict__ w_out,
-                                               SelShared &sh) {
-    uint64_t key[SEL_PER];
-    float prob[SEL_PER];
+                                               SelSharedT<MAXE> &sh) {
+    constexpr int PER = MAXE / SEL_THREADS;
+    uint64_t key[PER];
+    float prob[PER];
 #pragma unroll
-    for (int j = 0; j < SEL_PER; j++) {
+    for (int j = 0; j < PER; j++) {
         const int e = threadIdx.x + SEL_THREADS * j;
         key[j] = e < n_expert ? keys[e] : 0;
         prob[j] = e < n_expert ? probs[e] : 0.f;
     }
-    topk_select(key, prob, n_expert, top_k, scale, apply_scale, norm, ids_out, w_out, sh);
+    topk_select<MAXE>(key, prob, n_expert, top_k, scale, apply_scale, norm, ids_out, w_out, sh);
 }
 
 }  // namespace mx

@@ -200,6 +200,19 @@ def test_wide_rows(dev, orc):
         oracle_check(orc, layer, x, out, ids, w, f"wide rows t={t}", max_flips=1)
 
 
+def test_decode_in_block_topk_odd_expert_count(dev, orc):
+    """t = 1 with 4096-wide Q4_K gate/up rows: the gate/up blocks run the top-k
+    themselves (no k_decode_select launch) and one of them writes ids and weights.
+    100 experts leave a partial group of 8 in the pruned selection; scale 2.5."""
+    spec = LayerSpec(4096, 512, 100, 8, GgmlDType.Q4_K, GgmlDType.Q6_K, shared=True, weights_scale=2.5)
+    layer = build_layer(spec, seed=1071)
+    for seed in range(3):
+        _log(f"in-block top-k seed={seed}")
+        x = make_x(spec, 81 + seed, 1)
+        out, ids, w = run_block(layer, x)
+        oracle_check(orc, layer, x, out, ids, w, f"in-block top-k seed={seed}", max_flips=0)
+
+
 def test_prefill_ragged_router_tiles(dev, orc):
     """Prefill at t = 300 with 96 experts: the MFMA router's 32-token and
     64-expert tiles and the GEMM's m-tiles are all left partly filled."""
