@@ -358,7 +358,6 @@ struct Layout {
     uint8_t *xstage = nullptr, *xstage_gm = nullptr;
     float *part = nullptr;
     int32_t *map = nullptr, *map_sh = nullptr;
-    uint32_t *ids_aug = nullptr;
     _Float16 *x16 = nullptr, *act16 = nullptr;
     float *x16s = nullptr, *act16s = nullptr, *down = nullptr, *act_u = nullptr;
     float *sh_g = nullptr, *sh_u = nullptr, *sh_out = nullptr;
@@ -405,7 +404,6 @@ Layout carve(const mx_moe_layer *L, int64_t t, const Plan &p, void *base) {
         const int64_t KK = K + S;
         const int64_t EM = E + (p.shared_in_decode ? 1 : 0);
         const int64_t KM = K + (p.shared_in_decode ? 1 : 0);
-        if (p.has_shared) o.ids_aug = ws.take<uint32_t>(t * KK);
         o.map = ws.take<int32_t>(map0_bytes((int)EM, (int)t, (int)KM) / 4);
         if (p.has_shared && !p.shared_in_decode) {
             o.map_sh = ws.take<int32_t>(map0_bytes(1, (int)t, 1) / 4);
@@ -637,8 +635,7 @@ mx_status moe_forward_impl(const mx_moe_layer *L, const float *x, int64_t t, con
     const bool one_map = p.shared_in_decode;  // shared joins the routed map as expert E
     const int EM = (int)E + (one_map ? 1 : 0), KM = one_map ? KK : (int)K;
     if (one_map) {
-        MX_TRY(launch_ids_with_shared(ids, (int)t, (int)K, (int)E, o.ids_aug, s));
-        MX_TRY(launch_map0(o.ids_aug, (int)t, KM, EM, o.map, s, GM_BM));
+        MX_TRY(launch_map0(ids, (int)t, KM, EM, o.map, s, GM_BM, (int)K));  // slot K: expert E
     } else {
         MX_TRY(launch_map0(ids, (int)t, (int)K, (int)E, o.map, s, GM_BM));
         if (p.has_shared) {

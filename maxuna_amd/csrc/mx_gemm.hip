@@ -735,16 +735,6 @@ __global__ void __launch_bounds__(256) k_to_f16_rows(const float *__restrict__ x
     if (threadIdx.x == 0) scale[row] = ldexpf(1.0f, ex);
 }
 
-__global__ void k_ids_with_shared(const uint32_t *__restrict__ ids, int t, int top_k, int n_expert,
-                                  uint32_t *__restrict__ out) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const int kk = top_k + 1;
-    if (i >= (int64_t)t * kk) return;
-    const int64_t tok = i / kk;
-    const int s = (int)(i % kk);
-    out[i] = s < top_k ? ids[tok * top_k + s] : (uint32_t)n_expert;
-}
-
 // out = residual + (sum_s w_s down_s) + shared   (moe.rs:78; combine.metal:16-40 order)
 // KK > 0: compiled for kk = top_k + has_shared == KK, so every slot's load is
 // issued before the first one is used; KK == 0: any kk, one slot at a time.
@@ -844,16 +834,6 @@ mx_status launch_to_f16_rows(const float *x, int64_t rows, int k, const int32_t 
     else if (k <= 1024 * 4) hipLaunchKernelGGL(k_to_f16_rows<4>, grid, dim3(256), 0, s, x, k, count, y, scale);
     else hipLaunchKernelGGL(k_to_f16_rows<0>, grid, dim3(256), 0, s, x, k, count, y, scale);
     MX_LAUNCH("k_to_f16_rows");
-    return MX_OK;
-}
-
-mx_status launch_ids_with_shared(const uint32_t *ids, int t, int top_k, int n_expert, uint32_t *ids_aug,
-                                 hipStream_t s) {
-    const int64_t n = (int64_t)t * (top_k + 1);
-    if (n == 0) return MX_OK;
-    hipLaunchKernelGGL(k_ids_with_shared, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, ids, t, top_k,
-                       n_expert, ids_aug);
-    MX_LAUNCH("k_ids_with_shared");
     return MX_OK;
 }
 

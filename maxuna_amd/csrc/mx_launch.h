@@ -182,8 +182,10 @@ struct MapLayout {
     }
 };
 size_t map0_bytes(int n_expert, int t, int top_k);
+// routed_k (0: top_k): ids per token in `ids`; slots routed_k .. top_k - 1 of
+// every token go to expert n_expert - 1 (a shared expert joined to the map).
 mx_status launch_map0(const uint32_t *ids, int t, int top_k, int n_expert, int32_t *scratch,
-                      hipStream_t s, int bm = MM_BM);
+                      hipStream_t s, int bm = MM_BM, int routed_k = 0);
 struct MmArgs {
     const uint8_t *w;
     int64_t expert_bytes, row_bytes;
@@ -223,9 +225,6 @@ mx_status launch_gemm(int dtype, bool swiglu, const GemmArgs &a, hipStream_t s);
 // rows at or beyond *count (when count != NULL) are skipped
 mx_status launch_to_f16_rows(const float *x, int64_t rows, int k, const int32_t *count, _Float16 *y,
                              float *scale, hipStream_t s);
-// ids_aug[t, top_k + 1]: ids with a last slot = n_expert (the shared expert)
-mx_status launch_ids_with_shared(const uint32_t *ids, int t, int top_k, int n_expert, uint32_t *ids_aug,
-                                 hipStream_t s);
 // out[t, n] = residual + (sum_s w[t, s] * down[t * kk + s] + shared), kk = top_k + has_shared,
 // shared = down[t * kk + top_k] (has_shared), shared_sep[t] (shared_sep != NULL) or 0; n % 4 == 0
 mx_status launch_combine_prefill(const float *down, const float *w, const float *residual, int t, int top_k,

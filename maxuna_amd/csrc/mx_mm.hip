@@ -30,10 +30,16 @@ size_t map0_bytes(int n_expert, int t, int top_k) {
 constexpr int BK_FLAG_SHIFT = 28;
 constexpr int32_t BK_COUNT_MASK = (1 << BK_FLAG_SHIFT) - 1;
 
-// Copies the chunk's ids into LDS (the duplicate checks then read LDS).
+// Copies the chunk's ids into LDS (the duplicate checks then read LDS).  `ids`
+// holds routed_k ids per token; a map of top_k > routed_k slots gives every
+// token slots routed_k .. top_k - 1 with expert n_expert - 1 (the shared expert
+// joined to the routed map as its last expert).
 __device__ __forceinline__ void stage_chunk_ids(const uint32_t *__restrict__ ids, int tok0, int n, int top_k,
-                                                uint32_t *s_ids) {
-    for (int i = threadIdx.x; i < n; i += blockDim.x) s_ids[i] = ids[(int64_t)tok0 * top_k + i];
+                                                int routed_k, int n_expert, uint32_t *s_ids) {
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const int tt = i / top_k, sl = i % top_k;
+        s_ids[i] = sl < routed_k ? ids[(int64_t)(tok0 + tt) * routed_k + sl] : (uint32_t)(n_expert - 1);
+    }
 }
 // true when slot `slot` of row `row` is the first slot of its token with this id
 __device__ __forceinline__ bool first_of_token(const uint32_t *row, int slot, uint32_t id) {
@@ -44,7 +50,7 @@ __device__ __forceinline__ bool first_of_token(const uint32_t *row, int slot, ui
 
 // chunk histogram: cnt[c][e] = pairs of chunk c routed to e, plus the chunk's flags.
 __global__ void __launch_bounds__(256) k_bucket_count(const uint32_t *__restrict__ ids, int t,
-                                                      int top_k, int n_expert,
+                                                      int top_k, int routed_k, int n_expert,
                                                       int32_t *__restrict__ map) {
     extern __shared__ int32_t s_hist[];  // [n_expert] counts | [BK_CHUNK * top_k] ids
     __shared__ int s_flag;
@@ -55,7 +61,7 @@ __global__ void __launch_bounds__(256) k_bucket_count(const uint32_t *__restrict
     const int ntok = min(BK_CHUNK, t - tok0);
     for (int e = tid; e < n_expert; e += 256) s_hist[e] = 0;
     if (tid == 0) s_flag = 0;
-    stage_chunk_ids(ids, tok0, ntok * top_k, top_k, s_ids);
+    stage_chunk_ids(ids, tok0, ntok * top_k, top_k, routed_k, n_expert, s_ids);
     __syncthreads();
     int flag = 0;
     for (int i = tid; i < ntok * top_k; i += 256) {
@@ -133,52 +139,125 @@ __global__ void __launch_bounds__(1024) k_bucket_scan(int t, int top_k, int n_ex
     }
 }
 
-// ordered fill: for each chunk, each expert-thread walks the chunk's tokens in order.
+// ordered fill with its own scan: for each chunk, each expert-thread walks the
+// chunk's tokens in order.  Every block reads all chunk counts of its experts
+// (a few KB from L2) and forms the offsets itself -- the exclusive prefix over
+// chunks within each expert and over experts -- so no scan launch sits between
+// the count and fill passes; block 0 also writes the header (counts, offsets,
+// tile list, flags), as k_bucket_scan does.
+// s_slot[e * BK_ROW + tt]: the first slot of token tt that picked expert e (0xFF:
+// none).  Each expert's thread reads its row as four 16-byte words and walks the
+// chunk's tokens from registers.
+constexpr int BK_ROW = 80;   // table row bytes: BK_CHUNK slots, padded to spread the rows over the banks
+constexpr int BK_EPT = 4;    // experts per thread (n_expert <= 1024)
+static_assert(BK_CHUNK == 64 && BK_ROW >= BK_CHUNK && BK_ROW % 16 == 0, "table row: four 16-byte words");
 __global__ void __launch_bounds__(256) k_bucket_fill(const uint32_t *__restrict__ ids, int t,
-                                                     int top_k, int n_expert,
+                                                     int top_k, int routed_k, int n_expert, int bm,
                                                      int32_t *__restrict__ map) {
-    // s_slot[tt * n_expert + e]: the first slot of token tt that picked expert e
-    // (0xFF: none), so each expert's thread walks the chunk's tokens in order
-    // with one LDS byte per token; the chunk's ids follow the table
-    extern __shared__ uint8_t s_slot[];
-    const int table = BK_CHUNK * ((n_expert + 3) & ~3);
+    extern __shared__ __attribute__((aligned(16))) uint8_t s_slot[];
+    __shared__ int32_t s_a[256], s_b[256];
+    __shared__ int s_flag;
+    const int table = n_expert * BK_ROW;
     uint32_t *s_ids = reinterpret_cast<uint32_t *>(s_slot + table);
     const MapLayout L(n_expert, t, top_k);
     const int c = blockIdx.x, tid = threadIdx.x;
     const int tok0 = c * BK_CHUNK;
     const int ntok = min(BK_CHUNK, t - tok0);
-    uint32_t *w32 = reinterpret_cast<uint32_t *>(s_slot);
-    for (int i = tid; i < table / 4; i += 256) w32[i] = 0xFFFFFFFFu;
-    stage_chunk_ids(ids, tok0, ntok * top_k, top_k, s_ids);
+    uint4 *w128 = reinterpret_cast<uint4 *>(s_slot);
+    for (int i = tid; i < table / 16; i += 256) w128[i] = make_uint4(~0u, ~0u, ~0u, ~0u);
+    if (tid == 0) s_flag = 0;
+    stage_chunk_ids(ids, tok0, ntok * top_k, top_k, routed_k, n_expert, s_ids);
+    // this thread's experts [e0, e1): totals and the prefix before chunk c
+    const int per = (n_expert + 255) / 256;
+    const int e0 = min(tid * per, n_expert), e1 = min(e0 + per, n_expert);
+    int tot[BK_EPT], before[BK_EPT];
+    int sum_pairs = 0, sum_tiles = 0, flag = 0;
+#pragma unroll
+    for (int j = 0; j < BK_EPT; j++) {
+        tot[j] = 0;
+        before[j] = 0;
+        const int e = e0 + j;
+        if (e < e1) {
+            const int32_t *p = map + L.chunk + e;
+            constexpr int CB = 16;  // chunk counts loaded together (independent loads in flight)
+            int run = 0;
+            for (int64_t q0 = 0; q0 < L.nchunks; q0 += CB) {
+                int32_t v[CB];
+#pragma unroll
+                for (int i = 0; i < CB; i++) v[i] = q0 + i < L.nchunks ? p[(q0 + i) * n_expert] : 0;
+#pragma unroll
+                for (int i = 0; i < CB; i++) {
+                    if (q0 + i == c) before[j] = run;
+                    flag |= v[i] >> BK_FLAG_SHIFT;
+                    run += v[i] & BK_COUNT_MASK;
+                }
+            }
+            tot[j] = run;
+            sum_pairs += run;
+            sum_tiles += (run + bm - 1) / bm;
+        }
+    }
+    if (flag) atomicOr(&s_flag, flag);
+    s_a[tid] = sum_pairs;
+    s_b[tid] = sum_tiles;
     __syncthreads();
     for (int i = tid; i < ntok * top_k; i += 256) {
         const int slot = i % top_k;
         const uint32_t id = s_ids[i];
         // out-of-range ids are dropped (flagged by the count pass)
         const bool first = id < (uint32_t)n_expert && first_of_token(s_ids + (i / top_k) * top_k, slot, id);
-        if (first) s_slot[(i / top_k) * n_expert + id] = (uint8_t)slot;  // one writer per (token, expert)
+        if (first) s_slot[id * BK_ROW + i / top_k] = (uint8_t)slot;  // one writer per (token, expert)
     }
-    __syncthreads();
-    for (int e = tid; e < n_expert; e += 256) {
-        int pos = map[L.off + e] + map[L.chunk + (int64_t)c * n_expert + e];
-        for (int tt = 0; tt < ntok; tt++) {
-            const int sl = s_slot[tt * n_expert + e];
-            if (sl != 0xFF) map[L.list + pos++] = (tok0 + tt) * top_k + sl;
+    for (int d = 1; d < 256; d <<= 1) {  // inclusive scans of (pairs, tiles) over threads
+        const int va = tid >= d ? s_a[tid - d] : 0, vb = tid >= d ? s_b[tid - d] : 0;
+        __syncthreads();
+        s_a[tid] += va;
+        s_b[tid] += vb;
+        __syncthreads();
+    }
+    int po = s_a[tid] - sum_pairs, to = s_b[tid] - sum_tiles;
+    int32_t *dst = map + L.list;
+#pragma unroll
+    for (int j = 0; j < BK_EPT; j++) {
+        const int e = e0 + j;
+        if (e >= e1) continue;
+        if (c == 0) {  // the header
+            map[L.tpe + e] = tot[j];
+            map[L.off + e] = po;
+            const int mt = (tot[j] + bm - 1) / bm;
+            for (int m = 0; m < mt; m++) map[L.tiles + to + m] = (e << 16) | m;
+            to += mt;
         }
+        int pos = po + before[j];
+        po += tot[j];
+        const uint4 *row = reinterpret_cast<const uint4 *>(s_slot + e * BK_ROW);
+        const uint4 q[4] = {row[0], row[1], row[2], row[3]};
+        const uint32_t wd[16] = {q[0].x, q[0].y, q[0].z, q[0].w, q[1].x, q[1].y, q[1].z, q[1].w,
+                                 q[2].x, q[2].y, q[2].z, q[2].w, q[3].x, q[3].y, q[3].z, q[3].w};
+#pragma unroll
+        for (int tt = 0; tt < BK_CHUNK; tt++) {
+            const uint32_t sl = (wd[tt >> 2] >> (8 * (tt & 3))) & 0xFFu;
+            if (sl != 0xFFu) dst[pos++] = (tok0 + tt) * top_k + (int)sl;  // (rows past ntok stay 0xFF)
+        }
+    }
+    if (c == 0 && tid == 255) {
+        map[L.off + n_expert] = s_a[255];
+        map[L.n_tiles] = s_b[255];
+        map[L.dup] = s_flag;
     }
 }
 
 // The same list for expert counts whose slot table does not fit in LDS: each
 // expert's thread scans the chunk's ids directly.
 __global__ void __launch_bounds__(256) k_bucket_fill_scan(const uint32_t *__restrict__ ids, int t,
-                                                          int top_k, int n_expert,
+                                                          int top_k, int routed_k, int n_expert,
                                                           int32_t *__restrict__ map) {
     extern __shared__ uint32_t s_ids[];
     const MapLayout L(n_expert, t, top_k);
     const int c = blockIdx.x, tid = threadIdx.x;
     const int tok0 = c * BK_CHUNK;
     const int ntok = min(BK_CHUNK, t - tok0);
-    for (int i = tid; i < ntok * top_k; i += 256) s_ids[i] = ids[(int64_t)tok0 * top_k + i];
+    stage_chunk_ids(ids, tok0, ntok * top_k, top_k, routed_k, n_expert, s_ids);
     __syncthreads();
     for (int e = tid; e < n_expert; e += 256) {
         int pos = map[L.off + e] + map[L.chunk + (int64_t)c * n_expert + e];
@@ -194,26 +273,30 @@ __global__ void __launch_bounds__(256) k_bucket_fill_scan(const uint32_t *__rest
 }
 
 mx_status launch_map0(const uint32_t *ids, int t, int top_k, int n_expert, int32_t *map,
-                      hipStream_t s, int bm) {
+                      hipStream_t s, int bm, int routed_k) {
+    if (routed_k <= 0) routed_k = top_k;
     const MapLayout L(n_expert, t, top_k);
     const size_t ids_lds = (size_t)BK_CHUNK * top_k * 4;
     if (t > 0) {
         hipLaunchKernelGGL(k_bucket_count, dim3((unsigned)L.nchunks), dim3(256), n_expert * 4 + ids_lds, s, ids, t,
-                           top_k, n_expert, map);
+                           top_k, routed_k, n_expert, map);
         MX_LAUNCH("k_bucket_count");
+    }
+    const size_t slot_lds = (size_t)n_expert * BK_ROW + ids_lds;
+    if (t > 0 && slot_lds <= 60 * 1024 && n_expert <= 256 * BK_EPT) {
+        // the fill pass forms the offsets itself (and block 0 writes the header)
+        hipLaunchKernelGGL(k_bucket_fill, dim3((unsigned)L.nchunks), dim3(256), slot_lds, s, ids, t, top_k,
+                           routed_k, n_expert, bm, map);
+        MX_LAUNCH("k_bucket_fill");
+        return MX_OK;
     }
     // writes the whole header (tpe, off, n_tiles, dup), also for t == 0
     hipLaunchKernelGGL(k_bucket_scan, dim3(1), dim3(1024), 0, s, t, top_k, n_expert, bm, map);
     MX_LAUNCH("k_bucket_scan");
     if (t == 0) return MX_OK;
-    const size_t slot_lds = (size_t)BK_CHUNK * ((n_expert + 3) & ~3) + ids_lds;
-    if (slot_lds <= 96 * 1024) {
-        hipLaunchKernelGGL(k_bucket_fill, dim3((unsigned)L.nchunks), dim3(256), slot_lds, s, ids, t, top_k,
-                           n_expert, map);
-        MX_LAUNCH("k_bucket_fill");
-    } else {
+    {
         hipLaunchKernelGGL(k_bucket_fill_scan, dim3((unsigned)L.nchunks), dim3(256), BK_CHUNK * top_k * 4, s, ids,
-                           t, top_k, n_expert, map);
+                           t, top_k, routed_k, n_expert, map);
         MX_LAUNCH("k_bucket_fill_scan");
     }
     return MX_OK;
