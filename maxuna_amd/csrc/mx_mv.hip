@@ -1301,6 +1301,126 @@ __global__ void __launch_bounds__(64 * DN_SLOTS_MAX) k_decode_down_q6(DecodeDown
 #ifndef MX_DN_Q6
 #define MX_DN_Q6 1
 #endif
+// Ring form of k_decode_down_q6: the 16-row tile in four 4-row batches through
+// two LDS buffers per slot wave, so batch b + 1's copy is in flight while batch
+// b is contracted (the 8-row form copies a batch into the wave's one buffer
+// and waits for it before every contraction).  The staged act row (4992 bytes)
+// is built in the second buffer while the first batch's copy runs, and read
+// into registers before that buffer's first copy.  Work, arithmetic and
+// summation order per row are the 8-row kernel's.
+#ifndef MX_DQ6_RING
+#define MX_DQ6_RING 1
+#endif
+constexpr int DQ6R_BROWS = 4, DQ6R_CH = DQ6R_BROWS * DQ6_RB / 16, DQ6R_NI = (DQ6R_CH + 63) / 64;
+static_assert(DQ6R_BROWS == DQ6_RPI, "one row per lane group per batch");
+__global__ void __launch_bounds__(64 * DN_SLOTS_MAX) k_decode_down_q6r(DecodeDownArgs a, Geo<kQ6_K> geo) {
+    constexpr int DT = kQ6_K, NB = RW_DN / DQ6R_BROWS;
+    // two separate LDS objects, so the compiler can tell a copy into one buffer
+    // from the reads of the other
+    __shared__ __attribute__((aligned(16))) uint8_t ring0[DN_SLOTS_MAX][DQ6R_NI * 1024];
+    __shared__ __attribute__((aligned(16))) uint8_t ring1[DN_SLOTS_MAX][DQ6R_NI * 1024];
+    __shared__ float s_part[DN_SLOTS_MAX][RW_DN];
+    static_assert((size_t)xstage_bytes(DQ6_FF) <= (size_t)DQ6R_NI * 1024, "the staged row fits one buffer");
+    const int slots = a.top_k + (a.sh_down ? 1 : 0);
+    const int slot = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int sub = lane & (DQ6_P - 1), rsub = lane / DQ6_P;
+    const int tok = blockIdx.y;
+    const int r0 = blockIdx.x * RW_DN;
+    const float *xrow = a.act + ((int64_t)tok * slots + slot) * a.ff;
+    const uint8_t *wp;
+    if (slot < a.top_k) {
+        const uint32_t id = a.ids[tok * a.top_k + slot];
+        const int e = id < (uint32_t)a.n_expert ? (int)id : a.n_expert - 1;
+        wp = a.down + (int64_t)e * a.d_expert_bytes;
+    } else {
+        wp = a.sh_down;
+    }
+    wp += (int64_t)r0 * DQ6_RB;
+    uint8_t *const b0 = ring0[slot], *const b1 = ring1[slot];
+    // every lane copies (the last instruction's spare lanes repeat the batch's last
+    // chunk into the buffer's unused tail): no branch around a copy, so the
+    // compiler's copy counts stay exact and it adds no vmcnt(0) of its own
+    auto issue = [&](int bi, uint8_t *dst) {
+        const uint8_t *src = wp + bi * (DQ6R_BROWS * DQ6_RB);
+#pragma unroll
+        for (int q = 0; q < DQ6R_NI; q++) {
+            const int ci = min(64 * q + lane, DQ6R_CH - 1);
+            dma16(src + (uint32_t)(16 * ci), dst + 1024 * q);
+        }
+        asm volatile("" ::: "memory");
+    };
+    XPreT<XPRE_W> xp;
+    stage_pre_t(xrow, a.ff, xp, lane, 64);
+    // the act loads have returned before the first copy is issued (ordinary loads
+    // are not counted across LDS copies), so the copy overlaps the staging work
+    wait_vmcnt(0);
+#pragma unroll
+    for (int i = 0; i < XPRE_W; i++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) asm volatile("" : "+v"(xp.v[i][j]));
+    issue(0, b0);
+    typename Q<DT>::X xs[DQ6_NG];
+    stage_post_t(xrow, a.ff, xp, b1, lane, 64);
+    load_xs<DT, DQ6_NG>(b1, a.ff, geo, xs);
+    wait_lgkmcnt0();
+    if (NB > 1) issue(1, b1);
+    // this lane's field offsets inside a row (Q<kQ6_K>::load's, hoisted)
+    uint32_t oa[DQ6_NG], ohq[DQ6_NG], osc[DQ6_NG], od[DQ6_NG], sh[DQ6_NG];
+#pragma unroll
+    for (int jg = 0; jg < DQ6_NG; jg++) {
+        const int g = sub + DQ6_P * jg, b = g >> 3, gi = g & 7, n = gi >> 2, j = gi & 3;
+        const uint32_t mis = (uint32_t)(210 * b) & 2u, ab = (uint32_t)(210 * b) - mis;
+        oa[jg] = ab + 64 * n + 8 * j;
+        ohq[jg] = ab + 128 + 32 * n + 8 * j;
+        osc[jg] = ab + 192 + 8 * n;
+        od[jg] = (uint32_t)(210 * b) + 208;
+        sh[jg] = mis << 3;
+    }
+#pragma unroll
+    for (int bi = 0; bi < NB; bi++) {
+        uint8_t *const buf = (bi & 1) ? b1 : b0;
+        wait_vmcnt(bi + 1 < NB ? DQ6R_NI : 0);  // batch bi has landed (bi + 1 may be in flight)
+        const uint8_t *rl = buf + rsub * DQ6_RB;
+        float acc[1][1];
+        {
+            float v = 0.f;
+#pragma unroll
+            for (int jg = 0; jg < DQ6_NG; jg++) {
+                typename Q<DT>::Raw r;
+                Q<DT>::ld3(rl + oa[jg], r.a);
+                Q<DT>::ld3(rl + oa[jg] + 32, r.b);
+                Q<DT>::ld3(rl + ohq[jg], r.hq);
+                Q<DT>::ld3(rl + osc[jg], r.sc);
+                r.d = ld_u16(rl + od[jg]);
+                r.sh = sh[jg];
+                v += Q<DT>::dot(r, sub + DQ6_P * jg, xs[jg]);
+            }
+            acc[0][0] = v;
+        }
+        int which;
+        bool leader;
+        reduce_tuples<1, 1>(acc, DQ6_P, sub, which, leader);
+        if (leader) s_part[slot][bi * DQ6R_BROWS + rsub] = acc[0][0];
+        if (bi + 2 < NB) {
+            wait_lgkmcnt0();  // every read of the buffer returned before it is overwritten
+            issue(bi + 2, buf);
+        }
+    }
+    __syncthreads();
+    const int r = threadIdx.x;
+    if (r >= RW_DN) return;
+    const int c = r0 + r;
+    const int64_t o = (int64_t)tok * a.hidden + c;
+    const float shv = a.sh_down ? s_part[a.top_k][r] : a.shared_out ? a.shared_out[o] : 0.f;
+    const float res = a.residual ? a.residual[o] : 0.f;
+    const float *wt = a.w + tok * a.top_k;
+    float vv = 0.f;
+    for (int s2 = 0; s2 < a.top_k; s2++) vv = vv + s_part[s2][r] * wt[s2];
+    if (a.sh_down || a.shared_out) vv = vv + shv;
+    if (a.residual) vv = res + vv;
+    a.out[o] = vv;
+}
+
 static bool dn_q6_ok(const DecodeDownArgs &a) {
     if (MX_DN_Q6 == 0) return false;
     auto al = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
@@ -1348,8 +1468,11 @@ static mx_status launch_dn_slots_dt(const DecodeDownArgs &a, hipStream_t s) {
         if (dn_q6_ok(a)) {
             const int slots = a.top_k + (a.sh_down ? 1 : 0);
             const dim3 grid((unsigned)(a.hidden / RW_DN), (unsigned)a.t);
-            hipLaunchKernelGGL(k_decode_down_q6, grid, dim3(64 * slots), (size_t)slots * DQ6_NI * 1024, s, a,
-                               Geo<kQ6_K>(DQ6_FF, DN_FULL));
+            if (MX_DQ6_RING)
+                hipLaunchKernelGGL(k_decode_down_q6r, grid, dim3(64 * slots), 0, s, a, Geo<kQ6_K>(DQ6_FF, DN_FULL));
+            else
+                hipLaunchKernelGGL(k_decode_down_q6, grid, dim3(64 * slots), (size_t)slots * DQ6_NI * 1024, s, a,
+                                   Geo<kQ6_K>(DQ6_FF, DN_FULL));
             return MX_OK;
         }
     }
