@@ -15,6 +15,7 @@
 #include "mx_launch.h"
 #include "mx_stage.h"
 #include "mx_select.h"
+#include "mx_dma.h"
 
 namespace mx {
 
@@ -184,9 +185,120 @@ __global__ void __launch_bounds__(64 * RL_W) k_route_logits_mfma(const float *__
     }
 }
 
+// The same contraction with its operands staged through LDS (hidden % 128 == 0).
+// Per 128-wide K stage the block's 32 x rows and 64 router rows (48 KB) are
+// copied into LDS by global_load_lds, each copy instruction moving two whole
+// 512-byte row slices (8 cache lines, where a lane-per-row register load
+// touches 32), double-buffered so stage s + 1 is in flight while stage s is
+// contracted (a third buffer measured slower: 50 against 47 us at C3).  Wave w contracts the stage's 16-wide chunk w, so chunk c of K
+// still goes to wave c % 8 with the lane permutation of k_route_logits_mfma:
+// the sums are the same operations in the same order, bit for bit.  The 16-byte
+// chunks of a row are XOR-swizzled by row (position = chunk ^ (row & 31)), so
+// the 32 lanes reading one chunk of 32 rows hit distinct banks.
+#ifndef MX_RL_LDS
+#define MX_RL_LDS 1
+#endif
+constexpr int RLL_KS = 128, RLL_ROWB = RLL_KS * 4, RLL_ROWS = RL_T + RL_E;   // 96 rows of 512 bytes
+constexpr int RLL_STAGE = RLL_ROWS * RLL_ROWB, RLL_NI = RLL_STAGE / 1024;       // 48 KB, 48 copies
+static_assert(RLL_NI % RL_W == 0, "copies split evenly over the waves");
+static_assert(2 * RLL_STAGE >= RL_W * RL_T * RL_E * 4, "the reduction fits the staging buffers");
+
+__global__ void __launch_bounds__(64 * RL_W) k_route_logits_lds(const float *__restrict__ x,
+                                                                 const float *__restrict__ r, int t, int hidden,
+                                                                 int n_expert, float *__restrict__ logits) {
+    // two separate objects: a copy into one buffer is not ordered against reads of the other
+    __shared__ __attribute__((aligned(1024))) uint8_t sb0[RLL_STAGE];
+    __shared__ __attribute__((aligned(1024))) uint8_t sb1[RLL_STAGE];
+    const int t0 = blockIdx.y * RL_T, e0 = blockIdx.x * RL_E;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int i = lane & 31, kh = lane >> 5;
+    // copy q of a stage moves LDS bytes [1024 q, 1024 q + 1024): rows 2q and 2q + 1
+    // (0..31: x rows, 32..95: router rows); lane l writes position l & 31 of row
+    // 2q + (l >> 5), which holds the row's chunk (l & 31) ^ (row & 31)
+    const float *src[RLL_NI / RL_W];
+#pragma unroll
+    for (int u = 0; u < RLL_NI / RL_W; u++) {
+        const int q = wave + RL_W * u, row = 2 * q + (lane >> 5);
+        const int chunk = (lane & 31) ^ (row & 31);
+        const float *base = row < RL_T ? x + (int64_t)min(t0 + row, t - 1) * hidden
+                                       : r + (int64_t)min(e0 + row - RL_T, n_expert - 1) * hidden;
+        src[u] = base + 4 * chunk;
+    }
+    auto issue = [&](int st, uint8_t *buf) {
+#pragma unroll
+        for (int u = 0; u < RLL_NI / RL_W; u++)
+            dma16(reinterpret_cast<const uint8_t *>(src[u] + (int64_t)st * RLL_KS), buf + 1024 * (wave + RL_W * u));
+        asm volatile("" ::: "memory");
+    };
+    // this lane's operand addresses inside a stage: chunks 4w + 2kh and 4w + 2kh + 1
+    // of its x row i and router rows i and 32 + i
+    auto pos = [&](int row, int c) { return row * RLL_ROWB + 16 * (c ^ (row & 31)); };
+    const int c0 = 4 * wave + 2 * kh;
+    const int ax0 = pos(i, c0), ax1 = pos(i, c0 + 1);
+    const int aa0 = pos(RL_T + i, c0), aa1 = pos(RL_T + i, c0 + 1);
+    const int ab0 = pos(RL_T + 32 + i, c0), ab1 = pos(RL_T + 32 + i, c0 + 1);
+    float16_t acc0, acc1;
+#pragma unroll
+    for (int q = 0; q < 16; q++) acc0[q] = acc1[q] = 0.f;
+    const int nst = hidden / RLL_KS;
+    // stage st from cur while stage st + 1 is copied into nxt; the loop is unrolled
+    // by two so each buffer is a compile-time object (a runtime choice between
+    // them makes the compiler wait for every copy before any LDS read)
+    auto step = [&](int st, const uint8_t *cur, uint8_t *nxt) {
+        wait_vmcnt(0);    // this wave's copies of stage st have landed
+        __syncthreads();  // every wave's copies have; every read of nxt (stage st - 1) is done
+        if (st + 1 < nst) issue(st + 1, nxt);
+        const float4 x0 = *reinterpret_cast<const float4 *>(cur + ax0), x1 = *reinterpret_cast<const float4 *>(cur + ax1);
+        const float4 a0 = *reinterpret_cast<const float4 *>(cur + aa0), a1 = *reinterpret_cast<const float4 *>(cur + aa1);
+        const float4 b0 = *reinterpret_cast<const float4 *>(cur + ab0), b1 = *reinterpret_cast<const float4 *>(cur + ab1);
+        const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        const float as[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+        const float bs[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(xs[q], as[q], acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(xs[q], bs[q], acc1, 0, 0, 0);
+        }
+    };
+    issue(0, sb0);
+    for (int st = 0; st < nst; st += 2) {
+        step(st, sb0, sb1);
+        if (st + 1 < nst) step(st + 1, sb1, sb0);
+    }
+    __syncthreads();  // the staging buffers now hold the wave partials
+    // the wave partials [RL_W][RL_T * RL_E] over sb0 | sb1
+    static_assert(RLL_STAGE % (RL_T * RL_E * 4) == 0, "wave partial tiles do not straddle the buffers");
+    auto red_at = [&](int w2) -> float * {
+        const int per = RLL_STAGE / (RL_T * RL_E * 4);
+        return reinterpret_cast<float *>(w2 < per ? sb0 : sb1) + (w2 % per) * (RL_T * RL_E);
+    };
+    // acc[q] = D[token 8 (q / 4) + 4 kh + q % 4][expert i (+ 32)]
+    float *mine = red_at(wave);
+#pragma unroll
+    for (int q = 0; q < 16; q++) {
+        const int row = 8 * (q >> 2) + 4 * kh + (q & 3);
+        mine[row * RL_E + i] = acc0[q];
+        mine[row * RL_E + 32 + i] = acc1[q];
+    }
+    __syncthreads();
+    for (int o = threadIdx.x; o < RL_T * RL_E; o += 64 * RL_W) {
+        float v = red_at(0)[o];
+#pragma unroll
+        for (int w2 = 1; w2 < RL_W; w2++) v += red_at(w2)[o];
+        const int tok = t0 + o / RL_E, e = e0 + o % RL_E;
+        if (tok < t && e < n_expert) logits[(int64_t)tok * n_expert + e] = v;
+    }
+}
+
 mx_status launch_route_logits(const float *x, const float *router, int t, int hidden, int n_expert, float *logits,
                               hipStream_t s) {
     if (t == 0) return MX_OK;
+    if (MX_RL_LDS && hidden % RLL_KS == 0 && t >= 8) {
+        const dim3 grid((unsigned)((n_expert + RL_E - 1) / RL_E), (unsigned)((t + RL_T - 1) / RL_T));
+        hipLaunchKernelGGL(k_route_logits_lds, grid, dim3(64 * RL_W), 0, s, x, router, t, hidden, n_expert, logits);
+        MX_LAUNCH("k_route_logits_lds");
+        return MX_OK;
+    }
     if (hidden % RL_KC == 0 && t >= 8) {
         const dim3 grid((unsigned)((n_expert + RL_E - 1) / RL_E), (unsigned)((t + RL_T - 1) / RL_T));
         hipLaunchKernelGGL(k_route_logits_mfma, grid, dim3(64 * RL_W), 0, s, x, router, t, hidden, n_expert, logits);

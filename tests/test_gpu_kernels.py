@@ -172,13 +172,16 @@ def test_route_kats_on_device(dev, orc):
 
 
 def test_route_logits(dev, orc):
+    """t = 1: the plain kernel; t >= 8 with hidden % 128 == 0: the LDS-staged MFMA
+    kernel; hidden 1040 (% 16 only): the register-fed MFMA kernel (the two MFMA
+    kernels form the same sums in the same order)."""
     _log("route_logits")
     rng = np.random.default_rng(5)
-    for t in (1, 70):
-        x = rng.standard_normal((t, 1024)).astype(np.float32)
-        r = (rng.standard_normal((256, 1024)) * 0.02).astype(np.float32)  # [n_expert, hidden]
+    for t, hidden, n_expert in ((1, 1024, 256), (70, 1024, 256), (45, 1040, 100), (45, 1024, 100)):
+        x = rng.standard_normal((t, hidden)).astype(np.float32)
+        r = (rng.standard_normal((n_expert, hidden)) * 0.02).astype(np.float32)  # [n_expert, hidden]
         got = host(ops.route_logits(dev_f32(r), dev_f32(x)))
-        assert_close(got, orc.route_logits(x, np.ascontiguousarray(r.T)), rel=1e-5, what="logits")
+        assert_close(got, orc.route_logits(x, np.ascontiguousarray(r.T)), rel=1e-5, what=f"logits t={t} h={hidden}")
 
 
 def _distinct_ids(rng, t, k, E):
