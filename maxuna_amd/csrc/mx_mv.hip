@@ -821,6 +821,10 @@ k_decode_gate_up(DecodeGateUpArgs a, int ni, int slot0, Geo<DT> geo) {
 #define MX_GU64_R 2
 #endif
 constexpr int GU64_R = MX_GU64_R;
+#ifndef MX_GU64_TPB
+#define MX_GU64_TPB 8
+#endif
+constexpr int GU64_TPB = MX_GU64_TPB;
 template <int DT> struct Row64 {
     static_assert(DT == kQ4_K || DT == kQ5_K, "64-group rows: the K-quants with 64-weight groups");
     static constexpr int RB = 16 * (DT == kQ4_K ? 144 : 176);  // row bytes (16 super-blocks)
@@ -828,7 +832,7 @@ template <int DT> struct Row64 {
 };
 constexpr int GU_SEL_E = 256;  // experts of the in-block top-k
 static_assert(64 * WAVES == SEL_THREADS, "the in-block top-k needs SEL_THREADS threads");
-template <int DT, int R>
+template <int DT, int R, bool LOOP>
 __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(MX_GU_WPE)))
 k_decode_gate_up64(DecodeGateUpArgs a, int slot0, Geo<DT> geo) {
     constexpr int RB = Row64<DT>::RB, CH = Row64<DT>::CH, NI = Row64<DT>::NI;
@@ -844,9 +848,11 @@ k_decode_gate_up64(DecodeGateUpArgs a, int slot0, Geo<DT> geo) {
     }
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    const int r0 = (blockIdx.x * WAVES + wave) * R;
+    // LOOP: the workgroup walks row-pair tiles blockIdx.x, blockIdx.x + gridDim.x,
+    // ... of its (slot, token), loading the activation slices and the expert once
+    const int rfirst = (blockIdx.x * WAVES + wave) * R;
     typename Q<DT>::X xs[1];
-    if (r0 < a.ff) load_xs_gm<DT, 1>(a.xstage_gm + (int64_t)tok * xstage_gm_stride(a.hidden), a.hidden, geo, xs);
+    if (rfirst < a.ff) load_xs_gm<DT, 1>(a.xstage_gm + (int64_t)tok * xstage_gm_stride(a.hidden), a.hidden, geo, xs);
     if (a.sel_keys && slot < a.top_k) {  // block-uniform: the whole block selects (t == 1)
         auto &sh = *reinterpret_cast<SelSharedT<GU_SEL_E> *>(lds + WAVES * 2 * RB);
         const bool writer = blockIdx.x == 0 && blockIdx.y == 0;
@@ -854,8 +860,7 @@ k_decode_gate_up64(DecodeGateUpArgs a, int slot0, Geo<DT> geo) {
                                  a.sel_norm, writer ? a.sel_ids : nullptr, a.sel_w, sh);
         pe = sh.pick[slot];
     }
-    if (r0 >= a.ff) return;  // wave-uniform; no block barrier below
-    const int n = min(R, a.ff - r0);
+    if (rfirst >= a.ff) return;  // wave-uniform; no block barrier below
     const uint8_t *gw, *uw;
     if (slot < a.top_k) {
         const uint32_t id = pe >= 0 ? (uint32_t)pe : a.ids[tok * a.top_k + slot];
@@ -866,9 +871,15 @@ k_decode_gate_up64(DecodeGateUpArgs a, int slot0, Geo<DT> geo) {
         gw = a.sh_gate;
         uw = a.sh_up;
     }
-    gw += (int64_t)r0 * RB;
-    uw += (int64_t)r0 * RB;
+    const uint8_t *const gw0 = gw, *const uw0 = uw;
     uint8_t *buf = lds + wave * (2 * RB);
+    for (int tile = blockIdx.x;; tile += gridDim.x) {
+    const int r0 = (tile * WAVES + wave) * R;
+    if (LOOP && r0 >= a.ff) break;
+    const int n = min(R, a.ff - r0);
+    gw = gw0 + (int64_t)r0 * RB;
+    uw = uw0 + (int64_t)r0 * RB;
+    if (LOOP && tile != (int)blockIdx.x) wait_lgkmcnt0();  // the last tile's reads of the buffer returned
     // row r of matrix m (0 gate, 1 up) into the matrix's half of the buffer; every
     // address a scalar base plus a 32-bit lane offset
     auto issue = [&](int m, int r) {
@@ -919,6 +930,8 @@ k_decode_gate_up64(DecodeGateUpArgs a, int slot0, Geo<DT> geo) {
 #pragma unroll
         for (int r = 0; r < R; r++)
             if (r == lane) act[r] = res[r];
+    }
+    if (!LOOP) break;
     }
 }
 
@@ -1019,10 +1032,18 @@ static mx_status launch_gu_dt(const DecodeGateUpArgs &a, int slot0, int nslot, h
     if constexpr (DT == kQ4_K || DT == kQ5_K) {
         if (gu64_ok<DT>(a)) {
             const unsigned tiles = (unsigned)((a.ff + WAVES * GU64_R - 1) / (WAVES * GU64_R));
-            const dim3 grid(tiles, (unsigned)nslot, (unsigned)a.t);
+            // verify blocks (t > 1): GU64_TPB tiles per workgroup, the activation
+            // slices and per-wave setup amortised over more rows (C2: 8 tiles
+            // 369 -> 363 us; 16 and 24 slower; t = 1 keeps one tile per workgroup)
+            const bool loop = a.t > 1 && GU64_TPB > 1;
+            const dim3 grid(loop ? (tiles + GU64_TPB - 1) / GU64_TPB : tiles, (unsigned)nslot, (unsigned)a.t);
             const size_t lds = (size_t)WAVES * 2 * Row64<DT>::RB + (a.sel_keys ? sizeof(SelSharedT<GU_SEL_E>) : 0);
-            hipLaunchKernelGGL((k_decode_gate_up64<DT, (GU64_R > 0 ? GU64_R : 1)>), grid, dim3(64 * WAVES), lds, s, a, slot0,
-                               Geo<DT>(a.hidden));
+            if (loop)
+                hipLaunchKernelGGL((k_decode_gate_up64<DT, (GU64_R > 0 ? GU64_R : 1), true>), grid, dim3(64 * WAVES), lds,
+                                   s, a, slot0, Geo<DT>(a.hidden));
+            else
+                hipLaunchKernelGGL((k_decode_gate_up64<DT, (GU64_R > 0 ? GU64_R : 1), false>), grid, dim3(64 * WAVES), lds,
+                                   s, a, slot0, Geo<DT>(a.hidden));
             return MX_OK;
         }
     }
