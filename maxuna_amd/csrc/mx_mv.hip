@@ -607,6 +607,10 @@ constexpr bool GU_EARLY = MX_GU_EARLY != 0;
 #endif
 constexpr int WAVES = MX_WAVES;
 constexpr int WAVES_DN = MX_WAVES_DN;  // waves per block of the fused down kernel
+#ifndef MX_DN_TPB
+#define MX_DN_TPB 4
+#endif
+constexpr int DN_TPB = MX_DN_TPB;  // RW_DN-row tiles per wave of k_decode_down
 constexpr int RW_MV = 16, RW_GU = MX_RW_GU, RW_DN = MX_RW_DN;
 constexpr int RING_MV = 2, RING_GU = MX_RING_GU, RING_DN = MX_RING_DN;
 
@@ -1090,7 +1094,9 @@ mx_status launch_decode_gate_up(int dtype, const DecodeGateUpArgs &a, int slot0,
 }
 
 // ---- fused decode: down (one slot per block), then the combine kernel ---------------------
-// grid (hidden / (WAVES_DN * RW_DN), n_slot_blocks, t).  Each block writes its slot's down rows to part[tok, slot, :]; the
+// grid (hidden / (WAVES_DN * rpw), slots, t), rpw = RW_DN * DN_TPB rows per wave (C2:
+// 4 tiles per wave 362 -> 334 us, the act row staged once per workgroup for 4x the
+// rows; 2 and 8 measured 343).  Each block writes its slot's down rows to part[tok, slot, :]; the
 // combine kernel that follows on the stream (the kernel boundary orders the two)
 // forms out[c] = residual[c] + ( sum_k w[k] * part[k][c] + shared[c] )
 // (combine.metal:70-97, moe.rs:73-78, model.rs:351).  The shared expert is
@@ -1099,7 +1105,7 @@ mx_status launch_decode_gate_up(int dtype, const DecodeGateUpArgs &a, int slot0,
 #define MX_DN_WPE 1
 #endif
 template <int DT, int NG>
-__global__ void __launch_bounds__(64 * WAVES_DN) __attribute__((amdgpu_waves_per_eu(MX_DN_WPE))) k_decode_down(DecodeDownArgs a, int ni, Geo<DT> geo) {
+__global__ void __launch_bounds__(64 * WAVES_DN) __attribute__((amdgpu_waves_per_eu(MX_DN_WPE))) k_decode_down(DecodeDownArgs a, int ni, int rpw, Geo<DT> geo) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int slots = a.top_k + (a.sh_down ? 1 : 0);
     const int tile = blockIdx.x;  // grid (row tiles, slots, t)
@@ -1110,9 +1116,8 @@ __global__ void __launch_bounds__(64 * WAVES_DN) __attribute__((amdgpu_waves_per
         slot = (v & 0xFFFF) % slots;
         pe = v >> 16;
     }
-    constexpr int ROWS_PER_WG = WAVES_DN * RW_DN;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (scalar)
-    const int r0 = tile * ROWS_PER_WG + wave * RW_DN;
+    const int r0 = (tile * WAVES_DN + wave) * rpw;  // rpw rows per wave, the act row staged once
     const float *xrow = a.act + ((int64_t)tok * slots + slot) * a.ff;
     uint8_t *ring = lds + align16(xstage_bytes(a.ff)) + wave * (RING_DN * ni * 1024);
     XPre xp;
@@ -1135,7 +1140,7 @@ __global__ void __launch_bounds__(64 * WAVES_DN) __attribute__((amdgpu_waves_per
     const uint8_t *const w[1] = {wp};
     typename Q<DT>::X xs[NG];
     float *part = a.part + ((int64_t)tok * slots + slot) * a.hidden;
-    stream_rows<DT, NG, BatchDn<NG>::NIT, 1, RING_DN>(w, rb, geo, xs, r0, min(r0 + RW_DN, a.hidden), ring, ni,
+    stream_rows<DT, NG, BatchDn<NG>::NIT, 1, RING_DN>(w, rb, geo, xs, r0, min(r0 + rpw, a.hidden), ring, ni,
                                                      [&] { stage_pre(xrow, a.ff, xp); },
                                                      [&] {
                                                          stage_post(xrow, a.ff, xp, lds);
@@ -1510,7 +1515,10 @@ static mx_status launch_dn_ng(const DecodeDownArgs &a, dim3 grid, hipStream_t s)
     if (ni > DMA_MAX_INSTS) return fail(MX_ERR_SHAPE, "decode down: rows too long for the LDS ring");
     const size_t lds = align16(xstage_bytes(a.ff)) + (size_t)WAVES_DN * RING_DN * ni * 1024;
     if (lds > 160 * 1024) return fail(MX_ERR_SHAPE, "decode down: expert_ff = %d needs %zu bytes of LDS", a.ff, lds);
-    hipLaunchKernelGGL((k_decode_down<DT, NG>), grid, dim3(64 * WAVES_DN), lds, s, a, ni, Geo<DT>(a.ff, DN_FULL));
+    // RW_DN * DN_TPB rows per wave: each workgroup stages its act row once for that many
+    const int rpw = RW_DN * DN_TPB;
+    const dim3 g((unsigned)((a.hidden + WAVES_DN * rpw - 1) / (WAVES_DN * rpw)), grid.y, grid.z);
+    hipLaunchKernelGGL((k_decode_down<DT, NG>), g, dim3(64 * WAVES_DN), lds, s, a, ni, rpw, Geo<DT>(a.ff, DN_FULL));
     return MX_OK;
 }
 
