@@ -341,6 +341,12 @@ template <int DT> __device__ __forceinline__ void wb_load(WB<DT> &w, const uint8
     else w.load_lds(slot, kh, m1);
 }
 
+#ifndef MX_GEMM_IGLP_SWIGLU
+#define MX_GEMM_IGLP_SWIGLU -1
+#endif
+#ifndef MX_GEMM_IGLP_PLAIN
+#define MX_GEMM_IGLP_PLAIN 0
+#endif
 #ifndef MX_GEMM_BPAD
 #define MX_GEMM_BPAD 2
 #endif
@@ -559,6 +565,11 @@ __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
         for (int mb = 0; mb < MB; mb++) af[0][mb] = *reinterpret_cast<const half8_t *>(buf + mb * 32 * ROWB + aoff[0]);
 #pragma unroll
         for (int s = 0; s < 8; s++) {
+            // plain tiles: let the scheduler interleave the step's LDS reads,
+            // dequantisation and MFMAs (iglp_opt(0): down GEMM 548 -> 520 us at C3);
+            // the SwiGLU tiles measured slower with it (0 or 1: +2-4%)
+            if constexpr (!SWIGLU && MX_GEMM_IGLP_PLAIN >= 0) __builtin_amdgcn_iglp_opt(MX_GEMM_IGLP_PLAIN);
+            if constexpr (SWIGLU && MX_GEMM_IGLP_SWIGLU >= 0) __builtin_amdgcn_iglp_opt(MX_GEMM_IGLP_SWIGLU);
             const int p = s >> 1, hh = s & 1, cur = s & 1;
             if (s + 1 < 8) {
 #pragma unroll
