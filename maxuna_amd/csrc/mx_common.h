@@ -32,6 +32,13 @@ typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef float float16_t __attribute__((ext_vector_type(16)));
 
+// 16 bytes read once and not again by this kernel (streamed intermediates): a
+// non-temporal load, which keeps the stream from displacing cached lines
+__device__ __forceinline__ float4 ld_stream4(const float *p) {
+    const float4_t q = __builtin_nontemporal_load(reinterpret_cast<const float4_t *>(p));
+    return make_float4(q[0], q[1], q[2], q[3]);
+}
+
 __host__ __device__ constexpr int block_size(int dt) {
     return dt == kQ8_0 ? 32 : (dt == kQ4_K || dt == kQ5_K || dt == kQ6_K) ? 256 : -1;
 }
