@@ -11,9 +11,18 @@ namespace mx {
 
 // one 16-byte global -> LDS copy per lane; `lds_dst` must be wave-uniform (the
 // hardware writes lane i's 16 bytes at lds_dst + 16 * i)
+template <int AUX = 0>
 __device__ __forceinline__ void dma16(const uint8_t *src, uint8_t *lds_dst) {
-    __builtin_amdgcn_global_load_lds((MX_AS_GLB void *)src, (MX_AS_LDS void *)lds_dst, 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((MX_AS_GLB void *)src, (MX_AS_LDS void *)lds_dst, 16, 0, AUX);
 }
+// Cache policy of copies whose bytes nothing reads again soon: non-temporal (the
+// gfx950 NT bit of the instruction's cache-policy operand).  The t = 1 decode
+// weight streams use it (C1 layer 41.9 -> 39.5 us); verify blocks must not:
+// their repeated experts are served from L2 (C2 335 -> 353 us with it).
+#ifndef MX_DMA_NT
+#define MX_DMA_NT 2
+#endif
+constexpr int DMA_NT = MX_DMA_NT;
 
 // s_waitcnt vmcnt(n) for a wave-uniform n in 0..63 (expcnt / lgkmcnt not waited)
 #define MX_VMW(n) \

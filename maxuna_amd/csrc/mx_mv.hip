@@ -891,7 +891,7 @@ k_decode_gate_up64(DecodeGateUpArgs a, int slot0, Geo<DT> geo) {
 #pragma unroll
         for (int q = 0; q < NI; q++) {
             const int ci = 64 * q + lane;
-            if (q < NI - 1 || ci < CH) dma16(src + (uint32_t)(16 * ci), buf + m * RB + 1024 * q);
+            if (q < NI - 1 || ci < CH) dma16<LOOP ? 0 : DMA_NT>(src + (uint32_t)(16 * ci), buf + m * RB + 1024 * q);
         }
         asm volatile("" ::: "memory");
     };
@@ -1339,6 +1339,7 @@ __global__ void __launch_bounds__(64 * DN_SLOTS_MAX) k_decode_down_q6(DecodeDown
 #endif
 constexpr int DQ6R_BROWS = 4, DQ6R_CH = DQ6R_BROWS * DQ6_RB / 16, DQ6R_NI = (DQ6R_CH + 63) / 64;
 static_assert(DQ6R_BROWS == DQ6_RPI, "one row per lane group per batch");
+template <int AUX>  // cache policy of the weight copies (DMA_NT at t = 1)
 __global__ void __launch_bounds__(64 * DN_SLOTS_MAX) k_decode_down_q6r(DecodeDownArgs a, Geo<kQ6_K> geo) {
     constexpr int DT = kQ6_K, NB = RW_DN / DQ6R_BROWS;
     // two separate LDS objects, so the compiler can tell a copy into one buffer
@@ -1371,7 +1372,7 @@ __global__ void __launch_bounds__(64 * DN_SLOTS_MAX) k_decode_down_q6r(DecodeDow
 #pragma unroll
         for (int q = 0; q < DQ6R_NI; q++) {
             const int ci = min(64 * q + lane, DQ6R_CH - 1);
-            dma16(src + (uint32_t)(16 * ci), dst + 1024 * q);
+            dma16<AUX>(src + (uint32_t)(16 * ci), dst + 1024 * q);
         }
         asm volatile("" ::: "memory");
     };
@@ -1495,7 +1496,13 @@ static mx_status launch_dn_slots_dt(const DecodeDownArgs &a, hipStream_t s) {
             const int slots = a.top_k + (a.sh_down ? 1 : 0);
             const dim3 grid((unsigned)(a.hidden / RW_DN), (unsigned)a.t);
             if (MX_DQ6_RING)
-                hipLaunchKernelGGL(k_decode_down_q6r, grid, dim3(64 * slots), 0, s, a, Geo<kQ6_K>(DQ6_FF, DN_FULL));
+            {
+                if (a.t == 1)
+                    hipLaunchKernelGGL(k_decode_down_q6r<DMA_NT>, grid, dim3(64 * slots), 0, s, a,
+                                       Geo<kQ6_K>(DQ6_FF, DN_FULL));
+                else
+                    hipLaunchKernelGGL(k_decode_down_q6r<0>, grid, dim3(64 * slots), 0, s, a, Geo<kQ6_K>(DQ6_FF, DN_FULL));
+            }
             else
                 hipLaunchKernelGGL(k_decode_down_q6, grid, dim3(64 * slots), (size_t)slots * DQ6_NI * 1024, s, a,
                                    Geo<kQ6_K>(DQ6_FF, DN_FULL));
