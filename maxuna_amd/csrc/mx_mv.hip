@@ -836,8 +836,9 @@ template <int DT> struct Row64 {
 };
 constexpr int GU_SEL_E = 256;  // experts of the in-block top-k
 static_assert(64 * WAVES == SEL_THREADS, "the in-block top-k needs SEL_THREADS threads");
+// (the verify form, LOOP, runs at 4 waves/SIMD: C2 333 -> 324 us; t = 1 keeps 5)
 template <int DT, int R, bool LOOP>
-__global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(MX_GU_WPE)))
+__global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(LOOP ? 4 : MX_GU_WPE)))
 k_decode_gate_up64(DecodeGateUpArgs a, int slot0, Geo<DT> geo) {
     constexpr int RB = Row64<DT>::RB, CH = Row64<DT>::CH, NI = Row64<DT>::NI;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
