@@ -125,6 +125,7 @@ __device__ __forceinline__ void topk_select(const uint64_t (&key)[MAXE / SEL_THR
         }
     }
     __syncthreads();
+    if (!ids_out) return;  // (block-uniform) the caller needs only sh.pick: no weights
     if (tid == 0) {
         float sum = 0.f;
         for (int k = 0; k < top_k; k++) sum = sum + sh.prob[k];
