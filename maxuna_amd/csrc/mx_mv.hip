@@ -1226,117 +1226,20 @@ __global__ void __launch_bounds__(64 * DN_SLOTS_MAX) k_decode_down_slots(DecodeD
 }
 
 // Q6_K down rows of the C1 shape (ff = 1536: 48 groups of 32 weights per row of
-// 1260 bytes), compile-time: the slot-per-wave kernel's work, schedule and
-// arithmetic (16 lanes per row, 3 groups per lane, 8-row copy batches, the ring
-// overlaid on the staged act row), with every lane's field offsets computed once.
-// Rows are 4-byte aligned when the stacks are 16-byte aligned (1260 = 4 * 315),
-// so a block's 2-byte phase is its index parity: lane constants, not per-row
-// arithmetic.  Results are bit-identical to k_decode_down_slots.
+// 1260 bytes), compile-time: the slot-per-wave kernel's work and arithmetic (16
+// lanes per row, 3 groups per lane), with every lane's field offsets computed
+// once.  Rows are 4-byte aligned when the stacks are 16-byte aligned (1260 = 4 *
+// 315), so a block's 2-byte phase is its index parity: lane constants, not
+// per-row arithmetic.  Results are bit-identical to k_decode_down_slots.
+// The 16-row tile runs in four 4-row batches through two LDS buffers per slot
+// wave, so batch b + 1's copy is in flight while batch b is contracted (a form
+// that copied 8-row batches into one buffer per wave and waited for each before
+// contracting measured 17.05 against 15.4 us at C1).  The staged act row (4992
+// bytes) is built in the second buffer while the first batch's copy runs, and
+// read into registers before that buffer's first copy.
 constexpr int DQ6_FF = 1536, DQ6_RB = 1260, DQ6_P = 16, DQ6_NG = 3, DQ6_RPI = 64 / DQ6_P;
-constexpr int DQ6_BROWS = 8, DQ6_CH = DQ6_BROWS * DQ6_RB / 16, DQ6_NI = (DQ6_CH + 63) / 64;
-static_assert(DQ6_BROWS * DQ6_RB % 16 == 0, "8-row batches of whole 16-byte chunks");
-__global__ void __launch_bounds__(64 * DN_SLOTS_MAX) k_decode_down_q6(DecodeDownArgs a, Geo<kQ6_K> geo) {
-    constexpr int DT = kQ6_K, NIT = DQ6_BROWS / DQ6_RPI, NB = RW_DN / DQ6_BROWS;
-    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    __shared__ float s_part[DN_SLOTS_MAX][RW_DN];
-    const int slots = a.top_k + (a.sh_down ? 1 : 0);
-    const int slot = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-    const int sub = lane & (DQ6_P - 1), rsub = lane / DQ6_P;
-    const int tok = blockIdx.y;
-    const int r0 = blockIdx.x * RW_DN;
-    const float *xrow = a.act + ((int64_t)tok * slots + slot) * a.ff;
-    const uint8_t *wp;
-    if (slot < a.top_k) {
-        const uint32_t id = a.ids[tok * a.top_k + slot];
-        const int e = id < (uint32_t)a.n_expert ? (int)id : a.n_expert - 1;
-        wp = a.down + (int64_t)e * a.d_expert_bytes;
-    } else {
-        wp = a.sh_down;
-    }
-    wp += (int64_t)r0 * DQ6_RB;
-    // the ring reuses the staged row's bytes (the row is in registers first)
-    uint8_t *area = lds + (size_t)slot * (DQ6_NI * 1024);
-    XPreT<XPRE_W> xp;
-    stage_pre_t(xrow, a.ff, xp, lane, 64);
-    typename Q<DT>::X xs[DQ6_NG];
-    stage_post_t(xrow, a.ff, xp, area, lane, 64);
-    load_xs<DT, DQ6_NG>(area, a.ff, geo, xs);
-    wait_lgkmcnt0();
-    // this lane's field offsets inside a row (Q<kQ6_K>::load's, hoisted)
-    uint32_t oa[DQ6_NG], ohq[DQ6_NG], osc[DQ6_NG], od[DQ6_NG], sh[DQ6_NG];
-#pragma unroll
-    for (int jg = 0; jg < DQ6_NG; jg++) {
-        const int g = sub + DQ6_P * jg, b = g >> 3, gi = g & 7, n = gi >> 2, j = gi & 3;
-        const uint32_t mis = (uint32_t)(210 * b) & 2u, ab = (uint32_t)(210 * b) - mis;
-        oa[jg] = ab + 64 * n + 8 * j;
-        ohq[jg] = ab + 128 + 32 * n + 8 * j;
-        osc[jg] = ab + 192 + 8 * n;
-        od[jg] = (uint32_t)(210 * b) + 208;
-        sh[jg] = mis << 3;
-    }
-    const uint8_t *lrow = area + rsub * DQ6_RB;
-#pragma unroll
-    for (int bi = 0; bi < NB; bi++) {
-        {
-            const uint8_t *src = wp + bi * (DQ6_BROWS * DQ6_RB);
-#pragma unroll
-            for (int q = 0; q < DQ6_NI; q++) {
-                const int ci = 64 * q + lane;
-                if (q < DQ6_NI - 1 || ci < DQ6_CH) dma16(src + (uint32_t)(16 * ci), area + 1024 * q);
-            }
-            asm volatile("" ::: "memory");
-        }
-        wait_vmcnt(0);
-        float acc[NIT][1];
-#pragma unroll
-        for (int ib = 0; ib < NIT; ib++) {
-            const uint8_t *rl = lrow + ib * (DQ6_RPI * DQ6_RB);
-            float v = 0.f;
-#pragma unroll
-            for (int jg = 0; jg < DQ6_NG; jg++) {
-                typename Q<DT>::Raw r;
-                Q<DT>::ld3(rl + oa[jg], r.a);
-                Q<DT>::ld3(rl + oa[jg] + 32, r.b);
-                Q<DT>::ld3(rl + ohq[jg], r.hq);
-                Q<DT>::ld3(rl + osc[jg], r.sc);
-                r.d = ld_u16(rl + od[jg]);
-                r.sh = sh[jg];
-                v += Q<DT>::dot(r, sub + DQ6_P * jg, xs[jg]);
-            }
-            acc[ib][0] = v;
-        }
-        int which;
-        bool leader;
-        reduce_tuples<1, NIT>(acc, DQ6_P, sub, which, leader);
-        if (leader) s_part[slot][bi * DQ6_BROWS + rsub + DQ6_RPI * which] = acc[0][0];
-        if (bi + 1 < NB) wait_lgkmcnt0();  // every read of the buffer returned before it is overwritten
-    }
-    __syncthreads();
-    const int r = threadIdx.x;
-    if (r >= RW_DN) return;
-    const int c = r0 + r;
-    const int64_t o = (int64_t)tok * a.hidden + c;
-    const float shv = a.sh_down ? s_part[a.top_k][r] : a.shared_out ? a.shared_out[o] : 0.f;
-    const float res = a.residual ? a.residual[o] : 0.f;
-    const float *wt = a.w + tok * a.top_k;
-    float vv = 0.f;
-    for (int s2 = 0; s2 < a.top_k; s2++) vv = vv + s_part[s2][r] * wt[s2];
-    if (a.sh_down || a.shared_out) vv = vv + shv;
-    if (a.residual) vv = res + vv;
-    a.out[o] = vv;
-}
 #ifndef MX_DN_Q6
 #define MX_DN_Q6 1
-#endif
-// Ring form of k_decode_down_q6: the 16-row tile in four 4-row batches through
-// two LDS buffers per slot wave, so batch b + 1's copy is in flight while batch
-// b is contracted (the 8-row form copies a batch into the wave's one buffer
-// and waits for it before every contraction).  The staged act row (4992 bytes)
-// is built in the second buffer while the first batch's copy runs, and read
-// into registers before that buffer's first copy.  Work, arithmetic and
-// summation order per row are the 8-row kernel's.
-#ifndef MX_DQ6_RING
-#define MX_DQ6_RING 1
 #endif
 constexpr int DQ6R_BROWS = 4, DQ6R_CH = DQ6R_BROWS * DQ6_RB / 16, DQ6R_NI = (DQ6R_CH + 63) / 64;
 static_assert(DQ6R_BROWS == DQ6_RPI, "one row per lane group per batch");
@@ -1454,7 +1357,7 @@ static bool dn_q6_ok(const DecodeDownArgs &a) {
     auto al = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
     const Geo<kQ6_K> g(DQ6_FF, DN_FULL);
     return a.ff == DQ6_FF && a.d_row_bytes == DQ6_RB && g.P == DQ6_P && g.NG == DQ6_NG && g.G == DQ6_P * DQ6_NG &&
-           a.hidden % RW_DN == 0 && (size_t)xstage_bytes(DQ6_FF) <= (size_t)DQ6_NI * 1024 &&
+           a.hidden % RW_DN == 0 && (size_t)xstage_bytes(DQ6_FF) <= (size_t)DQ6R_NI * 1024 &&
            a.d_expert_bytes % 16 == 0 && al(a.down) && (!a.sh_down || (a.sh_row_bytes == DQ6_RB && al(a.sh_down)));
 }
 
@@ -1496,17 +1399,11 @@ static mx_status launch_dn_slots_dt(const DecodeDownArgs &a, hipStream_t s) {
         if (dn_q6_ok(a)) {
             const int slots = a.top_k + (a.sh_down ? 1 : 0);
             const dim3 grid((unsigned)(a.hidden / RW_DN), (unsigned)a.t);
-            if (MX_DQ6_RING)
-            {
-                if (a.t == 1)
-                    hipLaunchKernelGGL(k_decode_down_q6r<DMA_NT>, grid, dim3(64 * slots), 0, s, a,
-                                       Geo<kQ6_K>(DQ6_FF, DN_FULL));
-                else
-                    hipLaunchKernelGGL(k_decode_down_q6r<0>, grid, dim3(64 * slots), 0, s, a, Geo<kQ6_K>(DQ6_FF, DN_FULL));
-            }
-            else
-                hipLaunchKernelGGL(k_decode_down_q6, grid, dim3(64 * slots), (size_t)slots * DQ6_NI * 1024, s, a,
+            if (a.t == 1)
+                hipLaunchKernelGGL(k_decode_down_q6r<DMA_NT>, grid, dim3(64 * slots), 0, s, a,
                                    Geo<kQ6_K>(DQ6_FF, DN_FULL));
+            else
+                hipLaunchKernelGGL(k_decode_down_q6r<0>, grid, dim3(64 * slots), 0, s, a, Geo<kQ6_K>(DQ6_FF, DN_FULL));
             return MX_OK;
         }
     }
