@@ -163,7 +163,10 @@ mx_status launch_add3(const float *a, const float *b, const float *c, int64_t n,
 // Sized for the smallest m-tile (MM_BM pairs); launch_map0 cuts m-tiles of
 // `bm` >= MM_BM pairs.
 constexpr int MM_BM = 64;
-constexpr int BK_CHUNK = 64;    // tokens per bucket chunk
+#ifndef MX_BK_CHUNK
+#define MX_BK_CHUNK 32
+#endif
+constexpr int BK_CHUNK = MX_BK_CHUNK;  // tokens per bucket chunk (C3 bucket pass: 16 / 32 / 48 / 64 / 128 tokens 32.4 / 29.8 / 32.3 / 32.0 / 44 us)
 struct MapLayout {
     int64_t tpe, off, n_tiles, dup, tiles, list, chunk;  // word offsets
     int64_t t_max, nchunks, words;

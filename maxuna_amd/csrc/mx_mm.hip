@@ -148,9 +148,10 @@ __global__ void __launch_bounds__(1024) k_bucket_scan(int t, int top_k, int n_ex
 // s_slot[e * BK_ROW + tt]: the first slot of token tt that picked expert e (0xFF:
 // none).  Each expert's thread reads its row as four 16-byte words and walks the
 // chunk's tokens from registers.
-constexpr int BK_ROW = 80;   // table row bytes: BK_CHUNK slots, padded to spread the rows over the banks
+constexpr int BK_ROW = BK_CHUNK + 16;  // table row bytes: BK_CHUNK slots, padded to spread the rows over the banks
+constexpr int BK_W = BK_CHUNK / 16;    // 16-byte words per table row
 constexpr int BK_EPT = 4;    // experts per thread (n_expert <= 1024)
-static_assert(BK_CHUNK == 64 && BK_ROW >= BK_CHUNK && BK_ROW % 16 == 0, "table row: four 16-byte words");
+static_assert(BK_CHUNK % 16 == 0 && BK_ROW % 16 == 0, "table rows: whole 16-byte words");
 __global__ void __launch_bounds__(256) k_bucket_fill(const uint32_t *__restrict__ ids, int t,
                                                      int top_k, int routed_k, int n_expert, int bm,
                                                      int32_t *__restrict__ map) {
@@ -231,9 +232,15 @@ __global__ void __launch_bounds__(256) k_bucket_fill(const uint32_t *__restrict_
         int pos = po + before[j];
         po += tot[j];
         const uint4 *row = reinterpret_cast<const uint4 *>(s_slot + e * BK_ROW);
-        const uint4 q[4] = {row[0], row[1], row[2], row[3]};
-        const uint32_t wd[16] = {q[0].x, q[0].y, q[0].z, q[0].w, q[1].x, q[1].y, q[1].z, q[1].w,
-                                 q[2].x, q[2].y, q[2].z, q[2].w, q[3].x, q[3].y, q[3].z, q[3].w};
+        uint32_t wd[4 * BK_W];
+#pragma unroll
+        for (int q = 0; q < BK_W; q++) {
+            const uint4 v = row[q];
+            wd[4 * q] = v.x;
+            wd[4 * q + 1] = v.y;
+            wd[4 * q + 2] = v.z;
+            wd[4 * q + 3] = v.w;
+        }
 #pragma unroll
         for (int tt = 0; tt < BK_CHUNK; tt++) {
             const uint32_t sl = (wd[tt >> 2] >> (8 * (tt & 3))) & 0xFFu;
