@@ -371,11 +371,13 @@ __global__ void __launch_bounds__(RF_THREADS) k_route_fused(
     uint64_t *keys = reinterpret_cast<uint64_t *>(ws);
     float *probs = reinterpret_cast<float *>(keys + (int64_t)t * n_expert);
     const int tid = threadIdx.x;
-    if (blockIdx.x >= n_expert) {
+    // expert blocks: one per (expert, group of RF_MAX_T tokens), each one register pass
+    const int n_tg = (t + RF_MAX_T - 1) / RF_MAX_T, n_eb = n_expert * n_tg;
+    if ((int)blockIdx.x >= n_eb) {
         // ---- staging blocks: quarter qi = 8 values of token qi / nq
         __shared__ float s_m[RF_TOKENS];
         const int nq = hidden / 8;
-        const int qi0 = (blockIdx.x - n_expert) * RF_THREADS;
+        const int qi0 = (blockIdx.x - n_eb) * RF_THREADS;
         const int qi = qi0 + tid;
         const int tok = qi / nq, q = qi % nq;
         const bool valid = tok < t;
@@ -413,12 +415,12 @@ __global__ void __launch_bounds__(RF_THREADS) k_route_fused(
                           xstage_gm ? xstage_gm + (int64_t)(valid ? tok : 0) * xstage_gm_stride(hidden) : nullptr);
         return;
     }
-    // ---- expert blocks: the expert's router row against every token, RF_MAX_T
-    // tokens per pass (the row stays in L1/L2 after the first pass)
-    const int e = blockIdx.x;
+    // ---- expert blocks: the expert's router row against its group of RF_MAX_T
+    // tokens (the groups of one expert read the row from L2 after the first)
+    const int e = blockIdx.x % n_expert, tg = blockIdx.x / n_expert;
     const float be = bias[e];  // issued early: needed only after the reduction
     const float *rr = router + (int64_t)e * hidden;
-    for (int t0 = 0; t0 < t; t0 += RF_MAX_T) {
+    for (int t0 = tg * RF_MAX_T; t0 < min(t, (tg + 1) * RF_MAX_T); t0 += RF_MAX_T) {
         const int tc = min(RF_MAX_T, t - t0);
         const float *xt = x + (int64_t)t0 * hidden;
         float dot[RF_MAX_T] = {}, ss[RF_MAX_T] = {};
@@ -476,7 +478,8 @@ mx_status launch_route_fused(const float *x, const float *rms_alpha, float rms_e
     if (xstage_gm && hidden % 64) return fail(MX_ERR_SHAPE, "group-major staging needs hidden %% 64 == 0");
     const int nq = t * (hidden / 8);
     const int n_stage = (xstage || x_normed) ? (nq + RF_THREADS - 1) / RF_THREADS : 0;
-    hipLaunchKernelGGL(k_route_fused, dim3((unsigned)(n_expert + n_stage)), dim3(RF_THREADS), 0, s, x, rms_alpha,
+    const int n_tg = (t + RF_MAX_T - 1) / RF_MAX_T;
+    hipLaunchKernelGGL(k_route_fused, dim3((unsigned)(n_expert * n_tg + n_stage)), dim3(RF_THREADS), 0, s, x, rms_alpha,
                        rms_eps, x_normed, router, bias, t, hidden, n_expert, reinterpret_cast<uint8_t *>(ws),
                        xstage, xstage_gm);
     MX_LAUNCH("k_route_fused");
