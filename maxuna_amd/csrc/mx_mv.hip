@@ -1352,6 +1352,118 @@ __global__ void __launch_bounds__(64 * DN_SLOTS_MAX) k_decode_down_q6r(DecodeDow
     a.out[o] = vv;
 }
 
+// Verify-block form of the compile-time Q6_K down rows (t > 4, the grid of
+// k_decode_down: one workgroup per (row tile, slot, token), DQ6V_RPW rows per
+// wave, the pair's act row staged once per workgroup): the field offsets of
+// k_decode_down_q6r, hoisted out of the row loop, and its two-buffer ring of
+// 4-row batches per wave.  Same per-row arithmetic as k_decode_down (part rows
+// bit-identical).
+constexpr int DQ6V_RPW = 64;
+#ifndef MX_DN_Q6V
+#define MX_DN_Q6V 1
+#endif
+__global__ void __launch_bounds__(64 * WAVES_DN) k_decode_down_q6v(DecodeDownArgs a, Geo<kQ6_K> geo) {
+    constexpr int DT = kQ6_K, NB = DQ6V_RPW / DQ6R_BROWS;
+    __shared__ __attribute__((aligned(16))) uint8_t ring0[WAVES_DN][DQ6R_NI * 1024];
+    __shared__ __attribute__((aligned(16))) uint8_t ring1[WAVES_DN][DQ6R_NI * 1024];
+    __shared__ __attribute__((aligned(16))) uint8_t stg[(xstage_bytes(DQ6_FF) + 15) & ~15];
+    const int slots = a.top_k + (a.sh_down ? 1 : 0);
+    int slot = blockIdx.y, tok = blockIdx.z, pe = -1;
+    if (a.perm) {  // expert-ordered pairs (as k_decode_down)
+        const int v = a.perm[blockIdx.z * slots + blockIdx.y];
+        tok = (v & 0xFFFF) / slots;
+        slot = (v & 0xFFFF) % slots;
+        pe = v >> 16;
+    }
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int sub = lane & (DQ6_P - 1), rsub = lane / DQ6_P;
+    const int r0 = (blockIdx.x * WAVES_DN + wave) * DQ6V_RPW;  // hidden % (WAVES_DN * DQ6V_RPW) == 0
+    const float *xrow = a.act + ((int64_t)tok * slots + slot) * a.ff;
+    const uint8_t *wp;
+    if (slot < a.top_k) {
+        const uint32_t id = pe >= 0 ? (uint32_t)pe : a.ids[tok * a.top_k + slot];
+        const int e = id < (uint32_t)a.n_expert ? (int)id : a.n_expert - 1;
+        wp = a.down + (int64_t)e * a.d_expert_bytes;
+    } else {
+        wp = a.sh_down;
+    }
+    wp += (int64_t)r0 * DQ6_RB;
+    uint8_t *const b0 = ring0[wave], *const b1 = ring1[wave];
+    // every lane copies every batch (spare lanes repeat the last chunk into the
+    // buffer's tail; the batch after the last repeats the last batch): no branch
+    // around a copy, so the compiler's counts stay exact
+    auto issue = [&](int bi, uint8_t *dst) {
+        const uint8_t *src = wp + min(bi, NB - 1) * (DQ6R_BROWS * DQ6_RB);
+#pragma unroll
+        for (int q = 0; q < DQ6R_NI; q++) {
+            const int ci = min(64 * q + lane, DQ6R_CH - 1);
+            dma16(src + (uint32_t)(16 * ci), dst + 1024 * q);
+        }
+        asm volatile("" ::: "memory");
+    };
+    XPre xp;
+    stage_pre(xrow, a.ff, xp);
+    // the act loads have returned before the first copies are issued (ordinary
+    // loads are not counted across LDS copies), so the copies overlap the staging
+    wait_vmcnt(0);
+#pragma unroll
+    for (int i = 0; i < XPRE; i++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) asm volatile("" : "+v"(xp.v[i][j]));
+    issue(0, b0);
+    issue(1, b1);
+    stage_post_t(xrow, a.ff, xp, stg, (int)threadIdx.x, (int)blockDim.x);
+    // a bare barrier after this wave's LDS writes: __syncthreads would also wait
+    // for the weight copies just issued
+    wait_lgkmcnt0();
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    typename Q<DT>::X xs[DQ6_NG];
+    load_xs<DT, DQ6_NG>(stg, a.ff, geo, xs);
+    uint32_t oa[DQ6_NG], ohq[DQ6_NG], osc[DQ6_NG], od[DQ6_NG], sh[DQ6_NG];
+#pragma unroll
+    for (int jg = 0; jg < DQ6_NG; jg++) {
+        const int g = sub + DQ6_P * jg, b = g >> 3, gi = g & 7, n = gi >> 2, j = gi & 3;
+        const uint32_t mis = (uint32_t)(210 * b) & 2u, ab = (uint32_t)(210 * b) - mis;
+        oa[jg] = ab + 64 * n + 8 * j;
+        ohq[jg] = ab + 128 + 32 * n + 8 * j;
+        osc[jg] = ab + 192 + 8 * n;
+        od[jg] = (uint32_t)(210 * b) + 208;
+        sh[jg] = mis << 3;
+    }
+    float *part = a.part + ((int64_t)tok * slots + slot) * a.hidden + r0;
+    auto batch = [&](int bi, uint8_t *buf) {
+        wait_vmcnt(DQ6R_NI);  // batch bi has landed (the next copy is in flight)
+        const uint8_t *rl = buf + rsub * DQ6_RB;
+        float acc[1][1];
+        float v = 0.f;
+#pragma unroll
+        for (int jg = 0; jg < DQ6_NG; jg++) {
+            typename Q<DT>::Raw r;
+            Q<DT>::ld3(rl + oa[jg], r.a);
+            Q<DT>::ld3(rl + oa[jg] + 32, r.b);
+            Q<DT>::ld3(rl + ohq[jg], r.hq);
+            Q<DT>::ld3(rl + osc[jg], r.sc);
+            r.d = ld_u16(rl + od[jg]);
+            r.sh = sh[jg];
+            v += Q<DT>::dot(r, sub + DQ6_P * jg, xs[jg]);
+        }
+        acc[0][0] = v;
+        int which;
+        bool leader;
+        reduce_tuples<1, 1>(acc, DQ6_P, sub, which, leader);
+        if (leader) part[bi * DQ6R_BROWS + rsub] = acc[0][0];
+        wait_lgkmcnt0();  // every read of the buffer returned before it is overwritten
+        issue(bi + 2, buf);
+    };
+#pragma unroll 1
+    for (int bi = 0; bi < NB; bi += 2) {
+        batch(bi, b0);
+        batch(bi + 1, b1);
+    }
+    wait_vmcnt(0);  // no copy into this workgroup's LDS outlives it
+}
+
 static bool dn_q6_ok(const DecodeDownArgs &a) {
     if (MX_DN_Q6 == 0) return false;
     auto al = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
@@ -1460,6 +1572,13 @@ mx_status launch_decode_down(int dtype, const DecodeDownArgs &a, hipStream_t s) 
         }
         MX_LAUNCH("k_decode_down_slots");
         return MX_OK;
+    }
+    if (dtype == kQ6_K && MX_DN_Q6V && dn_q6_ok(a) && a.hidden % (WAVES_DN * DQ6V_RPW) == 0) {
+        const dim3 g((unsigned)(a.hidden / (WAVES_DN * DQ6V_RPW)), grid.y, grid.z);
+        hipLaunchKernelGGL(k_decode_down_q6v, g, dim3(64 * WAVES_DN), 0, s, a, Geo<kQ6_K>(DQ6_FF, DN_FULL));
+        MX_LAUNCH("k_decode_down_q6v");
+        return launch_combine_prefill(a.part, a.w, a.residual, a.t, a.top_k, a.sh_down ? 1 : 0, a.hidden, a.out, s,
+                                      a.shared_out);
     }
     switch (dtype) {
     case kQ4_K: MX_TRY(launch_dn_dt<kQ4_K>(a, grid, s)); break;

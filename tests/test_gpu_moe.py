@@ -275,7 +275,8 @@ def test_decode_down_compiled_shape_matches_generic(dev):
     a kernel with compile-time geometry; the same weights placed 2 bytes off
     16-byte alignment (Q6_K needs 2) take the generic slot-per-wave kernel.  Both
     perform the same operations in the same order, so the outputs must be
-    bit-identical (t = 1 and 3: the slot-per-wave path)."""
+    bit-identical (t = 1 and 3: the slot-per-wave path; t = 6 and 16: the
+    per-(slot, row tile) verify path)."""
     from maxuna_amd.gguf import ExpertStack
     from maxuna_amd.moe import MoeBlock, SharedExpert
 
@@ -291,7 +292,7 @@ def test_decode_down_compiled_shape_matches_generic(dev):
     e, sh = blk.experts, blk.shared
     other = MoeBlock(blk.router, blk.exp_probs_b, e.gate, e.up, shifted(e.down), blk.cfg,
                      shared=SharedExpert(sh.gate, sh.up, shifted(sh.down)))
-    for t in (1, 3):
+    for t in (1, 3, 6, 16):
         x = dev_f32(make_x(spec, 300 + t, t))
         a = host(blk.forward(x))
         b = host(other.forward(x))
