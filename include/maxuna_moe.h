@@ -104,7 +104,10 @@ mx_status mx_mul_mv_id(const mx_expert_stack *stack, const float *x, int64_t t,
  * >= n_expert).  The gather kernels clamp an out-of-range id into range (no
  * fault, wrong expert) and the bucket pass collapses repeats (mm_id.metal:
  * 243-251), so callers that take ids from outside the router check them here.
- * Ids produced by mx_route_from_logits / mx_moe_forward are always valid. */
+ * Ids produced by mx_route_from_logits / mx_moe_forward are always valid.
+ * Cost: one 1024-thread workgroup walks every token (top_k^2 / 2 compares
+ * each), so its time grows linearly with t on a single CU -- a validation
+ * step for ids from outside the router, not for a serving loop's hot path. */
 mx_status mx_check_ids(const uint32_t *ids, int64_t t, int64_t top_k, int64_t n_expert,
                        uint32_t *flags, mx_stream_t stream);
 
@@ -250,39 +253,6 @@ size_t mx_moe_forward_noalloc_max_bytes(void);
 mx_status mx_moe_forward_noalloc(const mx_moe_layer *layer, const float *x, int64_t t,
                                  const float *residual, float *out, uint32_t *ids_out, float *w_out,
                                  mx_stream_t stream);
-
-/* Same as mx_moe_forward, and additionally records a HIP event after each
- * stage on `stream`, waits for the last one and returns the stage durations
- * in milliseconds.  Decode (t < mm_min_seq): router (fused router: logits,
- * sort keys and activation staging; else logits + top-k), top-k (fused router:
- * k_decode_select, and for a verify block the expert-ordered pair list; empty
- * otherwise, and at t = 1 when the 64-group gate/up kernel runs the top-k in its
- * own blocks), routed + shared gate/up + SwiGLU, down + combine.
- * Grouped path: route, map0, x -> f16, then per bucket map gate/up GEMM +
- * SwiGLU, act -> f16, down GEMM (one map when the shared expert has the
- * routed quant types, else a second map for it), then combine.  For profiling
- * and the benchmark; no reference counterpart.  Not capturable. */
-mx_status mx_moe_forward_profiled(const mx_moe_layer *layer, const float *x, int64_t t,
-                                  const float *residual, float *out, uint32_t *ids_out,
-                                  float *w_out, void *workspace, size_t workspace_bytes,
-                                  mx_stream_t stream, float *stage_ms, int32_t max_stages,
-                                  int32_t *n_stages);
-
-/* Same as mx_moe_forward, with the kernels of decode stage `stage` (0 router
- * logits + staging, 1 top-k (nothing at t = 1 when gate/up selects in its own
- * blocks), 2 routed + shared gate/up, 3 down + combine; the
- * fused-router decode path, t < mm_min_seq <= 32) launched `times` times (0..16).  times = 0 skips
- * the stage: the later stages then read what the workspace holds from the
- * previous forward of the same layer (valid inputs, stale results) -- a graph
- * of layers with one stage skipped, subtracted from the full graph, gives that
- * stage's time inside the replayed pipeline.  Every stage recomputes its
- * outputs from its inputs, so times > 1 leaves the result unchanged; `residual`
- * must not alias `out` then.  Capturable.  For profiling and the benchmark; no
- * reference counterpart. */
-mx_status mx_moe_forward_repeat(const mx_moe_layer *layer, const float *x, int64_t t,
-                                const float *residual, float *out, uint32_t *ids_out, float *w_out,
-                                void *workspace, size_t workspace_bytes, mx_stream_t stream,
-                                int32_t stage, int32_t times);
 
 /* ---- GGUF ingestion --------------------------------------------------------------
  * A GGUF v2/v3 file: header, typed metadata, tensor table and data section

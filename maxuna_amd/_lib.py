@@ -111,8 +111,6 @@ SIGNATURES = {
     "mx_moe_forward": (I32, [C.POINTER(MoeLayerC), P, I64, P, P, P, P, P, SZ, P]),
     "mx_moe_forward_noalloc": (I32, [C.POINTER(MoeLayerC), P, I64, P, P, P, P, P]),
     "mx_moe_forward_noalloc_max_bytes": (SZ, []),
-    "mx_moe_forward_profiled": (I32, [C.POINTER(MoeLayerC), P, I64, P, P, P, P, P, SZ, P, P, I32, P]),
-    "mx_moe_forward_repeat": (I32, [C.POINTER(MoeLayerC), P, I64, P, P, P, P, P, SZ, P, I32, I32]),
     "mx_tensor_key": (U64, [U64, U32, U32]),
     "mx_gguf_open": (I32, [C.c_char_p, C.POINTER(P)]),
     "mx_gguf_close": (None, [P]),
@@ -132,6 +130,13 @@ SIGNATURES = {
     "mx_synth_blocks": (I32, [I32, U64, P, I64, P]),
 }
 
+# bench-only instrumentation (maxuna_amd/csrc/mx_instrument.h): exported by the
+# library, not part of the boundary header
+INSTRUMENT_SIGNATURES = {
+    "mx_moe_forward_profiled": (I32, [C.POINTER(MoeLayerC), P, I64, P, P, P, P, P, SZ, P, P, I32, P]),
+    "mx_moe_forward_repeat": (I32, [C.POINTER(MoeLayerC), P, I64, P, P, P, P, P, SZ, P, I32, I32]),
+}
+
 _lib = None
 
 
@@ -144,7 +149,7 @@ def lib() -> C.CDLL:
                 f"{LIB_PATH} is missing: build it with `python -m maxuna_amd.build` "
                 "(maxuna_amd has no non-native fallback)")
         handle = C.CDLL(os.fspath(LIB_PATH))
-        for name, (res, args) in SIGNATURES.items():
+        for name, (res, args) in {**SIGNATURES, **INSTRUMENT_SIGNATURES}.items():
             fn = getattr(handle, name)
             fn.restype = res
             fn.argtypes = args

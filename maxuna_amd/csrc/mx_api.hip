@@ -8,6 +8,7 @@
 
 #include "mx_launch.h"
 #include "mx_stage.h"
+#include "mx_instrument.h"
 
 // bytes of the device-resident workspace of mx_moe_forward_noalloc (per device)
 #ifndef MX_NOALLOC_SCRATCH_BYTES

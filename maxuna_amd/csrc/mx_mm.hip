@@ -146,7 +146,7 @@ __global__ void __launch_bounds__(1024) k_bucket_scan(int t, int top_k, int n_ex
 // the count and fill passes; block 0 also writes the header (counts, offsets,
 // tile list, flags), as k_bucket_scan does.
 // s_slot[e * BK_ROW + tt]: the first slot of token tt that picked expert e (0xFF:
-// none).  Each expert's thread reads its row as four 16-byte words and walks the
+// none).  Each expert's thread reads its row as BK_W 16-byte words and walks the
 // chunk's tokens from registers.
 constexpr int BK_ROW = BK_CHUNK + 16;  // table row bytes: BK_CHUNK slots, padded to spread the rows over the banks
 constexpr int BK_W = BK_CHUNK / 16;    // 16-byte words per table row

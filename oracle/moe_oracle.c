@@ -331,13 +331,34 @@ static float *deq_matrix(int dtype, const uint8_t *blocks, int64_t rows, int64_t
 
 /* y[m,n] = a[m,k] . W[n,k]^T, f64 accumulation rounded to f32 */
 static void matmul_nt(const float *a, const float *wt, int64_t m, int64_t n, int64_t k, float *y) {
-    #pragma omp parallel for schedule(static)
-    for (int64_t i = 0; i < m * n; i++) {
-        const int64_t r = i / n, c = i % n;
-        const float *ar = a + r * k, *wr = wt + c * k;
-        double acc = 0.0;
-        for (int64_t j = 0; j < k; j++) acc += (double)ar[j] * (double)wr[j];
-        y[i] = (float)acc;
+    /* y[r, c] = sum_j a[r, j] * wt[c, j], each output summed in j order in
+     * double and rounded once.  Four rows share every weight load (the order of
+     * each output's sum is unchanged), so large m runs at several GFLOP/s. */
+    #pragma omp parallel for schedule(dynamic, 16)
+    for (int64_t c = 0; c < n; c++) {
+        const float *wr = wt + c * k;
+        int64_t r = 0;
+        for (; r + 4 <= m; r += 4) {
+            const float *a0 = a + r * k, *a1 = a0 + k, *a2 = a1 + k, *a3 = a2 + k;
+            double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
+            for (int64_t j = 0; j < k; j++) {
+                const double wj = (double)wr[j];
+                s0 += (double)a0[j] * wj;
+                s1 += (double)a1[j] * wj;
+                s2 += (double)a2[j] * wj;
+                s3 += (double)a3[j] * wj;
+            }
+            y[r * n + c] = (float)s0;
+            y[(r + 1) * n + c] = (float)s1;
+            y[(r + 2) * n + c] = (float)s2;
+            y[(r + 3) * n + c] = (float)s3;
+        }
+        for (; r < m; r++) {
+            const float *ar = a + r * k;
+            double acc = 0.0;
+            for (int64_t j = 0; j < k; j++) acc += (double)ar[j] * (double)wr[j];
+            y[r * n + c] = (float)acc;
+        }
     }
 }
 

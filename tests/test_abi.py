@@ -11,12 +11,14 @@ import pytest
 from maxuna_amd import _lib
 from maxuna_amd._lib import ExpertStackC, Map0C, MoeLayerC
 
-HEADER = Path(__file__).resolve().parent.parent / "include" / "maxuna_moe.h"
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "maxuna_moe.h"
+INSTRUMENT = ROOT / "maxuna_amd" / "csrc" / "mx_instrument.h"
 FAKE = 0x10000  # an aligned address no test ever lets reach a launch
 
 
-def declared_symbols():
-    text = HEADER.read_text()
+def declared_symbols(path=HEADER):
+    text = path.read_text()
     return sorted(set(re.findall(r"^\w[\w\s\*]*?\b(mx_\w+)\(", text, re.M)))
 
 
@@ -27,6 +29,17 @@ def test_library_exports_every_declared_symbol():
     for s in syms:
         assert hasattr(L, s), s
     assert set(syms) == set(_lib.SIGNATURES), set(syms) ^ set(_lib.SIGNATURES)
+
+
+def test_instrumentation_stays_outside_the_boundary_header():
+    """The bench-only hooks are exported but declared only in the internal
+    instrumentation header, never in the boundary header."""
+    L = _lib.lib()
+    inst = declared_symbols(INSTRUMENT)
+    assert set(inst) == set(_lib.INSTRUMENT_SIGNATURES), inst
+    assert not set(inst) & set(declared_symbols())
+    for s in inst:
+        assert hasattr(L, s), s
 
 
 def test_block_geometry():

@@ -3,6 +3,8 @@ device-resident scratch) against mx_moe_forward with a caller workspace: same
 kernels, so outputs, ids and weights must be identical bit for bit, on two
 calls in a row (the second with fewer tokens, so it reads scratch the first
 left behind), with and without an in-place residual."""
+import ctypes as C
+
 import numpy as np
 import pytest
 import torch
@@ -13,6 +15,7 @@ from maxuna_amd.synth import CONFIGS, build_layer, make_x
 from tests.gpu_util import dev_f32, host
 
 pytestmark = pytest.mark.gpu
+MX_ERR_SCRATCH = 6
 
 
 def test_noalloc_forward_matches_workspace_forward(dev):
@@ -41,3 +44,36 @@ def test_noalloc_rejects_oversized_t(dev):
     x = dev_f32(make_x(spec, 600, 512))
     with pytest.raises(ops.MaxunaError, match="no-alloc forward: t = 512 needs"):
         layer.block.forward_noalloc(x)
+
+
+def _largest_fitting_t(blk, cap):
+    t = 1
+    while lib().mx_moe_workspace_bytes(C.byref(blk._c), t + 1) <= cap:
+        t += 1
+    return t
+
+
+def test_noalloc_grouped_path_and_limit(dev):
+    """The grouped-GEMM path (t >= mm_min_seq) from the static scratch: the
+    largest t whose workspace fits the 16 MiB scratch (57 for the C1 shape, as
+    the header states) runs bit-identical to the workspace forward, and t + 1 is
+    rejected with MX_ERR_SCRATCH before any launch."""
+    spec = CONFIGS["C2"]["spec"]
+    layer = build_layer(spec, seed=1307)
+    blk = layer.block
+    cap = lib().mx_moe_forward_noalloc_max_bytes()
+    t_max = _largest_fitting_t(blk, cap)
+    assert t_max == 57, t_max
+    assert t_max >= ops.mm_id_min_seq()  # the grouped path runs from the scratch
+    for t in (ops.mm_id_min_seq(), t_max):
+        print(f"no-alloc grouped t={t}", flush=True)
+        x = dev_f32(make_x(spec, 900 + t, t))
+        want, wid, ww = blk.forward(x, return_routing=True)
+        got, gid, gw = blk.forward_noalloc(x, return_routing=True)
+        assert np.array_equal(host(got).view(np.uint32), host(want).view(np.uint32)), f"t={t}: out"
+        assert np.array_equal(host(gid), host(wid)), f"t={t}: ids"
+        assert np.array_equal(host(gw).view(np.uint32), host(ww).view(np.uint32)), f"t={t}: w"
+    x = dev_f32(make_x(spec, 999, t_max + 1))
+    with pytest.raises(ops.MaxunaError) as ei:
+        blk.forward_noalloc(x)
+    assert ei.value.code == MX_ERR_SCRATCH, ei.value
