@@ -83,17 +83,22 @@ __device__ __forceinline__ half8_t pack8(const float (&f)[8]) {
     return h;
 }
 
-// Packed-f16 dequantisation.  Bytes b < 1024 of two dwords become
-// the f16 numbers 1024 + b by placing them under the exponent byte 0x64
-// (v_perm_b32); the rest is v_pk_*_f16 arithmetic on small integers, exact
-// except where noted:
-//   K-quants with min (Q4_K, Q5_K): t = fma(1024 + q, sc, -1024 sc) = sc * q
-//     (exact: |sc * q| <= 63 * 31), y = fl16(fma(t, d, -fl16(dmin * m)))
-//   Q6_K: t = ((1024 + q) - 1056) * sc = sc * (q - 32) (exact while <= 2048 in
-//     magnitude), y = fl16(t * d)
-// d and dmin are the blocks' own f16 values, so against the f32 form (one f16
-// rounding of the f32 value) only fl16(dmin * m) adds an error.  About 1.5
-// VALU per weight instead of 3.
+// Dequantisation into the MFMA B operand: every weight is the f16 rounding of
+// the reference's f32 dequantised value (mm_id.metal:75-167), rounded once.
+// Bytes b < 1024 of two dwords become the f16 numbers 1024 + b by placing them
+// under the exponent byte 0x64 (v_perm_b32); each weight is then one
+// v_fma_mix{lo,hi}_f16, an f32 fma of that f16 input with f32 scale factors,
+// rounded to f16 once:
+//   K-quants with min (Q4_K, Q5_K): y = fma(1024 + q, d1, c), d1 = d * sc and
+//     c = -dmin * m - 1024 * d1 in f32.  Against the reference's
+//     fl(d1 * q) - fl(dmin * m) the f32 value differs by at most ~2^-13 * d1
+//     (the 1024 offset's f32 roundings), far below the f16 rounding that follows
+//     (|y| ~ 8 * d1, half an f16 ulp ~2^-9 * d1)
+//   Q6_K: y = fma(q - 32, d1, 0) with q - 32 exact in f16 and d1 = d * sc exact in
+//     f32: exactly the reference's f32 value fl(d1 * (q - 32)), then rounded to f16
+// One f16 rounding per weight (the packed-f16 form this replaces rounded twice:
+// fl16(dmin * m), and sc * (q - 32) beyond 2048), at the same VALU count: per
+// two weights one perm (shared), one pk_add (Q6_K) and two mix ops.
 __device__ __forceinline__ half2_t pk_bytes(uint32_t w, uint32_t sel) {
     return __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, w, sel));
 }
@@ -102,6 +107,13 @@ __device__ __forceinline__ void pk_bytes8(uint32_t w0, uint32_t w1, half2_t (&x)
     x[1] = pk_bytes(w0, 0x04030402u);  // bytes 2, 3
     x[2] = pk_bytes(w1, 0x04010400u);
     x[3] = pk_bytes(w1, 0x04030402u);
+}
+// (f16 fma(x.lo, a, c), f16 fma(x.hi, a, c)), each an f32 fma rounded to f16 once
+// (v_fma_mixlo_f16 / v_fma_mixhi_f16)
+__device__ __forceinline__ half2_t mix2(half2_t x, float a, float c) {
+    const _Float16 lo = (_Float16)__builtin_fmaf((float)x[0], a, c);
+    const _Float16 hi = (_Float16)__builtin_fmaf((float)x[1], a, c);
+    return half2_t{lo, hi};
 }
 __device__ __forceinline__ half8_t pk_join(const half2_t (&y)[4]) {
     half8_t r;
@@ -112,30 +124,22 @@ __device__ __forceinline__ half8_t pk_join(const half2_t (&y)[4]) {
     }
     return r;
 }
-// sc2 = (sc, sc), d2 = (d, d), nm2 = -fl16(dmin * m) twice
-__device__ __forceinline__ half8_t dq8_kmin(uint32_t w0, uint32_t w1, half2_t sc2, half2_t d2, half2_t nm2) {
-    half2_t x[4], y[4];
-    pk_bytes8(w0, w1, x);
-    const half2_t nb = sc2 * half2_t{(_Float16)-1024.0f, (_Float16)-1024.0f};  // exact
-#pragma unroll
-    for (int i = 0; i < 4; i++) y[i] = __builtin_elementwise_fma(__builtin_elementwise_fma(x[i], sc2, nb), d2, nm2);
-    return pk_join(y);
-}
-__device__ __forceinline__ half8_t dq8_q6(uint32_t w0, uint32_t w1, half2_t sc2, half2_t d2) {
+// d1 = d * sc, c = -dmin * m - 1024 * d1 (f32)
+__device__ __forceinline__ half8_t dq8_kmin(uint32_t w0, uint32_t w1, float d1, float c) {
     half2_t x[4], y[4];
     pk_bytes8(w0, w1, x);
 #pragma unroll
-    for (int i = 0; i < 4; i++) y[i] = ((x[i] + half2_t{(_Float16)-1056.0f, (_Float16)-1056.0f}) * sc2) * d2;
+    for (int i = 0; i < 4; i++) y[i] = mix2(x[i], d1, c);
     return pk_join(y);
 }
-__device__ __forceinline__ half2_t h2splat(float v) {
-    const _Float16 h = (_Float16)v;
-    return half2_t{h, h};
+// d1 = d * sc (f32, exact)
+__device__ __forceinline__ half8_t dq8_q6(uint32_t w0, uint32_t w1, float d1) {
+    half2_t x[4], y[4];
+    pk_bytes8(w0, w1, x);
+#pragma unroll
+    for (int i = 0; i < 4; i++) y[i] = mix2(x[i] + half2_t{(_Float16)-1056.0f, (_Float16)-1056.0f}, d1, 0.0f);
+    return pk_join(y);
 }
-__device__ __forceinline__ half2_t h2bits(uint32_t bits16) {
-    return __builtin_bit_cast(half2_t, (bits16 & 0xFFFFu) * 0x10001u);
-}
-
 // ---- per-type weight staging: LDS slots filled by DMA, lane registers read from them -----
 // Every stage, the workgroup copies the raw bytes of its weight rows for that
 // stage into LDS with buffer->LDS DMA (16-byte chunks, consecutive lanes take
@@ -174,16 +178,16 @@ template <> struct WB<kQ4_K> {
         q[0] = *reinterpret_cast<const uint4 *>(slot + 16 + 16 * kh);
         q[1] = *reinterpret_cast<const uint4 *>(slot + 48 + 16 * kh);
     }
-    half2_t scm[4], d2;  // (sc, -fl16(dmin * m)) of each sub-block, packed
+    float d1[4], c1[4];  // d * sc and -dmin * m - 1024 * d * sc of each sub-block
     template <int PAR> __device__ __forceinline__ void prep(int kh) {
         (void)kh;
-        const float dmin = h2f((uint16_t)(h.x >> 16));
-        d2 = h2bits(h.x);
+        const float d = h2f((uint16_t)(h.x & 0xFFFFu)), dmin = h2f((uint16_t)(h.x >> 16));
 #pragma unroll
         for (int p = 0; p < 4; p++) {
             uint32_t sc, mn;
             q4k_scale_min(4 * PAR + p, h.y, h.z, h.w, sc, mn);
-            scm[p] = half2_t{(_Float16)(float)sc, (_Float16)(-(dmin * (float)mn))};
+            d1[p] = d * (float)sc;
+            c1[p] = __builtin_fmaf(-1024.0f, d1[p], -(dmin * (float)mn));
         }
     }
     __device__ __forceinline__ half8_t step(int p, int hh) const {
@@ -191,7 +195,7 @@ template <> struct WB<kQ4_K> {
         const int sh = 4 * (p & 1);
         const uint32_t w0 = ((hh ? v.z : v.x) >> sh) & 0x0F0F0F0Fu;
         const uint32_t w1 = ((hh ? v.w : v.y) >> sh) & 0x0F0F0F0Fu;
-        return dq8_kmin(w0, w1, half2_t{scm[p][0], scm[p][0]}, d2, half2_t{scm[p][1], scm[p][1]});
+        return dq8_kmin(w0, w1, d1[p], c1[p]);
     }
 };
 
@@ -210,17 +214,17 @@ template <> struct WB<kQ5_K> {
         q[0] = *reinterpret_cast<const uint4 *>(slot + 48 + 16 * kh);
         q[1] = *reinterpret_cast<const uint4 *>(slot + 80 + 16 * kh);
     }
-    half2_t scm[4], d2;
+    float d1[4], c1[4];
     int hsh;
     template <int PAR> __device__ __forceinline__ void prep(int kh) {
         (void)kh;
-        const float dmin = h2f((uint16_t)(h.x >> 16));
-        d2 = h2bits(h.x);
+        const float d = h2f((uint16_t)(h.x & 0xFFFFu)), dmin = h2f((uint16_t)(h.x >> 16));
 #pragma unroll
         for (int p = 0; p < 4; p++) {
             uint32_t sc, mn;
             q4k_scale_min(4 * PAR + p, h.y, h.z, h.w, sc, mn);
-            scm[p] = half2_t{(_Float16)(float)sc, (_Float16)(-(dmin * (float)mn))};
+            d1[p] = d * (float)sc;
+            c1[p] = __builtin_fmaf(-1024.0f, d1[p], -(dmin * (float)mn));
         }
         hsh = 4 * PAR;
     }
@@ -230,7 +234,7 @@ template <> struct WB<kQ5_K> {
         const uint32_t hb = hsh + p;
         const uint32_t w0 = (((hh ? v.z : v.x) >> sh) & 0x0F0F0F0Fu) | ((((hh ? qh.z : qh.x) >> hb) & 0x01010101u) << 4);
         const uint32_t w1 = (((hh ? v.w : v.y) >> sh) & 0x0F0F0F0Fu) | ((((hh ? qh.w : qh.y) >> hb) & 0x01010101u) << 4);
-        return dq8_kmin(w0, w1, half2_t{scm[p][0], scm[p][0]}, d2, half2_t{scm[p][1], scm[p][1]});
+        return dq8_kmin(w0, w1, d1[p], c1[p]);
     }
 };
 
@@ -273,15 +277,15 @@ template <> struct WB<kQ6_K> {
         s1 = __builtin_amdgcn_alignbit(a2, a1, sh);
         dbits = *reinterpret_cast<const uint16_t *>(slot + 128 + m1 + 16);
     }
-    half2_t sc2[4], d2;
+    float d1[4];  // d * sc, exact in f32
     template <int PAR> __device__ __forceinline__ void prep(int kh) {
-        d2 = h2bits(dbits);
+        const float d = h2f(dbits);
 #pragma unroll
         for (int p = 0; p < 4; p++) {
             const int j = 2 * p + kh;  // byte j of the stage's 8 scales
             const uint32_t word = j < 4 ? s0 : s1;
             const int8_t s8 = (int8_t)((word >> (8 * (j & 3))) & 0xFFu);
-            sc2[p] = h2splat((float)s8);
+            d1[p] = d * (float)s8;
         }
     }
     __device__ __forceinline__ half8_t step(int p, int hh) const {
@@ -291,7 +295,7 @@ template <> struct WB<kQ6_K> {
         const uint32_t a1 = ((hh ? ql.w : ql.y) >> shl) & 0x0F0F0F0Fu;
         const uint32_t b0 = (((hh ? qh.z : qh.x) >> shh) & 0x03030303u) << 4;
         const uint32_t b1 = (((hh ? qh.w : qh.y) >> shh) & 0x03030303u) << 4;
-        return dq8_q6(a0 | b0, a1 | b1, sc2[p], d2);
+        return dq8_q6(a0 | b0, a1 | b1, d1[p]);
     }
 };
 

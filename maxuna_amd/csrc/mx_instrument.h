@@ -2,7 +2,7 @@
  * maxuna_moe instrumentation -- bench-only entry points of libmaxuna_moe.so.
  *
  * These are NOT part of the drop-in boundary (include/maxuna_moe.h): the
- * reference's MoE interface (src/moe.rs:19-21, src/ops/*.rs) has no
+ * reference's MoE interface (src/moe.rs:19-21, src/ops/ files) has no
  * counterpart, and a host binding for the reference never calls them.  They
  * exist so bench.py can time the decode stages inside a replayed graph and
  * read per-stage event times.  mx_moe_forward_repeat with times != 1 gives
