@@ -42,6 +42,9 @@
 
 namespace mx {
 
+// product of two values that fit 24-bit signed integers (v_mul_i32_i24)
+__device__ __forceinline__ int mul24(int a, int b) { return ((a << 8) >> 8) * ((b << 8) >> 8); }
+
 __device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }
@@ -221,10 +224,16 @@ template <> struct Q<kQ6_K> {
         r.d = ld_u16(blk + 208);
         return r;
     }
+    // The lane group's four parts (positions 128n + 32p + 8j of a block) lie in
+    // one 128-value staging block (Q6_K rows have k % 256 == 0, so they are
+    // always staged with one scale per 128 values, mx_stage.h) and share its scale
+    // x.s[0].  The accumulators start at -32 * (digit sums), so each part's plane
+    // sums are sum (q - 32) * digit, exact; the parts' sums are weighted by their
+    // int8 scales in integer arithmetic (|sc * sum| <= 128 * 32768 per part, at
+    // most 2^24 over the four: exact in f32), and the three planes are
+    // recombined in f32 (two roundings) and scaled once per group.
     __device__ static float dot(const Raw &r, int g, const X &x) {
         const int jh = ((g & 7) & 3) >> 1;  // scale byte is scales[8n + jh + 2p]
-        // the accumulators start at -32 * (digit sums): the plane sums are then
-        // sum (q - 32) * digit, exact
         int hacc[4] = {x.nh[0], x.nh[1], x.nh[2], x.nh[3]}, macc[4] = {0, 0, 0, 0},
             lacc[4] = {x.nml[0], x.nml[1], x.nml[2], x.nml[3]};
         auto fun = [&](const uint32_t (&d)[3], int w) { return __builtin_amdgcn_alignbit(d[w + 1], d[w], r.sh); };
@@ -245,15 +254,16 @@ template <> struct Q<kQ6_K> {
                 lacc[p] = dot4(qp[p], x.l[2 * p + w], lacc[p]);
             }
         }
-        float tot = 0.f;
+        int Hs = 0, Ms = 0, Ls = 0;
 #pragma unroll
         for (int p = 0; p < 4; p++) {
-            const uint32_t src = SC[p >> 1];
-            const int sc = (int)(int8_t)((src >> (8 * (jh + 2 * (p & 1)))) & 0xFFu);
-            // 256 * macc + lacc in int32: |macc| <= 63 * 128 * 8, |lacc| < 2^24
-            tot = __builtin_fmaf((float)sc * x.s[p], planes(hacc[p], macc[p], lacc[p]), tot);
+            const int sc = __builtin_amdgcn_sbfe((int)SC[p >> 1], 8 * (jh + 2 * (p & 1)), 8);
+            Hs += mul24(sc, hacc[p]);
+            Ms += mul24(sc, macc[p]);
+            Ls += mul24(sc, lacc[p]);
         }
-        return h2f((uint16_t)r.d) * tot;
+        const float v = __builtin_fmaf((float)Hs, 65536.0f, __builtin_fmaf((float)Ms, 256.0f, (float)Ls));
+        return h2f((uint16_t)r.d) * (x.s[0] * v);
     }
 };
 
@@ -692,6 +702,158 @@ static mx_status launch_mv_dt(const MvArgs &a, dim3 grid, hipStream_t s) {
     return MX_OK;
 }
 
+// ---- compile-time Q6_K mat-vec (plain mul_mv and mul_mv_id, e.g. the lm_head) ----------
+// Q6_K rows of K = 32 * P * NG weights: P lanes per row, NG 32-weight groups per
+// lane, RPI = 64 / P rows per batch.  The geometry of k_mul_mv_id, with every
+// count compile-time: the row bytes, the batch's copy instructions (so every
+// vmcnt wait is an immediate, no runtime wait table), the lanes' field offsets
+// and 2-byte block phases (rows are 4-byte aligned: 210 * K / 256 is a multiple
+// of 4), hoisted out of the row loop as in k_decode_down_q6r.  Each wave walks
+// MVQ6_RPW rows of one (token, slot) pair in batches through two LDS buffers of
+// its own (batch b + 1 in flight while b is contracted); the workgroup stages the
+// pair's activation row once.  Same per-row arithmetic and 32-lane sum as
+// k_mul_mv_id (Q<kQ6_K>::dot, reduce_tuples).
+#ifndef MX_MV_Q6
+#define MX_MV_Q6 1
+#endif
+#ifndef MX_MVQ6_RPW
+#define MX_MVQ6_RPW 16
+#endif
+constexpr int MVQ6_RPW = MX_MVQ6_RPW;  // rows per wave
+
+template <int NG, int P> struct MvQ6 {
+    static constexpr int K = 32 * P * NG, RB = K / 256 * 210, RPI = 64 / P;
+    static constexpr int BCH = RPI * RB / 16, NI = (BCH + 63) / 64, NB = MVQ6_RPW / RPI;
+    static_assert((RPI * RB) % 16 == 0 && RB % 4 == 0, "batches start 16-byte aligned, rows 4-byte aligned");
+    static_assert(MVQ6_RPW % RPI == 0 && NB % 2 == 0, "whole batch pairs per wave");
+};
+template <int NG, int P>
+__global__ void __launch_bounds__(64 * WAVES) k_mv_q6(MvArgs a) {
+    using G = MvQ6<NG, P>;
+    constexpr int DT = kQ6_K, RB = G::RB, RPI = G::RPI, NI = G::NI, BCH = G::BCH, NB = G::NB;
+    __shared__ __attribute__((aligned(16))) uint8_t ring0[WAVES][NI * 1024];
+    __shared__ __attribute__((aligned(16))) uint8_t ring1[WAVES][NI * 1024];
+    __shared__ __attribute__((aligned(16))) uint8_t stg[(xstage_bytes(G::K) + 15) & ~15];
+    const int pair = blockIdx.y;  // token * top_k + slot
+    const int tok = pair / a.top_k, slot = pair % a.top_k;
+    int e = 0;
+    if (a.ids) {
+        const uint32_t id = a.ids[pair];
+        e = id < (uint32_t)a.n_expert ? (int)id : a.n_expert - 1;
+    }
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int sub = lane & (P - 1), rsub = lane / P;
+    const int r0 = (blockIdx.x * WAVES + wave) * MVQ6_RPW;
+    // the last batch that holds a row of this matrix (a wave past the end re-copies it)
+    const int nbv = r0 < a.n_out ? (min(a.n_out - r0, MVQ6_RPW) + RPI - 1) / RPI : 1;
+    const int rlast = r0 < a.n_out ? r0 : ((a.n_out - 1) / RPI) * RPI;
+    const float *xrow = a.x + ((int64_t)tok * a.x_per_row + (a.x_per_row == 1 ? 0 : slot)) * a.k;
+    const uint8_t *wp = a.w + (int64_t)e * a.expert_bytes + (int64_t)rlast * RB;
+    uint8_t *const b0 = ring0[wave], *const b1 = ring1[wave];
+    // every lane issues every copy (spare lanes repeat the batch's last chunk into
+    // the buffer's unused tail): no branch around a copy, so the counts stay exact
+    auto issue = [&](int bi, uint8_t *dst) {
+        const uint8_t *src = wp + min(bi, nbv - 1) * (RPI * RB);
+#pragma unroll
+        for (int q = 0; q < NI; q++) {
+            const int ci = min(64 * q + lane, BCH - 1);
+            dma16(src + (uint32_t)(16 * ci), dst + 1024 * q);
+        }
+        asm volatile("" ::: "memory");
+    };
+    XPre xp;
+    stage_pre(xrow, G::K, xp);
+    // the activation loads have returned before the first copies are issued
+    // (ordinary loads are not counted across LDS copies)
+    wait_vmcnt(0);
+#pragma unroll
+    for (int i = 0; i < XPRE; i++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) asm volatile("" : "+v"(xp.v[i][j]));
+    issue(0, b0);
+    issue(1, b1);
+    stage_post_t(xrow, G::K, xp, stg, (int)threadIdx.x, (int)blockDim.x);
+    wait_lgkmcnt0();
+    __builtin_amdgcn_s_barrier();  // (a bare barrier: __syncthreads would wait for the copies)
+    asm volatile("" ::: "memory");
+    typename Q<DT>::X xs[NG];
+    {
+        const XView xv(stg, G::K);
+#pragma unroll
+        for (int jg = 0; jg < NG; jg++) Q<DT>::load_x(xv, sub + P * jg, xs[jg]);
+    }
+    uint32_t oa[NG], ohq[NG], osc[NG], od[NG], sh[NG];
+#pragma unroll
+    for (int jg = 0; jg < NG; jg++) {
+        const int g = sub + P * jg, b = g >> 3, gi = g & 7, n = gi >> 2, j = gi & 3;
+        const uint32_t mis = (uint32_t)(210 * b) & 2u, ab = (uint32_t)(210 * b) - mis;
+        oa[jg] = ab + 64 * n + 8 * j;
+        ohq[jg] = ab + 128 + 32 * n + 8 * j;
+        osc[jg] = ab + 192 + 8 * n;
+        od[jg] = (uint32_t)(210 * b) + 208;
+        sh[jg] = mis << 3;
+    }
+    float *dst = a.dst + (int64_t)pair * a.n_out;
+    auto batch = [&](int bi, uint8_t *buf) {
+        wait_vmcnt(NI);  // batch bi has landed (bi + 1 is in flight)
+        const uint8_t *rl = buf + rsub * RB;
+        float acc[1][1];
+        float v = 0.f;
+#pragma unroll
+        for (int jg = 0; jg < NG; jg++) {
+            typename Q<DT>::Raw r;
+            Q<DT>::ld3(rl + oa[jg], r.a);
+            Q<DT>::ld3(rl + oa[jg] + 32, r.b);
+            Q<DT>::ld3(rl + ohq[jg], r.hq);
+            Q<DT>::ld3(rl + osc[jg], r.sc);
+            r.d = ld_u16(rl + od[jg]);
+            r.sh = sh[jg];
+            v += Q<DT>::dot(r, sub + P * jg, xs[jg]);
+        }
+        acc[0][0] = v;
+        int which;
+        bool leader;
+        reduce_tuples<1, 1>(acc, P, sub, which, leader);
+        const int row = r0 + bi * RPI + rsub;
+        if (leader && bi < nbv && row < a.n_out && r0 < a.n_out) dst[row] = acc[0][0];
+        wait_lgkmcnt0();  // every read of the buffer returned before it is overwritten
+        issue(bi + 2, buf);
+    };
+#pragma unroll 1
+    for (int bi = 0; bi < NB; bi += 2) {
+        batch(bi, b0);
+        batch(bi + 1, b1);
+    }
+    wait_vmcnt(0);  // no copy into this workgroup's LDS outlives it
+}
+
+// the (NG, P) variant of k_mv_q6 for this shape, or false
+static bool mv_q6_pick(const MvArgs &a, int &ng, int &p) {
+    auto al = [](const void *q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+    if (!al(a.w) || a.expert_bytes % 16 != 0 || a.row_bytes != (int64_t)a.k / 256 * 210) return false;
+    switch (a.k) {
+    case 1536: ng = 3; p = 16; break;
+    case 2048: ng = 2; p = 32; break;
+    case 3072: ng = 3; p = 32; break;
+    case 4096: ng = 4; p = 32; break;
+    default: return false;
+    }
+    // whole batches: a batch's copy never reads past the matrix's last row
+    return a.n_out % (64 / p) == 0;
+}
+static mx_status launch_mv_q6(const MvArgs &a, int ng, int p, hipStream_t s) {
+    const unsigned tiles = (unsigned)((a.n_out + WAVES * MVQ6_RPW - 1) / (WAVES * MVQ6_RPW));
+    const dim3 grid(tiles, (unsigned)(a.t * a.top_k));
+#define MX_Q6(NG, P) hipLaunchKernelGGL((k_mv_q6<NG, P>), grid, dim3(64 * WAVES), 0, s, a)
+    if (ng == 3 && p == 16) MX_Q6(3, 16);
+    else if (ng == 2) MX_Q6(2, 32);
+    else if (ng == 3) MX_Q6(3, 32);
+    else MX_Q6(4, 32);
+#undef MX_Q6
+    MX_LAUNCH("k_mv_q6");
+    return MX_OK;
+}
+
 // ---- shape fits of the LDS-ring kernels (host) --------------------------------------
 // Each kernel holds NG <= NG_MAX activation groups per lane, copies a batch of rows
 // with at most DMA_MAX_INSTS wave instructions per matrix set, and needs its LDS.
@@ -741,6 +903,8 @@ mx_status launch_mul_mv_id(int dtype, const MvArgs &a, hipStream_t s) {
                         a.ids, a.t, a.top_k, a.dst, a.top_k, 0};
         return launch_mv_f32(dtype, f, s);
     }
+    int ng = 0, p = 0;
+    if (dtype == kQ6_K && MX_MV_Q6 && mv_q6_pick(a, ng, p)) return launch_mv_q6(a, ng, p, s);
     switch (dtype) {
     case kQ4_K: MX_TRY(launch_mv_dt<kQ4_K>(a, grid, s)); break;
     case kQ5_K: MX_TRY(launch_mv_dt<kQ5_K>(a, grid, s)); break;

@@ -1,7 +1,8 @@
 // Staged activations: the integer form in which the decode kernels consume an
 // activation row (x for gate/up, the SwiGLU output for down).
 //
-// Per 32-value group g of a k-vector (k % 32 == 0), with m = max|x| over g:
+// Per scale group g of a k-vector (k % 32 == 0) -- the aligned 128-value block
+// when k % 128 == 0, else the 32-value group -- with m = max|x| over g:
 //   s_g = 2^e, e = frexp_exp(m) - 23 (+1 if m / 2^e > X24_MAX), e >= -149
 //   x24 = rint(x / s_g), an integer in [-2^23, X24_MAX]
 //   x24 = 65536 * xh + 256 * xm + xl, three signed int8 digits in [-128, 127]
@@ -15,7 +16,9 @@
 // Stored as three byte planes so four consecutive values form one dword for
 // v_dot4_i32_i8, plus the integer sum of x24 over every 32 values (the Q4_K
 // "min" term is applied from it).
-// Layout (bytes): xh[k] | xm[k] | xl[k] | s[k/32] f32 | S32[k/32] i32.
+// Layout (bytes): xh[k] | xm[k] | xl[k] | s[k/32] f32 | S32[k/32] i32 (s per
+// 32-value group; with 128-value scale groups the four entries of a block hold
+// the same scale).
 // The same layout is used in LDS (per-workgroup staging) and in global memory
 // (staged once per layer by the router kernel).
 #pragma once
@@ -77,8 +80,15 @@ __device__ __forceinline__ void x24_digits(int v, int &h, int &m, int &l) {
 // together (cross-lane max and sum); `valid` = false lanes contribute zeros.  A
 // group holding Inf or NaN gets a NaN scale, so it poisons the rows that read it,
 // as f32 arithmetic would.
+// wide (rows with k % 128 == 0, uniform over the wave): the scale is shared by
+// the 16 quarters (128 values) of an aligned block, which then sit in 16
+// consecutive lanes (16m .. 16m+15): every 32-value group of the block gets the
+// same s_g, so the grid is relative to the block's largest magnitude.  The four
+// 32-value parts a Q6_K lane group reads lie in one such block, so their integer
+// sums are scaled and added before the conversion to f32 (Q<kQ6_K>::dot).  s32
+// stays per 32-value group.
 __device__ __forceinline__ void quarter_digits(const float (&v)[8], bool valid, uint32_t (&h)[2], uint32_t (&m)[2],
-                                               uint32_t (&l)[2], float &sg, int &s32) {
+                                               uint32_t (&l)[2], float &sg, int &s32, bool wide) {
     float mx = 0.f;
     if (valid) {
 #pragma unroll
@@ -90,6 +100,10 @@ __device__ __forceinline__ void quarter_digits(const float (&v)[8], bool valid, 
     }
     mx = fmaxf(mx, lane_partner<1>(mx));
     mx = fmaxf(mx, lane_partner<2>(mx));
+    if (wide) {
+        mx = fmaxf(mx, lane_partner<4>(mx));
+        mx = fmaxf(mx, lane_partner<8>(mx));
+    }
     const bool finite = mx < __builtin_inff();
     const bool nz = finite && mx > 0.f;
     const int e = nz ? x24_exponent(mx) : 0;
@@ -120,12 +134,14 @@ __device__ __forceinline__ void quarter_digits(const float (&v)[8], bool valid, 
 // layout at `base` (and, when gm != NULL and k % 64 == 0, into the group-major
 // copy at gm), under quarter_digits' lane rules; `valid` = false lanes store
 // nothing.
+// Rows with k % 128 == 0 take one scale per 128-value block (quarter_digits'
+// wide rule: the 16 quarters of a block in 16 consecutive lanes).
 __device__ __forceinline__ void stage_quarter(const float (&v)[8], int q, bool valid, uint8_t *base, int k,
                                               uint8_t *gm = nullptr) {
     uint32_t h[2], m[2], l[2];
     float sg;
     int s32;
-    quarter_digits(v, valid, h, m, l, sg, s32);
+    quarter_digits(v, valid, h, m, l, sg, s32, k % 128 == 0);
     if (valid) {
         int8_t *xh = reinterpret_cast<int8_t *>(base);
         int8_t *xm = xh + k;
@@ -183,7 +199,7 @@ __device__ __forceinline__ void stage_pre_t(const float *__restrict__ x, int k, 
         if (q < nq) load8f(x + 8 * q, p.v[i]);
     }
 }
-// nth must be a multiple of 4 and uniform over the group; no barrier
+// nth must be a multiple of 16 and uniform over the group; no barrier
 template <int NP>
 __device__ __forceinline__ void stage_post_t(const float *__restrict__ x, int k, const XPreT<NP> &p, uint8_t *lds,
                                              int tid, int nth) {

@@ -115,6 +115,29 @@ def test_mul_mv_plain(dev, orc):
     assert_close(got, x.astype(np.float64) @ w.T, what="mul_mv")
 
 
+def test_mul_mv_q6_compiled_rows(dev, orc):
+    """Q6_K rows of k = 1536, 2048, 3072 (the lm_head width) and 4096 take the
+    compile-time mat-vec when n_out is a whole number of row batches.  Checked
+    against the oracle, and against the generic LDS-ring kernel on the same rows
+    (one more row makes n_out odd, which selects the generic kernel): bit-identical
+    where both use the same lane geometry (k = 1536, 3072)."""
+    rng = np.random.default_rng(31)
+    dt = GgmlDType.Q6_K
+    for k, n in ((3072, 1000), (1536, 500), (4096, 260), (2048, 300)):
+        _log(f"mul_mv q6 k={k} n={n}")
+        rb = k // 256 * 210
+        blk = orc.expert_blocks(int(dt), 777 + k, 0, n + 1, k)
+        x = rng.standard_normal((2, k)).astype(np.float32)
+        got = host(ops.mul_mv(torch.from_numpy(blk[: n * rb].copy()).cuda(), dt, n, k, dev_f32(x)))
+        gen = host(ops.mul_mv(torch.from_numpy(blk).cuda(), dt, n + 1, k, dev_f32(x)))[:, :n]
+        w = orc.dequantize(int(dt), blk, (n + 1) * k).reshape(n + 1, k)[:n].astype(np.float64)
+        want = x.astype(np.float64) @ w.T
+        assert_close(got, want, what=f"mul_mv q6 k={k}")
+        assert_close(gen, want, what=f"mul_mv generic k={k}")
+        if k in (1536, 3072):
+            assert np.array_equal(got.view(np.uint32), gen.view(np.uint32)), f"k={k}: compiled != generic"
+
+
 def test_route_from_logits_bit_exact(dev, orc):
     _log("route_from_logits")
     rng = np.random.default_rng(4)
