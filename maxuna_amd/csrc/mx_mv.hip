@@ -993,6 +993,10 @@ constexpr int GU64_R = MX_GU64_R;
 #define MX_GU64_TPB 8
 #endif
 constexpr int GU64_TPB = MX_GU64_TPB;
+#ifndef MX_GU64_TPB1
+#define MX_GU64_TPB1 3
+#endif
+constexpr int GU64_TPB1 = MX_GU64_TPB1;
 template <int DT> struct Row64 {
     static_assert(DT == kQ4_K || DT == kQ5_K, "64-group rows: the K-quants with 64-weight groups");
     static constexpr int RB = 16 * (DT == kQ4_K ? 144 : 176);  // row bytes (16 super-blocks)
@@ -1000,9 +1004,12 @@ template <int DT> struct Row64 {
 };
 constexpr int GU_SEL_E = 256;  // experts of the in-block top-k
 static_assert(64 * WAVES == SEL_THREADS, "the in-block top-k needs SEL_THREADS threads");
-// (the verify form, LOOP, runs at 4 waves/SIMD: C2 333 -> 324 us; t = 1 keeps 5)
-template <int DT, int R, bool LOOP>
-__global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(LOOP ? 4 : MX_GU_WPE)))
+// TPB: row-pair tiles per workgroup (tiles blockIdx.x, blockIdx.x + gridDim.x, ...
+// of its (slot, token)); WPE: waves per SIMD the registers must allow (the verify
+// form runs at 4: C2 333 -> 324 us; t = 1 at 5); AUX: the weight copies' cache
+// policy (DMA_NT at t = 1).
+template <int DT, int R, int TPB, int WPE, int AUX>
+__global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(WPE)))
 k_decode_gate_up64(DecodeGateUpArgs a, int slot0, Geo<DT> geo) {
     constexpr int RB = Row64<DT>::RB, CH = Row64<DT>::CH, NI = Row64<DT>::NI;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -1017,8 +1024,7 @@ k_decode_gate_up64(DecodeGateUpArgs a, int slot0, Geo<DT> geo) {
     }
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    // LOOP: the workgroup walks row-pair tiles blockIdx.x, blockIdx.x + gridDim.x,
-    // ... of its (slot, token), loading the activation slices and the expert once
+    // the workgroup walks its tiles loading the activation slices and the expert once
     const int rfirst = (blockIdx.x * WAVES + wave) * R;
     typename Q<DT>::X xs[1];
     if (rfirst < a.ff) load_xs_gm<DT, 1>(a.xstage_gm + (int64_t)tok * xstage_gm_stride(a.hidden), a.hidden, geo, xs);
@@ -1042,42 +1048,42 @@ k_decode_gate_up64(DecodeGateUpArgs a, int slot0, Geo<DT> geo) {
     }
     const uint8_t *const gw0 = gw, *const uw0 = uw;
     uint8_t *buf = lds + wave * (2 * RB);
-    for (int tile = blockIdx.x;; tile += gridDim.x) {
-    const int r0 = (tile * WAVES + wave) * R;
-    if (LOOP && r0 >= a.ff) break;
-    const int n = min(R, a.ff - r0);
-    gw = gw0 + (int64_t)r0 * RB;
-    uw = uw0 + (int64_t)r0 * RB;
-    if (LOOP && tile != (int)blockIdx.x) wait_lgkmcnt0();  // the last tile's reads of the buffer returned
-    // row r of matrix m (0 gate, 1 up) into the matrix's half of the buffer; every
-    // address a scalar base plus a 32-bit lane offset
-    auto issue = [&](int m, int r) {
-        const uint8_t *src = (m ? uw : gw) + r * RB;
+    // The wave's row pairs i = tt * R + r: row r of its slice of tile blockIdx.x +
+    // tt * gridDim.x.  Valid pairs form a prefix (only the matrix's last tile is
+    // partial), and the copy of pair i + 1 is issued as soon as pair i's words are
+    // in registers, across tiles too: the wave never waits for a first copy after
+    // its first pair.
+    constexpr int NR = TPB * R;
+    auto row_of = [&](int i) { return ((int)blockIdx.x + (i / R) * (int)gridDim.x) * (WAVES * R) + wave * R + i % R; };
+    // row pair i of matrix m (0 gate, 1 up) into the matrix's half of the buffer;
+    // every address a scalar base plus a 32-bit lane offset
+    auto issue = [&](int m, int i) {
+        const uint8_t *src = (m ? uw0 : gw0) + (int64_t)row_of(i) * RB;
 #pragma unroll
         for (int q = 0; q < NI; q++) {
             const int ci = 64 * q + lane;
-            if (q < NI - 1 || ci < CH) dma16<LOOP ? 0 : DMA_NT>(src + (uint32_t)(16 * ci), buf + m * RB + 1024 * q);
+            if (q < NI - 1 || ci < CH) dma16<AUX>(src + (uint32_t)(16 * ci), buf + m * RB + 1024 * q);
         }
         asm volatile("" ::: "memory");
     };
-    float res[R];
-    issue(0, 0);
+    float res[NR];
+    issue(0, 0);  // (row_of(0) < ff: checked above)
     issue(1, 0);
     // Only the copies count in vmcnt inside the loop (the act stores come after it):
-    // when row r's gate copy is waited for, at most row r's up copy is younger; when
-    // its up copy is, at most row r + 1's gate copy.
+    // when pair i's gate copy is waited for, at most pair i's up copy is younger; when
+    // its up copy is, at most pair i + 1's gate copy.
 #pragma unroll
-    for (int r = 0; r < R; r++) {
-        if (r < n) {
+    for (int i = 0; i < NR; i++) {
+        if (i == 0 || row_of(i) < a.ff) {  // wave-uniform
+            const bool more = i + 1 < NR && row_of(i + 1) < a.ff;
             float v2[2];
 #pragma unroll
             for (int m = 0; m < 2; m++) {
-                if (m == 0 || r + 1 >= n) wait_vmcnt(m == 0 ? NI : 0);
-                else wait_vmcnt(NI);
+                wait_vmcnt(m == 0 || more ? NI : 0);
                 const typename Q<DT>::Raw rw = Q<DT>::load(buf + m * RB, lane);
-                if (r + 1 < n) {
+                if (more) {
                     wait_lgkmcnt0();  // the words are in registers: the half may be overwritten
-                    issue(m, r + 1);
+                    issue(m, i + 1);
                 }
                 v2[m] = Q<DT>::dot(rw, lane, xs[0]);
             }
@@ -1091,17 +1097,13 @@ k_decode_gate_up64(DecodeGateUpArgs a, int slot0, Geo<DT> geo) {
             v += lane_partner<1>(v);
             const float G = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
             const float U = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
-            res[r] = G / (1.0f + expf(-G)) * U;
+            res[i] = G / (1.0f + expf(-G)) * U;
         }
     }
-    float *act = a.act + ((int64_t)tok * slots + slot) * a.ff + r0;
-    if (lane < n) {
+    float *act = a.act + ((int64_t)tok * slots + slot) * a.ff;
 #pragma unroll
-        for (int r = 0; r < R; r++)
-            if (r == lane) act[r] = res[r];
-    }
-    if (!LOOP) break;
-    }
+    for (int i = 0; i < NR; i++)
+        if ((i == 0 || row_of(i) < a.ff) && lane == i % R) act[row_of(i)] = res[i];
 }
 
 // The selection blocks alone (a launch with no expert slots): their own kernel,
@@ -1203,15 +1205,18 @@ static mx_status launch_gu_dt(const DecodeGateUpArgs &a, int slot0, int nslot, h
             const unsigned tiles = (unsigned)((a.ff + WAVES * GU64_R - 1) / (WAVES * GU64_R));
             // verify blocks (t > 1): GU64_TPB tiles per workgroup, the activation
             // slices and per-wave setup amortised over more rows (C2: 8 tiles
-            // 369 -> 363 us; 16 and 24 slower; t = 1 keeps one tile per workgroup)
-            const bool loop = a.t > 1 && GU64_TPB > 1;
-            const dim3 grid(loop ? (tiles + GU64_TPB - 1) / GU64_TPB : tiles, (unsigned)nslot, (unsigned)a.t);
+            // 369 -> 363 us; 16 and 24 slower); t = 1: GU64_TPB1 tiles, so the
+            // in-block top-k and the activation loads run once per workgroup
+            const bool verify = a.t > 1;
+            const int tpb = verify ? GU64_TPB : GU64_TPB1;
+            const dim3 grid((tiles + tpb - 1) / tpb, (unsigned)nslot, (unsigned)a.t);
             const size_t lds = (size_t)WAVES * 2 * Row64<DT>::RB + (a.sel_keys ? sizeof(SelSharedT<GU_SEL_E>) : 0);
-            if (loop)
-                hipLaunchKernelGGL((k_decode_gate_up64<DT, (GU64_R > 0 ? GU64_R : 1), true>), grid, dim3(64 * WAVES), lds,
-                                   s, a, slot0, Geo<DT>(a.hidden));
+            constexpr int R = GU64_R > 0 ? GU64_R : 1;
+            if (verify)
+                hipLaunchKernelGGL((k_decode_gate_up64<DT, R, GU64_TPB, 4, 0>), grid, dim3(64 * WAVES), lds, s, a, slot0,
+                                   Geo<DT>(a.hidden));
             else
-                hipLaunchKernelGGL((k_decode_gate_up64<DT, (GU64_R > 0 ? GU64_R : 1), false>), grid, dim3(64 * WAVES), lds,
+                hipLaunchKernelGGL((k_decode_gate_up64<DT, R, GU64_TPB1, MX_GU_WPE, DMA_NT>), grid, dim3(64 * WAVES), lds,
                                    s, a, slot0, Geo<DT>(a.hidden));
             return MX_OK;
         }
