@@ -65,13 +65,6 @@ __device__ __forceinline__ int x24_exponent(float m) {
     return e;
 }
 
-// Splits x24 in [-2^23, X24_MAX] into balanced base-256 digits h, m, l.
-__device__ __forceinline__ void x24_digits(int v, int &h, int &m, int &l) {
-    l = ((v + 128) & 255) - 128;
-    const int r = (v - l) >> 8;
-    m = ((r + 128) & 255) - 128;
-    h = (r - m) >> 8;
-}
 
 // The staged form of quarter-group values v (8 consecutive values of one 32-value
 // group): digit words h, m, l (4 values per word), the group scale sg and the
@@ -89,41 +82,52 @@ __device__ __forceinline__ void x24_digits(int v, int &h, int &m, int &l) {
 // stays per 32-value group.
 __device__ __forceinline__ void quarter_digits(const float (&v)[8], bool valid, uint32_t (&h)[2], uint32_t (&m)[2],
                                                uint32_t (&l)[2], float &sg, int &s32, bool wide) {
-    float mx = 0.f;
+    // max |x| as the integer order of the magnitude bits: Inf and NaN patterns
+    // are above every finite one, so a group holding either ends with a
+    // non-finite maximum (also across lanes: integer max never drops a NaN)
+    uint32_t mb = 0;
     if (valid) {
 #pragma unroll
-        for (int i = 0; i < 8; i++) mx = fmaxf(mx, fabsf(v[i]));
-        // fmaxf drops NaN: carry it explicitly
-#pragma unroll
-        for (int i = 0; i < 8; i++)
-            if (v[i] != v[i]) mx = __builtin_inff();
+        for (int i = 0; i < 8; i++) mb = max(mb, __float_as_uint(v[i]) & 0x7FFFFFFFu);
     }
-    mx = fmaxf(mx, lane_partner<1>(mx));
-    mx = fmaxf(mx, lane_partner<2>(mx));
+    auto pmax = [&](auto c) {
+        mb = max(mb, __float_as_uint(lane_partner<decltype(c)::value>(__uint_as_float(mb))));
+    };
+    pmax(std::integral_constant<int, 1>{});
+    pmax(std::integral_constant<int, 2>{});
     if (wide) {
-        mx = fmaxf(mx, lane_partner<4>(mx));
-        mx = fmaxf(mx, lane_partner<8>(mx));
+        pmax(std::integral_constant<int, 4>{});
+        pmax(std::integral_constant<int, 8>{});
     }
-    const bool finite = mx < __builtin_inff();
-    const bool nz = finite && mx > 0.f;
+    const float mx = __uint_as_float(mb);
+    const bool finite = mb < 0x7F800000u;
+    const bool nz = finite && mb != 0;
     const int e = nz ? x24_exponent(mx) : 0;
+    // x24 = 65536 h + 256 m + l with balanced digits in [-128, 127]: l is the low
+    // byte of x24 read as signed, r = (x24 + 128) >> 8 = 256 h + m, and
+    // h = (r + 128) >> 8; each digit's byte is the low byte of x24, r and h, which
+    // v_perm_b32 gathers four at a time into the plane words
+    int xq[8], r[8], hh[8];
     int s8 = 0;
 #pragma unroll
-    for (int w = 0; w < 2; w++) {
-        uint32_t hw = 0, mw = 0, lw = 0;
+    for (int i = 0; i < 8; i++) {
+        xq[i] = (valid && nz) ? (int)rintf(__builtin_amdgcn_ldexpf(v[i], -e)) : 0;
+        r[i] = (xq[i] + 128) >> 8;
+        hh[i] = (r[i] + 128) >> 8;
+        s8 += xq[i];
+    }
+    // low bytes of a, b, c, d -> one word, a in byte 0 (v_perm_b32 selector byte
+    // 0 = the second operand's low byte, 4 = the first operand's)
+    auto gather = [](int a0, int b0, int c0, int d0) {
+        const uint32_t ab = __builtin_amdgcn_perm((uint32_t)b0, (uint32_t)a0, 0x0C0C0400u);
+        const uint32_t cd = __builtin_amdgcn_perm((uint32_t)d0, (uint32_t)c0, 0x0C0C0400u);
+        return __builtin_amdgcn_perm(cd, ab, 0x05040100u);
+    };
 #pragma unroll
-        for (int b = 0; b < 4; b++) {
-            const int xq = (valid && nz) ? (int)rintf(__builtin_amdgcn_ldexpf(v[4 * w + b], -e)) : 0;
-            int hd, md, ld;
-            x24_digits(xq, hd, md, ld);
-            s8 += xq;
-            hw |= ((uint32_t)hd & 0xFFu) << (8 * b);
-            mw |= ((uint32_t)md & 0xFFu) << (8 * b);
-            lw |= ((uint32_t)ld & 0xFFu) << (8 * b);
-        }
-        h[w] = hw;
-        m[w] = mw;
-        l[w] = lw;
+    for (int w = 0; w < 2; w++) {
+        l[w] = gather(xq[4 * w], xq[4 * w + 1], xq[4 * w + 2], xq[4 * w + 3]);
+        m[w] = gather(r[4 * w], r[4 * w + 1], r[4 * w + 2], r[4 * w + 3]);
+        h[w] = gather(hh[4 * w], hh[4 * w + 1], hh[4 * w + 2], hh[4 * w + 3]);
     }
     s32 = s8 + __float_as_int(lane_partner<1>(__int_as_float(s8)));
     s32 = s32 + __float_as_int(lane_partner<2>(__int_as_float(s32)));
