@@ -19,7 +19,7 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 LIB_DIR = PKG / "lib"
 LIB_NAME = "libmaxuna_moe.so"
-SOURCES = ["mx_api.hip", "mx_dequant.hip", "mx_mv.hip", "mx_mvf.hip", "mx_route.hip", "mx_elem.hip", "mx_mm.hip", "mx_gemm.hip",
+SOURCES = ["mx_api.hip", "mx_dequant.hip", "mx_mv.hip", "mx_mvf.hip", "mx_route.hip", "mx_elem.hip", "mx_mm.hip", "mx_gemm.hip", "mx_vmm.hip",
            "mx_gguf.cpp"]
 ARCH = "gfx950"
 

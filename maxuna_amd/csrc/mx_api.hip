@@ -288,11 +288,17 @@ mx_status mx_route_from_logits(const float *logits, const float *bias, int64_t t
 // ---- whole MoE block --------------------------------------------------------------------
 namespace {
 
-constexpr int64_t kDefaultMmMinSeq = 32;
+constexpr int64_t kDefaultMmMinSeq = 32;  // ops/mod.rs:31 MM_ID_MIN_SEQ
 #ifndef MX_FUSE_SELECT
 #define MX_FUSE_SELECT 1
 #endif
-constexpr bool kFuseSelect = MX_FUSE_SELECT != 0;  // ops/mod.rs:31 MM_ID_MIN_SEQ
+constexpr bool kFuseSelect = MX_FUSE_SELECT != 0;
+// Below the grouped-GEMM threshold, blocks of at least this many tokens run their
+// experts as 16-pair MFMA tiles (mx_vmm.hip) instead of per-pair mat-vecs
+#ifndef MX_VMM_MIN_T
+#define MX_VMM_MIN_T 16
+#endif
+constexpr int64_t kVmmMinT = MX_VMM_MIN_T;
 
 struct Ws {
     uint8_t *base;
@@ -311,6 +317,7 @@ struct Plan {
     bool generic;           // below the GEMM threshold, shapes the fused decode kernels cannot hold:
                             // router + f32 gather mat-vecs + SwiGLU + combine
     bool shared_in_decode;  // shared expert rides in the fused decode kernels (same quant types)
+    bool vmm;               // verify block on the 16-pair MFMA tiles (after the fused router)
     int64_t min_seq;
 };
 
@@ -342,6 +349,13 @@ Plan plan_for(const mx_moe_layer *L, int64_t t) {
                              decode_down_fits(L->down.dtype, (int)L->expert_ff, stack_row_bytes(L->down));
     p.generic = !p.mm && !decode_fits;
     p.fused_router = !p.mm && !p.generic && t <= route_fused_max_t();
+    const int64_t slots = L->top_k + (p.shared_in_decode ? 1 : 0);
+    const int64_t gu_rb = stack_row_bytes(L->gate), d_rb = stack_row_bytes(L->down);
+    p.vmm = p.fused_router && t >= kVmmMinT && (!p.has_shared || p.shared_in_decode) &&
+            t * slots <= PAIR_ORDER_MAX && L->gate.n_expert <= 1024 &&
+            vmm_supported(L->gate.dtype, L->down.dtype, (int)L->hidden, (int)L->expert_ff, gu_rb, d_rb) &&
+            L->expert_ff * gu_rb < ((int64_t)1 << 31) && L->hidden * d_rb < ((int64_t)1 << 31) &&
+            (!p.has_shared || (stack_row_bytes(L->shared_gate) == gu_rb && stack_row_bytes(L->shared_down) == d_rb));
     return p;
 }
 
@@ -356,6 +370,7 @@ struct Layout {
     float *x_normed = nullptr, *logits = nullptr, *w = nullptr, *act = nullptr;
     uint32_t *ids = nullptr, *zero_ids = nullptr;
     int32_t *perm = nullptr;  // expert-ordered (token, slot) pairs of a verify block
+    int32_t *runs = nullptr;  // their 16-pair runs (MFMA verify tiles)
     uint8_t *xstage = nullptr, *xstage_gm = nullptr;
     float *part = nullptr;
     int32_t *map = nullptr, *map_sh = nullptr;
@@ -386,6 +401,16 @@ Layout carve(const mx_moe_layer *L, int64_t t, const Plan &p, void *base) {
             o.sh_u = ws.take<float>(t * FF);
         }
         o.down = ws.take<float>(t * KK * H);
+    } else if (p.vmm) {
+        const int64_t slots = K + (p.has_shared ? 1 : 0);
+        o.perm = ws.take<int32_t>(t * slots);
+        o.runs = ws.take<int32_t>(2 * (t * slots + 1));
+        o.x16 = ws.take<_Float16>(t * H);
+        o.x16s = ws.take<float>(t);
+        o.act = ws.take<float>(t * slots * FF);
+        o.act16 = ws.take<_Float16>(t * slots * FF);
+        o.act16s = ws.take<float>(t * slots);
+        o.down = ws.take<float>(t * slots * H);
     } else if (!p.mm) {
         const int64_t slots = K + (p.shared_in_decode ? 1 : 0);
         o.xstage = ws.take<uint8_t>(t * stage_row_bytes((int)H));
@@ -617,6 +642,56 @@ mx_status moe_forward_impl(const mx_moe_layer *L, const float *x, int64_t t, con
                 ga.sel_keys = nullptr;
                 for (int r = 0; r < rep(1); r++) MX_TRY(launch_decode_select((int)K, sel, s));
             }
+        }
+        if (p.vmm) {
+            // 16-pair MFMA tiles: x -> scaled f16, gate/up + SwiGLU, act -> scaled f16,
+            // down into rows token * slots + slot, then the prefill combine
+            const int slots = (int)K + (shf ? 1 : 0), np = (int)t * slots;
+            MX_TRY(launch_pair_order(ids, (int)t, (int)K, (int)E, slots, o.perm, s, o.runs));
+            MX_STAGE();
+            VmmArgs g{};
+            g.w[0] = gg.w;
+            g.w[1] = gu.w;
+            g.w_sh[0] = shf ? sg.w : nullptr;
+            g.w_sh[1] = shf ? su.w : nullptr;
+            g.expert_bytes = gg.expert_bytes;
+            g.row_bytes = gg.row_bytes;
+            g.sh_row_bytes = sg.row_bytes;
+            g.n_expert = (int)E;
+            g.n_out = (int)FF;
+            g.k = (int)H;
+            g.a = o.x16;
+            g.a_scale = o.x16s;
+            g.a_slots = slots;
+            g.perm = o.perm;
+            g.runs = o.runs;
+            g.out = o.act;
+            for (int r = 0; r < rep(2); r++) {
+                MX_TRY(launch_to_f16_rows(xin, t, (int)H, nullptr, o.x16, o.x16s, s));
+                MX_TRY(launch_vmm(L->gate.dtype, true, g, np, s));
+            }
+            MX_STAGE();
+            VmmArgs d = g;
+            d.w[0] = gd.w;
+            d.w[1] = nullptr;
+            d.w_sh[0] = shf ? sd.w : nullptr;
+            d.w_sh[1] = nullptr;
+            d.expert_bytes = gd.expert_bytes;
+            d.row_bytes = gd.row_bytes;
+            d.sh_row_bytes = sd.row_bytes;
+            d.n_out = (int)H;
+            d.k = (int)FF;
+            d.a = o.act16;
+            d.a_scale = o.act16s;
+            d.a_slots = 1;
+            d.out = o.down;
+            for (int r = 0; r < rep(3); r++) {
+                MX_TRY(launch_to_f16_rows(o.act, np, (int)FF, nullptr, o.act16, o.act16s, s));
+                MX_TRY(launch_vmm(L->down.dtype, false, d, np, s));
+                MX_TRY(launch_combine_prefill(o.down, w, residual, (int)t, (int)K, shf ? 1 : 0, (int)H, out, s));
+            }
+            MX_STAGE();
+            return MX_OK;
         }
         if (o.perm) MX_TRY(launch_pair_order(ids, (int)t, (int)K, (int)E, (int)K + (shf ? 1 : 0), o.perm, s));
         MX_STAGE();

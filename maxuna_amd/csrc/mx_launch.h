@@ -78,8 +78,11 @@ bool decode_gate_up_selects(int dtype, const DecodeGateUpArgs &a);
 // share an expert run back to back on one XCD and the repeats read its L2.
 // t * slots <= PAIR_ORDER_MAX; the order within an expert is unspecified.
 constexpr int PAIR_ORDER_MAX = 1024;
+// runs (optional, 2 * (t * slots + 1) words): runs[0] = the number of runs, run r
+// at runs[2 + 2r] = first perm position | pairs << 16 (1..16 pairs), runs[3 + 2r] =
+// its expert: every expert's pairs cut into consecutive runs of at most 16.
 mx_status launch_pair_order(const uint32_t *ids, int t, int top_k, int n_expert, int slots, int32_t *perm,
-                            hipStream_t s);
+                            hipStream_t s, int32_t *runs = nullptr);
 // Decode top-k (decode router split): block i < n_sel selects token i from
 // keys/probs [n_sel, n_expert] (written by launch_route_fused) into ids/w
 // [n_sel, top_k].
@@ -232,5 +235,22 @@ mx_status launch_to_f16_rows(const float *x, int64_t rows, int k, const int32_t 
 // shared = down[t * kk + top_k] (has_shared), shared_sep[t] (shared_sep != NULL) or 0; n % 4 == 0
 mx_status launch_combine_prefill(const float *down, const float *w, const float *residual, int t, int top_k,
                                  int has_shared, int n, float *out, hipStream_t s, const float *shared_sep = nullptr);
+
+// mx_vmm.hip -- verify blocks on MFMA (16-pair tiles, each touched expert's
+// weights streamed once).  Output row of pair v = tok * slots + slot: out[v].
+struct VmmArgs {
+    const uint8_t *w[2];        // routed stacks: gate, up (SwiGLU) / the only matrix
+    const uint8_t *w_sh[2];     // run expert n_expert: the shared expert
+    int64_t expert_bytes, row_bytes, sh_row_bytes;
+    int n_expert, n_out, k;     // k % 512 == 0, n_out % 32 == 0
+    const _Float16 *a;          // A rows, f16 scaled by a_scale (x = a * a_scale)
+    const float *a_scale;
+    int a_slots;                // A row of pair v: v / a_slots
+    const int32_t *perm, *runs; // launch_pair_order
+    float *out;                 // [pairs, n_out]; SwiGLU: silu(gate) * up
+};
+bool vmm_supported(int gate_dtype, int down_dtype, int hidden, int ff, int64_t gu_row_bytes, int64_t d_row_bytes);
+// max_runs: an upper bound of runs[0] (the grid is sized from it)
+mx_status launch_vmm(int dtype, bool swiglu, const VmmArgs &a, int max_runs, hipStream_t s);
 
 }  // namespace mx

@@ -1118,7 +1118,8 @@ __global__ void __launch_bounds__(SEL_THREADS) k_decode_select(int top_k, Decode
 
 __global__ void __launch_bounds__(PAIR_ORDER_MAX) k_pair_order(const uint32_t *__restrict__ ids, int t, int top_k,
                                                                 int n_expert, int slots,
-                                                                int32_t *__restrict__ perm) {
+                                                                int32_t *__restrict__ perm,
+                                                                int32_t *__restrict__ runs) {
     __shared__ int cnt[SEL_MAX_E + 2];
     __shared__ int s_scan[PAIR_ORDER_MAX];
     const int tid = threadIdx.x, n = t * slots, ne = n_expert + 1;  // expert n_expert: the shared slot
@@ -1136,11 +1137,12 @@ __global__ void __launch_bounds__(PAIR_ORDER_MAX) k_pair_order(const uint32_t *_
         rank = atomicAdd(&cnt[e], 1);
     }
     __syncthreads();
-    // exclusive scan of the counts: each thread sums a run of `per` experts
+    // exclusive scan of the counts (low 16 bits) and of the 16-pair runs (high
+    // 16 bits; both totals <= PAIR_ORDER_MAX): each thread sums `per` experts
     const int per = (ne + PAIR_ORDER_MAX - 1) / PAIR_ORDER_MAX;
     const int e0 = min(tid * per, ne), e1 = min(e0 + per, ne);
     int sum = 0;
-    for (int i = e0; i < e1; i++) sum += cnt[i];
+    for (int i = e0; i < e1; i++) sum += cnt[i] + (((cnt[i] + 15) >> 4) << 16);
     s_scan[tid] = sum;
     __syncthreads();
     for (int d = 1; d < PAIR_ORDER_MAX; d <<= 1) {
@@ -1149,21 +1151,29 @@ __global__ void __launch_bounds__(PAIR_ORDER_MAX) k_pair_order(const uint32_t *_
         s_scan[tid] += v;
         __syncthreads();
     }
-    int run = s_scan[tid] - sum;
+    const int ex = s_scan[tid] - sum;
+    int run = ex & 0xFFFF, r = ex >> 16;
     for (int i = e0; i < e1; i++) {
         const int c = cnt[i];
         cnt[i] = run;
+        if (runs)
+            for (int j = 0; j < c; j += 16, r++) {
+                runs[2 + 2 * r] = (run + j) | (min(16, c - j) << 16);
+                runs[3 + 2 * r] = i;
+            }
         run += c;
     }
+    if (runs && tid == PAIR_ORDER_MAX - 1) runs[0] = s_scan[tid] >> 16;
     __syncthreads();
     if (tid < n) perm[cnt[e] + rank] = tid | (e << 16);  // the expert rides along: no ids load downstream
 }
 
 mx_status launch_pair_order(const uint32_t *ids, int t, int top_k, int n_expert, int slots, int32_t *perm,
-                            hipStream_t s) {
+                            hipStream_t s, int32_t *runs) {
     if ((int64_t)t * slots > PAIR_ORDER_MAX || n_expert > SEL_MAX_E)
         return fail(MX_ERR_SHAPE, "pair order: t * slots <= %d and n_expert <= %d", PAIR_ORDER_MAX, SEL_MAX_E);
-    hipLaunchKernelGGL(k_pair_order, dim3(1), dim3(PAIR_ORDER_MAX), 0, s, ids, t, top_k, n_expert, slots, perm);
+    hipLaunchKernelGGL(k_pair_order, dim3(1), dim3(PAIR_ORDER_MAX), 0, s, ids, t, top_k, n_expert, slots, perm,
+                       runs);
     MX_LAUNCH("k_pair_order");
     return MX_OK;
 }

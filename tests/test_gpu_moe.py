@@ -60,8 +60,9 @@ def test_decode_layer(dev, orc, name):
 
 @pytest.mark.parametrize("t", [2, 4, 5, 16, 31])
 def test_verify_block(dev, orc, t):
-    """C2: speculative verify blocks below MM_ID_MIN_SEQ (decode kernels, (token,
-    slot) pairs walked in expert order)."""
+    """C2: speculative verify blocks below MM_ID_MIN_SEQ: t < 16 on the decode
+    kernels ((token, slot) pairs walked in expert order), t = 16 and 31 on the
+    16-pair MFMA tiles."""
     cfg = CONFIGS["C2"]
     _log(f"C2 t={t}")
     layer = build_layer(cfg["spec"], seed=1002)
@@ -273,8 +274,11 @@ def test_decode_down_compiled_shape_matches_generic(dev):
     a kernel with compile-time geometry; the same weights placed 2 bytes off
     16-byte alignment (Q6_K needs 2) take the generic slot-per-wave kernel.  Both
     perform the same operations in the same order, so the outputs must be
-    bit-identical (t = 1 and 3: the slot-per-wave path; t = 6 and 16: the
-    per-(slot, row tile) verify path)."""
+    bit-identical (t = 1 and 3: the slot-per-wave path; t = 6 and 12: the
+    per-(slot, row tile) verify path).  At t = 16 both run the MFMA verify tiles,
+    whose Q6_K copies take the 16-byte span around each block: the 2-byte offset
+    moves the expert's last block across a chunk boundary, and the results must
+    not change."""
     from maxuna_amd.gguf import ExpertStack
     from maxuna_amd.moe import MoeBlock, SharedExpert
 
@@ -290,7 +294,7 @@ def test_decode_down_compiled_shape_matches_generic(dev):
     e, sh = blk.experts, blk.shared
     other = MoeBlock(blk.router, blk.exp_probs_b, e.gate, e.up, shifted(e.down), blk.cfg,
                      shared=SharedExpert(sh.gate, sh.up, shifted(sh.down)))
-    for t in (1, 3, 6, 16):
+    for t in (1, 3, 6, 12, 16):
         x = dev_f32(make_x(spec, 300 + t, t))
         a = host(blk.forward(x))
         b = host(other.forward(x))

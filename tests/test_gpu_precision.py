@@ -1,14 +1,17 @@
 """Activation precision of the decode kernels, wide rows, and id validation.
 
-The decode kernels carry each activation value on a 24-bit grid per 32-value
-group (power-of-two scale, three int8 digit planes, exact int32 plane sums):
-every value to within 2^-23 * (1 + 2^-8) of its group's largest magnitude.
+The decode kernels carry each activation value on a 24-bit grid per scale group
+-- the aligned 128-value block (32-value group when k % 128 != 0) -- with a
+power-of-two scale, three int8 digit planes and exact int32 plane sums: every
+value to within 2^-23 * (1 + 2^-8) of its group's largest magnitude.
 That is the width of the reference's f32 `y` (mv.metal:227-275), so the
 decode outputs match the f32 oracle to f32-class error -- well inside the
 contract's rel-L2 1e-3 -- also when a group holds a large outlier channel next
 to unit-scale values, the case a block grid handles worst.  The tests below
 assert rel-L2 <= 2e-6 (a 16-bit grid misses that by an order of magnitude on
-the outlier inputs) and the contract bound on whole layers.
+the outlier inputs) and the contract bound on whole layers.  Verify blocks of
+16 to 31 tokens run the 16-pair MFMA tiles instead (f16 operands, like the
+grouped GEMM): those are held to the contract bound.
 """
 import numpy as np
 import pytest
@@ -69,12 +72,13 @@ def test_mv_id_f32_class_accuracy(dev, orc, dt, kind):
 
 
 def test_decode_layer_outlier_channels(dev, orc):
-    """C1 layer at t = 1 and a C2 verify block at t = 16 with one channel x1000 per
-    32-group: f32-class agreement with the oracle (same routing)."""
+    """C1 layer at t = 1 and a verify block at t = 12 (both on the decode kernels)
+    with one channel x1000 per 32-group: f32-class agreement with the oracle (same
+    routing)."""
     spec = CONFIGS["C1"]["spec"]
     layer = build_layer(spec, seed=1101)
     rng = np.random.default_rng(11)
-    for t in (1, 16):
+    for t in (1, 12):
         _log(f"C1 outlier t={t}")
         x = outlier_x(rng, (t, spec.hidden))
         out, ids, w = layer.block.forward(dev_f32(x), return_routing=True)
@@ -129,3 +133,23 @@ def test_check_ids(dev):
     assert ops.check_ids(dev_u32(both), 8, raise_on_error=False) == 3
     with pytest.raises(ops.MaxunaError, match="repeats an expert id"):
         ops.check_ids(dev_u32(dup), 8)
+
+
+def test_verify_tiles_outlier_channels(dev, orc):
+    """Verify blocks of 16 and 31 tokens run the 16-pair MFMA tiles (f16 operands,
+    per-row power-of-two scales, like the grouped GEMM): the contract bound on the
+    outlier inputs, not f32-class."""
+    spec = CONFIGS["C1"]["spec"]
+    layer = build_layer(spec, seed=1101)
+    rng = np.random.default_rng(12)
+    for t in (16, 31):
+        _log(f"C1 outlier verify tiles t={t}")
+        x = outlier_x(rng, (t, spec.hidden))
+        out, ids, w = layer.block.forward(dev_f32(x), return_routing=True)
+        out, ids, w = host(out), host(ids), host(w)
+        logits = orc.route_logits(x, layer.router_t)
+        oid, _ = orc.route_from_logits(logits, layer.bias, spec.top_k, 1.0, True)
+        check_ids(ids, oid, selection_margin(logits, layer.bias, spec.top_k))
+        want, _, _ = orc.moe_layer(spec, layer.keys, layer.router_t, layer.bias, x, ids=ids, w=w)
+        r = assert_close(out, want, what=f"C1 outlier verify tiles t={t}")
+        _log(f"  {r}")
