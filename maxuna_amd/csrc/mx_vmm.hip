@@ -58,9 +58,12 @@ template <> struct VmBlk<kQ6_K> {
     static constexpr int BLK = 210, CPR = 15, SLOT = 240;  // the aligned span (phase <= 14)
 };
 
-template <int DT, bool SWIGLU> struct VmGeo {
+// COLS output columns per item (16 or 32): the wave's weight rows are COLS rows
+// of each matrix, slot order matrix-major
+template <int DT, bool SWIGLU, int COLS> struct VmGeo {
+    static_assert(COLS == 16 || COLS == 32, "16 or 32 columns per item");
     static constexpr int NMAT = SWIGLU ? 2 : 1;
-    static constexpr int ROWS = 32 * NMAT;      // weight rows per wave and stage
+    static constexpr int ROWS = COLS * NMAT;    // weight rows per wave and stage
     static constexpr int NBLK = ROWS / 16;      // 16-row MFMA column blocks
     static constexpr int CPR = VmBlk<DT>::CPR, SLOT = VmBlk<DT>::SLOT, BLK = VmBlk<DT>::BLK;
     static constexpr int POS = ROWS * CPR;      // copy positions (rows x chunks)
@@ -121,14 +124,15 @@ struct VmQ4 {
 
 // One work item, as a wave sees it.  Uniform: the matrices and the run; per
 // lane: the copy sources, the A row and the output rows of its accumulators.
-template <int DT, bool SWIGLU> struct VmItem {
-    using G = VmGeo<DT, SWIGLU>;
+template <int DT, bool SWIGLU, int COLS> struct VmItem {
+    using G = VmGeo<DT, SWIGLU, COLS>;
     const uint8_t *base[G::NMAT];  // expert matrices (Q6_K: 16-byte-aligned base)
     __amdgpu_buffer_rsrc_t rsrc;   // Q6_K: the expert matrix as a buffer
     uint32_t src[G::NI];           // per copy instruction: chunk offset from its matrix (stage 0)
     int mat[G::NI];                // SwiGLU: the matrix of the lane's chunk
     uint32_t rowpos[G::NBLK];      // Q6_K: phase + row offset of the lane's rows (block phases)
     const _Float16 *arow;          // the lane's A row (pair n of the run, clamped)
+    bool aon;                      // pair n exists (else the lane's A fragments are 0)
     int pv[4];                     // pair index of accumulator row 4 q + r, -1: none
     float ps[4];                   // its A scale
     int cb;                        // column block
@@ -142,10 +146,10 @@ struct VmTabs {
     const float *__restrict__ a_scale;
 };
 
-template <int DT, bool SWIGLU>
+template <int DT, bool SWIGLU, int COLS>
 __device__ __forceinline__ void vm_item(const VmmArgs &a, const VmTabs &tb, int item, int CB, int lane,
-                                        VmItem<DT, SWIGLU> &it) {
-    using G = VmGeo<DT, SWIGLU>;
+                                        VmItem<DT, SWIGLU, COLS> &it) {
+    using G = VmGeo<DT, SWIGLU, COLS>;
     const int run = item / CB;
     const int cb = item - run * CB;
     const int w0 = tb.runs[2 + 2 * run], e = tb.runs[3 + 2 * run];
@@ -167,6 +171,7 @@ __device__ __forceinline__ void vm_item(const VmmArgs &a, const VmTabs &tb, int 
 #pragma unroll
     for (int m = 1; m < VM_ROWS_M; m++) mine = n == m ? pair[m] : mine;
     it.arow = a.a + (int64_t)(mine / a.a_slots) * a.k;
+    it.aon = n < cnt;
     float sc[VM_ROWS_M];  // (scalar loads)
 #pragma unroll
     for (int m = 0; m < VM_ROWS_M; m++) sc[m] = tb.a_scale[pair[m] / a.a_slots];
@@ -201,20 +206,20 @@ __device__ __forceinline__ void vm_item(const VmmArgs &a, const VmTabs &tb, int 
     for (int i = 0; i < G::NI; i++) {
         const int p = min(64 * i + lane, G::POS - 1);  // spare lanes repeat the last chunk
         const int R = p / G::CPR, c = p - R * G::CPR;
-        it.mat[i] = R / 32;
-        const uint32_t row = (uint32_t)(cb * 32 + R % 32) * (uint32_t)rb;
+        it.mat[i] = R / COLS;
+        const uint32_t row = (uint32_t)(cb * COLS + R % COLS) * (uint32_t)rb;
         it.src[i] = G::kBuf ? phase + row : row + 16u * (uint32_t)c;
     }
 #pragma unroll
     for (int nb = 0; nb < G::NBLK; nb++)
-        it.rowpos[nb] = phase + (uint32_t)(cb * 32 + (nb % 2) * 16 + n) * (uint32_t)rb;
+        it.rowpos[nb] = phase + (uint32_t)(cb * COLS + (16 * nb) % COLS + n) * (uint32_t)rb;
 }
 
 // stage ks's copies of the item into buf (every lane copies: no branch around a
 // copy, so the copy counts the waits assume are exact)
-template <int DT, bool SWIGLU>
-__device__ __forceinline__ void vm_issue_b(const VmItem<DT, SWIGLU> &it, int ks, int lane, uint8_t *buf) {
-    using G = VmGeo<DT, SWIGLU>;
+template <int DT, bool SWIGLU, int COLS>
+__device__ __forceinline__ void vm_issue_b(const VmItem<DT, SWIGLU, COLS> &it, int ks, int lane, uint8_t *buf) {
+    using G = VmGeo<DT, SWIGLU, COLS>;
 #pragma unroll
     for (int i = 0; i < G::NI; i++) {
         if constexpr (G::kBuf) {
@@ -232,41 +237,48 @@ __device__ __forceinline__ void vm_issue_b(const VmItem<DT, SWIGLU> &it, int ks,
 
 // stage ks's A fragments af[4 par + P]: the 8 values the lane's weight operand
 // holds at step P of half par (Q4_K: 32 q + 8 P, Q6_K: 32 P + 8 q of the half)
+// (lanes of missing pairs load nothing; lane n = 0 always loads, so every load
+// instruction issues and the wait counts stay exact)
 template <int DT>
-__device__ __forceinline__ void vm_issue_a(const _Float16 *arow, int ks, int q, half8_t (&af)[8]) {
+__device__ __forceinline__ void vm_issue_a(const _Float16 *arow, bool on, int ks, int q, half8_t (&af)[8]) {
     const _Float16 *p = arow + ks * 256 + (DT == kQ4_K ? 32 : 8) * q;
 #pragma unroll
-    for (int s = 0; s < 8; s++)
-        af[s] = *reinterpret_cast<const half8_t *>(p + 128 * (s >> 2) + (DT == kQ4_K ? 8 : 32) * (s & 3));
+    for (int s = 0; s < 8; s++) af[s] = half8_t{};
+    if (on) {
+#pragma unroll
+        for (int s = 0; s < 8; s++)
+            af[s] = *reinterpret_cast<const half8_t *>(p + 128 * (s >> 2) + (DT == kQ4_K ? 8 : 32) * (s & 3));
+    }
 }
 
 }  // namespace
 
-template <int DT, bool SWIGLU>
-__global__ void __launch_bounds__(64 * VM_WAVES) __attribute__((amdgpu_waves_per_eu(2))) k_vmm(VmmArgs a, const int32_t *__restrict__ perm, const int32_t *__restrict__ runs,
+template <int DT, bool SWIGLU, int COLS, int WPE>
+__global__ void __launch_bounds__(64 * VM_WAVES) __attribute__((amdgpu_waves_per_eu(WPE)))
+k_vmm(VmmArgs a, const int32_t *__restrict__ perm, const int32_t *__restrict__ runs,
       const float *__restrict__ a_scale) {
     const VmTabs tb{perm, runs, a_scale};
-    using G = VmGeo<DT, SWIGLU>;
+    using G = VmGeo<DT, SWIGLU, COLS>;
     __shared__ __attribute__((aligned(16))) uint8_t sB[2][VM_WAVES][G::BUF];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n = lane & 15, q = lane >> 4, kh = q >> 1, hh = q & 1;
     const int gw = blockIdx.x * VM_WAVES + wave, NW = gridDim.x * VM_WAVES;
-    const int CB = a.n_out / 32;
+    const int CB = a.n_out / COLS;
     const int n_items = runs[0] * CB;
     if (gw >= n_items) return;  // wave-uniform; no block barrier in this kernel
     const int nks = a.k / 256;  // even
     const int total = ((n_items - 1 - gw) / NW + 1) * nks;
     uint8_t *const b0 = sB[0][wave], *const b1 = sB[1][wave];
 
-    VmItem<DT, SWIGLU> cur, nxt;
+    VmItem<DT, SWIGLU, COLS> cur, nxt;
     vm_item(a, tb, gw, CB, lane, cur);
     nxt = cur;
     half8_t a0[8], a1[8];
     float4_t acc[G::NBLK];
 #pragma unroll
     for (int nb = 0; nb < G::NBLK; nb++) acc[nb] = float4_t{0.f, 0.f, 0.f, 0.f};
-    vm_issue_a<DT>(cur.arow, 0, q, a0);
+    vm_issue_a<DT>(cur.arow, cur.aon, 0, q, a0);
     vm_issue_b(cur, 0, lane, b0);
 
     // stage S from (buf, af); issues stage S + 1 (clamped: the last stage re-copies
@@ -278,7 +290,7 @@ __global__ void __launch_bounds__(64 * VM_WAVES) __attribute__((amdgpu_waves_per
         const int ks = S - (S / nks) * nks;
         if (ks1 == 0 && S1 != S) vm_item(a, tb, gw + j1 * NW, CB, lane, nxt);  // wave-uniform
         wait_lgkmcnt0();  // this wave's reads of nbuf (stage S - 1) have returned
-        vm_issue_a<DT>(nxt.arow, ks1, q, naf);
+        vm_issue_a<DT>(nxt.arow, nxt.aon, ks1, q, naf);
         vm_issue_b(nxt, ks1, lane, nbuf);
         // stage S's copy and fragments have landed: younger are only stage S + 1's
         wait_vmcnt(8 + G::NI);
@@ -288,7 +300,7 @@ __global__ void __launch_bounds__(64 * VM_WAVES) __attribute__((amdgpu_waves_per
             W wb[G::NBLK];
 #pragma unroll
             for (int nb = 0; nb < G::NBLK; nb++) {
-                const uint8_t *slot = buf + ((nb / 2) * 32 + (nb % 2) * 16 + n) * G::SLOT;
+                const uint8_t *slot = buf + (16 * nb + n) * G::SLOT;
                 if constexpr (DT == kQ4_K) {
                     wb[nb].template load<PAR>(slot, q);
                 } else {
@@ -313,11 +325,11 @@ __global__ void __launch_bounds__(64 * VM_WAVES) __attribute__((amdgpu_waves_per
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 if (cur.pv[r] < 0) continue;
-                float *orow = a.out + (int64_t)cur.pv[r] * a.n_out + cur.cb * 32 + n;
+                float *orow = a.out + (int64_t)cur.pv[r] * a.n_out + cur.cb * COLS + n;
                 if constexpr (SWIGLU) {
 #pragma unroll
-                    for (int h = 0; h < 2; h++) {
-                        const float g = acc[h][r] * cur.ps[r], u = acc[2 + h][r] * cur.ps[r];
+                    for (int h = 0; h < G::NBLK / 2; h++) {
+                        const float g = acc[h][r] * cur.ps[r], u = acc[G::NBLK / 2 + h][r] * cur.ps[r];
                         orow[16 * h] = g / (1.0f + expf(-g)) * u;  // silu(g) * u (silu_mul.metal:57-72)
                     }
                 } else {
@@ -359,17 +371,41 @@ bool vmm_supported(int gate_dtype, int down_dtype, int hidden, int ff, int64_t g
            (int64_t)hidden * 2 < (int64_t)1 << 31;
 }
 
-mx_status launch_vmm(int dtype, bool swiglu, const VmmArgs &a, int max_runs, hipStream_t s) {
-    const int64_t items = (int64_t)max_runs * (a.n_out / 32);
-    if (items == 0) return MX_OK;
+// columns per item and waves per SIMD of the SwiGLU (gate/up) and plain (down)
+// kernels
+#ifndef MX_VMM_GU_COLS
+#define MX_VMM_GU_COLS 32
+#endif
+#ifndef MX_VMM_GU_WPE
+#define MX_VMM_GU_WPE 2
+#endif
+#ifndef MX_VMM_DN_COLS
+#define MX_VMM_DN_COLS 32
+#endif
+#ifndef MX_VMM_DN_WPE
+#define MX_VMM_DN_WPE 2
+#endif
+
+namespace {
+template <int DT, bool SWIGLU, int COLS, int WPE>
+void vm_launch(const VmmArgs &a, int max_runs, hipStream_t s) {
+    using G = VmGeo<DT, SWIGLU, COLS>;
+    const int64_t items = (int64_t)max_runs * (a.n_out / COLS);
     const int64_t want = (items + VM_WAVES - 1) / VM_WAVES;
-    const int64_t cap = 2 * (int64_t)vm_cus();  // two workgroups per CU (LDS)
+    // resident workgroups per CU: WPE by registers (4 waves each), and by LDS
+    const int by_lds = (160 * 1024) / (2 * VM_WAVES * G::BUF);
+    const int64_t cap = (int64_t)(WPE < by_lds ? WPE : by_lds) * vm_cus();
     const unsigned grid = (unsigned)(want < cap ? want : cap);
-    if (dtype == kQ4_K && swiglu) hipLaunchKernelGGL((k_vmm<kQ4_K, true>), dim3(grid), dim3(64 * VM_WAVES), 0, s, a, a.perm, a.runs,
-                                                 a.a_scale);
-    else if (dtype == kQ4_K) hipLaunchKernelGGL((k_vmm<kQ4_K, false>), dim3(grid), dim3(64 * VM_WAVES), 0, s, a, a.perm, a.runs, a.a_scale);
-    else if (dtype == kQ6_K && !swiglu)
-        hipLaunchKernelGGL((k_vmm<kQ6_K, false>), dim3(grid), dim3(64 * VM_WAVES), 0, s, a, a.perm, a.runs, a.a_scale);
+    hipLaunchKernelGGL((k_vmm<DT, SWIGLU, COLS, WPE>), dim3(grid), dim3(64 * VM_WAVES), 0, s, a, a.perm, a.runs,
+                       a.a_scale);
+}
+}  // namespace
+
+mx_status launch_vmm(int dtype, bool swiglu, const VmmArgs &a, int max_runs, hipStream_t s) {
+    if (max_runs == 0) return MX_OK;
+    if (dtype == kQ4_K && swiglu) vm_launch<kQ4_K, true, MX_VMM_GU_COLS, MX_VMM_GU_WPE>(a, max_runs, s);
+    else if (dtype == kQ4_K) vm_launch<kQ4_K, false, MX_VMM_DN_COLS, MX_VMM_DN_WPE>(a, max_runs, s);
+    else if (dtype == kQ6_K && !swiglu) vm_launch<kQ6_K, false, MX_VMM_DN_COLS, MX_VMM_DN_WPE>(a, max_runs, s);
     else return fail(MX_ERR_DTYPE, "verify tiles: unsupported weight type %d", dtype);
     MX_LAUNCH("k_vmm");
     return MX_OK;
