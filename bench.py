@@ -425,9 +425,9 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4_K/q6_K weight blocks; activations on a 24-bit grid per 32-value group (power-of-two scale, "
-                 "three int8 digit planes, exact int32 plane sums on v_dot4_i32_i8) recombined and scaled in f32, "
-                 "f32 accumulation",
+        "dtype": "q4_K/q6_K weight blocks; activations on a 24-bit grid per 128-value block (power-of-two "
+                 "scale, three int8 digit planes, exact int32 plane sums on v_dot4_i32_i8, Q6_K part sums scaled "
+                 "in int32) recombined and scaled in f32, f32 accumulation",
         "data": "synthetic (seeded GGUF blocks generated on device; x, router ~ N(0,1), N(0,0.02))",
         "config": {"workload": f"C1 decode MoE layer, batch 1; one step = one forward of each of {args.layers} "
                                "distinct C1 layers (graph replay)",
