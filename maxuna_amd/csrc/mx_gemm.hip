@@ -156,6 +156,7 @@ __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
     constexpr int DMA_PER_WAVE = STAGE_BYTES / 1024 / NWAVE;
     constexpr int BROWS = GemmNb<DT, SWIGLU>::bn;           // weight rows of the tile
     using BS = BSlots<DT, SWIGLU>;
+    using GW = std::conditional_t<DT == kQ4_K, WB4L, WB<DT>>;  // the lane's weight registers
     constexpr int CPR = BS::CPR;
     constexpr int B_POS = BS::positions(BROWS);
     constexpr int B_INSTS = (B_POS + 63) / 64;                 // B copy instructions per stage
@@ -274,11 +275,13 @@ __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
         asm volatile("" ::: "memory");
     };
 
-    // per-lane LDS offsets of the A operand for the 8 steps of a stage
+    // per-lane LDS offsets of the A operand for the 8 steps of a stage: the
+    // 16-byte chunk (8 K values) the lane's weight operand holds at step s
+    // (Q4_K, WB4L: 64 kh + 8 s; the others: 32 (s / 2) + 16 kh + 8 (s % 2))
     int aoff[8];
 #pragma unroll
     for (int s = 0; s < 8; s++) {
-        const int c = 4 * (s >> 1) + 2 * kh + (s & 1);
+        const int c = DT == kQ4_K ? 8 * kh + s : 4 * (s >> 1) + 2 * kh + (s & 1);
         aoff[s] = j * ROWB + ((c ^ (j & 15)) << 4);
     }
 
@@ -292,7 +295,7 @@ __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
 
     // MB: 32-row blocks of the tile that hold rows (a partly filled last m-tile of
     // an expert skips the MFMAs and A reads of its empty blocks)
-    auto compute = [&](auto mbc, const uint8_t *buf, WB<DT>(&wb)[NB]) {
+    auto compute = [&](auto mbc, const uint8_t *buf, GW(&wb)[NB]) {
         constexpr int MB = decltype(mbc)::value;
         // the A fragments of step s + 1 are read while step s computes
         half8_t af[2][4];
@@ -313,7 +316,10 @@ __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
             }
             half8_t bf[NB];
 #pragma unroll
-            for (int nb = 0; nb < NB; nb++) bf[nb] = wb[nb].step(p, hh);
+            for (int nb = 0; nb < NB; nb++) {
+                if constexpr (DT == kQ4_K) bf[nb] = wb[nb].step(s);
+                else bf[nb] = wb[nb].step(p, hh);
+            }
 #pragma unroll
             for (int mb = 0; mb < MB; mb++)
 #pragma unroll
@@ -322,12 +328,14 @@ __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
         }
     };
     // stage ks's B registers from LDS (the block phase of the lane's row for this stage)
-    WB<DT> wb[NB];
+    GW wb[NB];
     auto load_b = [&](int ks, const uint8_t *buf) {
         const uint32_t so = stage_block_off<DT>(ks);
 #pragma unroll
-        for (int nb = 0; nb < NB; nb++)
-            wb_load<DT>(wb[nb], buf + BS::row_off(brow[nb]), kh, (rowoff[nb] + so) & 15u, ks & 1);
+        for (int nb = 0; nb < NB; nb++) {
+            if constexpr (DT == kQ4_K) wb[nb].load_lds(buf + BS::row_off(brow[nb]), kh, 0u);
+            else wb_load<DT>(wb[nb], buf + BS::row_off(brow[nb]), kh, (rowoff[nb] + so) & 15u, ks & 1);
+        }
     };
 
     const int nks = a.k / KS;  // even

@@ -141,6 +141,40 @@ template <> struct WB<kQ4_K> {
     }
 };
 
+// Q4_K, the form the prefill GEMM uses: the same stage slot, but lane half kh
+// owns the 64-value chunk kh of the half super-block -- sub-blocks 2 kh (low
+// nibbles) and 2 kh + 1 (high nibbles), qs bytes [32 kh, +32) of the slot's 64 --
+// so it unpacks two scale / min pairs per half instead of four; step s gives it
+// the values 64 kh + 8 s + [0, 8) of the half.  Same dequantised values as
+// WB<kQ4_K> (the K order of the MFMA steps differs; A follows it).
+struct WB4L {
+    static constexpr int CPR = WB<kQ4_K>::CPR, SLOT = WB<kQ4_K>::SLOT, BLK = WB<kQ4_K>::BLK;
+    uint4 h, q[2];
+    __device__ __forceinline__ void load_lds(const uint8_t *slot, int kh, uint32_t) {
+        h = *reinterpret_cast<const uint4 *>(slot);
+        q[0] = *reinterpret_cast<const uint4 *>(slot + 16 + 32 * kh);
+        q[1] = *reinterpret_cast<const uint4 *>(slot + 32 + 32 * kh);
+    }
+    float d1[2], c1[2];
+    template <int PAR> __device__ __forceinline__ void prep(int kh) {
+        const float d = h2f((uint16_t)(h.x & 0xFFFFu)), dmin = h2f((uint16_t)(h.x >> 16));
+        uint32_t sc, mn;
+        q4k_pair_scale_min(2 * PAR + kh, h.y, h.z, h.w, sc, mn);  // sub-blocks 4 PAR + 2 kh, + 1
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            d1[i] = d * (float)((sc >> (8 * i)) & 0xFFu);
+            c1[i] = __builtin_fmaf(-1024.0f, d1[i], -(dmin * (float)((mn >> (8 * i)) & 0xFFu)));
+        }
+    }
+    __device__ __forceinline__ half8_t step(int s) const {
+        const uint4 &v = q[(s & 3) >> 1];
+        const int sh = 4 * (s >> 2);
+        const uint32_t w0 = (((s & 1) ? v.z : v.x) >> sh) & 0x0F0F0F0Fu;
+        const uint32_t w1 = (((s & 1) ? v.w : v.y) >> sh) & 0x0F0F0F0Fu;
+        return dq8_kmin(w0, w1, d1[s >> 2], c1[s >> 2]);
+    }
+};
+
 // Q5_K: Q4_K's stage layout (qs at byte 48) plus lane half kh's 16 bytes of qh;
 // step p of half `par` adds bit 4 par + p of qh[l] as the fifth bit (mm_id.metal:113-134).
 template <> struct WB<kQ5_K> {
