@@ -89,6 +89,28 @@ def forward_repeat(block, x, out, stage, times):
                                       ws.data_ptr(), ws.numel(), ops._stream(), stage, times))
 
 
+def read_probe():
+    """Plain streaming reads (mx_probe_read) of the C1 expert kernels' byte counts and
+    larger ones, each launch on a different region of a 4 GiB pool (no cache
+    reuse), 40 launches per captured graph: the achievable HBM read rate."""
+    import torch
+    from maxuna_amd._lib import check, lib
+    from maxuna_amd import ops
+    pool = torch.empty(4 << 30, dtype=torch.uint8, device="cuda").fill_(1)
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+    sizes = {"router (4 MB)": 4 << 20, "C1 down (57 MB)": 56854528, "C1 gate/up (78 MB)": 77873152,
+             "C1 layer (135 MB)": 134727680, "512 MiB": 512 << 20}
+    for name, n in sizes.items():
+        n -= n % 16
+        slots = min(40, (4 << 30) // n)
+
+        def launches():
+            for r in range(40):
+                check(lib().mx_probe_read(pool.data_ptr() + (r % slots) * n, n, sink.data_ptr(), ops._stream()))
+        us = graph_us(launches, 3) / 40
+        log(f"read probe {name}: {us:.2f} us per read, {n / (us * 1e-6) / 1e9:.0f} GB/s")
+
+
 def graph_us(fn, replays):
     """Average time of one replay of the graph captured from fn(), us."""
     import torch
@@ -381,6 +403,8 @@ def main():
     ap.add_argument("--no-decode", action="store_true", help="prefill only (profiling); prints no JSON line")
     ap.add_argument("--no-extra", action="store_true", help="skip the C2 verify, C4 chain and lm_head figures")
     ap.add_argument("--no-chain", action="store_true", help="skip the C4 chain and lm_head figures (keep C2)")
+    ap.add_argument("--read-probe", action="store_true",
+                    help="only time plain streaming reads of the expert kernels' sizes (achievable HBM read rate)")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="only run N device-to-device copies of this many MB (HBM counter calibration) and exit")
     args = ap.parse_args()
@@ -390,6 +414,9 @@ def main():
         sys.exit(2)
     import torch
     torch.cuda.set_device(0)
+    if args.read_probe:
+        read_probe()
+        return
     if args.copy_probe_mb:
         # a plain copy of known size: FETCH_SIZE / WRITE_SIZE of its dispatches calibrate
         # the counters that give the decode kernels' HBM traffic

@@ -135,6 +135,7 @@ SIGNATURES = {
 INSTRUMENT_SIGNATURES = {
     "mx_moe_forward_profiled": (I32, [C.POINTER(MoeLayerC), P, I64, P, P, P, P, P, SZ, P, P, I32, P]),
     "mx_moe_forward_repeat": (I32, [C.POINTER(MoeLayerC), P, I64, P, P, P, P, P, SZ, P, I32, I32]),
+    "mx_probe_read": (I32, [P, I64, P, P]),
 }
 
 _lib = None

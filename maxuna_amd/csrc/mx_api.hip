@@ -800,6 +800,13 @@ mx_status mx_moe_forward_profiled(const mx_moe_layer *L, const float *x, int64_t
     return MX_OK;
 }
 
+mx_status mx_probe_read(const void *src, int64_t nbytes, uint32_t *sink, mx_stream_t stream) {
+    if (!src || !sink) return fail(MX_ERR_NULL, "probe_read: NULL pointer");
+    if (nbytes % 16 || (reinterpret_cast<uintptr_t>(src) & 15))
+        return fail(MX_ERR_ALIGN, "probe_read: 16-byte-aligned source and size");
+    return launch_read_probe(src, nbytes, sink, (hipStream_t)stream);
+}
+
 mx_status mx_moe_forward_repeat(const mx_moe_layer *L, const float *x, int64_t t, const float *residual, float *out,
                                 uint32_t *ids_out, float *w_out, void *workspace, size_t workspace_bytes,
                                 mx_stream_t stream, int32_t stage, int32_t times) {

@@ -50,6 +50,12 @@ mx_status mx_moe_forward_repeat(const mx_moe_layer *layer, const float *x, int64
                                 void *workspace, size_t workspace_bytes, mx_stream_t stream,
                                 int32_t stage, int32_t times);
 
+/* A plain streaming read of nbytes (multiple of 16) from src (16-byte aligned),
+ * 512 x 256 threads with four 16-byte loads in flight each: the achievable HBM
+ * read rate the expert kernels are compared with.  `sink` receives nothing in
+ * practice.  Capturable.  For the benchmark; no reference counterpart. */
+mx_status mx_probe_read(const void *src, int64_t nbytes, uint32_t *sink, mx_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

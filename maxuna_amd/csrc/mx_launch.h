@@ -155,6 +155,8 @@ mx_status launch_check_ids(const uint32_t *ids, int64_t t, int top_k, int n_expe
                            hipStream_t s);
 mx_status launch_add3(const float *a, const float *b, const float *c, int64_t n, float *dst,
                       hipStream_t s);
+// plain streaming read of nbytes (a multiple of 16) from 16-byte-aligned src
+mx_status launch_read_probe(const void *src, int64_t nbytes, uint32_t *sink, hipStream_t s);
 
 // mx_mm.hip -- bucketing + grouped GEMM
 //
