@@ -351,8 +351,9 @@ Plan plan_for(const mx_moe_layer *L, int64_t t) {
     p.fused_router = !p.mm && !p.generic && t <= route_fused_max_t();
     const int64_t slots = L->top_k + (p.shared_in_decode ? 1 : 0);
     const int64_t gu_rb = stack_row_bytes(L->gate), d_rb = stack_row_bytes(L->down);
-    p.vmm = p.fused_router && t >= kVmmMinT && (!p.has_shared || p.shared_in_decode) &&
-            t * slots <= PAIR_ORDER_MAX && L->gate.n_expert <= 1024 &&
+    // (LAGUNA_NO_MM_ID, mm_min_seq < 0, keeps every t on the mat-vec kernels)
+    p.vmm = p.fused_router && L->mm_min_seq >= 0 && t >= kVmmMinT &&
+            (!p.has_shared || p.shared_in_decode) && t * slots <= PAIR_ORDER_MAX && L->gate.n_expert <= 1024 &&
             vmm_supported(L->gate.dtype, L->down.dtype, (int)L->hidden, (int)L->expert_ff, gu_rb, d_rb) &&
             L->expert_ff * gu_rb < ((int64_t)1 << 31) && L->hidden * d_rb < ((int64_t)1 << 31) &&
             (!p.has_shared || (stack_row_bytes(L->shared_gate) == gu_rb && stack_row_bytes(L->shared_down) == d_rb));

@@ -153,3 +153,19 @@ def test_verify_tiles_outlier_channels(dev, orc):
         want, _, _ = orc.moe_layer(spec, layer.keys, layer.router_t, layer.bias, x, ids=ids, w=w)
         r = assert_close(out, want, what=f"C1 outlier verify tiles t={t}")
         _log(f"  {r}")
+
+
+def test_no_mm_id_keeps_verify_blocks_on_the_mat_vecs(dev, orc):
+    """mm_min_seq < 0 (LAGUNA_NO_MM_ID: mul_mv_id everywhere, ops/mod.rs:57-64)
+    keeps a 16-token block on the decode kernels: f32-class again."""
+    spec = CONFIGS["C1"]["spec"]
+    layer = build_layer(spec, seed=1101)
+    layer.block._c.mm_min_seq = -1
+    rng = np.random.default_rng(13)
+    x = outlier_x(rng, (16, spec.hidden))
+    out, ids, w = layer.block.forward(dev_f32(x), return_routing=True)
+    out, ids, w = host(out), host(ids), host(w)
+    want, _, _ = orc.moe_layer(spec, layer.keys, layer.router_t, layer.bias, x, ids=ids, w=w)
+    r = rel_l2(out, want)
+    _log(f"no-mm-id t=16: rel-L2 {r:.2e}")
+    assert r <= 1e-5, f"rel-L2 {r:.3e} is not f32-class"
