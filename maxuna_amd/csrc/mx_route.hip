@@ -346,8 +346,9 @@ __device__ __forceinline__ void norm8(float (&v)[8], const float *alpha, int h0,
     for (int i = 0; i < 8; i++) v[i] = v[i] / m * a[i];
 }
 
-// Block-wide sum of each token's partial (t <= RF_MAX_T, all threads call).
-__device__ __forceinline__ void block_sums(float (&v)[RF_MAX_T], int t, float (*s_red)[RF_THREADS / 64]) {
+// Block-wide sum of the first t partials (all threads call).
+template <int N>
+__device__ __forceinline__ void block_sums(float (&v)[N], int t, float (*s_red)[RF_THREADS / 64]) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     for (int tok = 0; tok < t; tok++) {
         float a = v[tok];
@@ -363,16 +364,23 @@ __device__ __forceinline__ void block_sums(float (&v)[RF_MAX_T], int t, float (*
     __syncthreads();
 }
 
+// EPB: experts per expert block (1, or 4 for t > RF_MAX_T: the block's token
+// rows, loaded once, serve four router rows, and a 16-token block runs 256
+// expert blocks instead of 1024).  Every logit is the same sum in the same
+// order for any EPB (each thread's partial over the same columns, then the same
+// block reduction).
+template <int EPB>
 __global__ void __launch_bounds__(RF_THREADS) k_route_fused(
     const float *__restrict__ x, const float *__restrict__ rms_alpha, float rms_eps, float *__restrict__ x_normed,
     const float *__restrict__ router, const float *__restrict__ bias, int t, int hidden, int n_expert,
     uint8_t *__restrict__ ws, uint8_t *__restrict__ xstage, uint8_t *__restrict__ xstage_gm) {
-    __shared__ float s_red[RF_MAX_T][RF_THREADS / 64];
+    __shared__ float s_red[EPB * RF_MAX_T][RF_THREADS / 64];
     uint64_t *keys = reinterpret_cast<uint64_t *>(ws);
     float *probs = reinterpret_cast<float *>(keys + (int64_t)t * n_expert);
     const int tid = threadIdx.x;
-    // expert blocks: one per (expert, group of RF_MAX_T tokens), each one register pass
-    const int n_tg = (t + RF_MAX_T - 1) / RF_MAX_T, n_eb = n_expert * n_tg;
+    // expert blocks: one per (EPB experts, group of RF_MAX_T tokens), each one register pass
+    const int n_eg = n_expert / EPB;
+    const int n_tg = (t + RF_MAX_T - 1) / RF_MAX_T, n_eb = n_eg * n_tg;
     if ((int)blockIdx.x >= n_eb) {
         // ---- staging blocks: quarter qi = 8 values of token qi / nq
         __shared__ float s_m[RF_TOKENS];
@@ -415,53 +423,62 @@ __global__ void __launch_bounds__(RF_THREADS) k_route_fused(
                           xstage_gm ? xstage_gm + (int64_t)(valid ? tok : 0) * xstage_gm_stride(hidden) : nullptr);
         return;
     }
-    // ---- expert blocks: the expert's router row against its group of RF_MAX_T
+    // ---- expert blocks: the experts' router rows against their group of RF_MAX_T
     // tokens (the groups of one expert read the row from L2 after the first)
-    const int e = blockIdx.x % n_expert, tg = blockIdx.x / n_expert;
-    const float be = bias[e];  // issued early: needed only after the reduction
-    const float *rr = router + (int64_t)e * hidden;
+    const int e0 = (blockIdx.x % n_eg) * EPB, tg = blockIdx.x / n_eg;
+    float be[EPB];  // issued early: needed only after the reduction
+#pragma unroll
+    for (int k = 0; k < EPB; k++) be[k] = bias[e0 + k];
     for (int t0 = tg * RF_MAX_T; t0 < min(t, (tg + 1) * RF_MAX_T); t0 += RF_MAX_T) {
         const int tc = min(RF_MAX_T, t - t0);
         const float *xt = x + (int64_t)t0 * hidden;
-        float dot[RF_MAX_T] = {}, ss[RF_MAX_T] = {};
+        float dot[EPB * RF_MAX_T] = {}, ss[RF_MAX_T] = {};
         for (int c0 = 4 * tid; c0 < hidden; c0 += 4 * RF_THREADS * RF_UNROLL) {
-            float4 rv[RF_UNROLL], av[RF_UNROLL], xv[RF_MAX_T][RF_UNROLL];
+            float4 rv[EPB][RF_UNROLL], av[RF_UNROLL], xv[RF_MAX_T][RF_UNROLL];
 #pragma unroll
             for (int i = 0; i < RF_UNROLL; i++) {
                 const int h = c0 + 4 * RF_THREADS * i;
                 const bool ok = h < hidden;
                 const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-                rv[i] = ok ? *reinterpret_cast<const float4 *>(rr + h) : z;
+#pragma unroll
+                for (int k = 0; k < EPB; k++)
+                    rv[k][i] = ok ? *reinterpret_cast<const float4 *>(router + (int64_t)(e0 + k) * hidden + h) : z;
                 av[i] = (ok && rms_alpha) ? *reinterpret_cast<const float4 *>(rms_alpha + h)
                                           : make_float4(1.f, 1.f, 1.f, 1.f);
 #pragma unroll
-                for (int k = 0; k < RF_MAX_T; k++)
-                    xv[k][i] = (ok && k < tc) ? *reinterpret_cast<const float4 *>(xt + (int64_t)k * hidden + h) : z;
+                for (int j = 0; j < RF_MAX_T; j++)
+                    xv[j][i] = (ok && j < tc) ? *reinterpret_cast<const float4 *>(xt + (int64_t)j * hidden + h) : z;
             }
 #pragma unroll
-            for (int k = 0; k < RF_MAX_T; k++) {
-                if (k >= tc) break;
+            for (int j = 0; j < RF_MAX_T; j++) {
+                if (j >= tc) break;
 #pragma unroll
                 for (int i = 0; i < RF_UNROLL; i++) {
-                    const float4 v = xv[k][i];
-                    ss[k] = __builtin_fmaf(v.x, v.x, ss[k]);
-                    ss[k] = __builtin_fmaf(v.y, v.y, ss[k]);
-                    ss[k] = __builtin_fmaf(v.z, v.z, ss[k]);
-                    ss[k] = __builtin_fmaf(v.w, v.w, ss[k]);
-                    dot[k] = __builtin_fmaf(v.x * av[i].x, rv[i].x, dot[k]);
-                    dot[k] = __builtin_fmaf(v.y * av[i].y, rv[i].y, dot[k]);
-                    dot[k] = __builtin_fmaf(v.z * av[i].z, rv[i].z, dot[k]);
-                    dot[k] = __builtin_fmaf(v.w * av[i].w, rv[i].w, dot[k]);
+                    const float4 v = xv[j][i];
+                    ss[j] = __builtin_fmaf(v.x, v.x, ss[j]);
+                    ss[j] = __builtin_fmaf(v.y, v.y, ss[j]);
+                    ss[j] = __builtin_fmaf(v.z, v.z, ss[j]);
+                    ss[j] = __builtin_fmaf(v.w, v.w, ss[j]);
+#pragma unroll
+                    for (int k = 0; k < EPB; k++) {
+                        float &d = dot[k * RF_MAX_T + j];
+                        d = __builtin_fmaf(v.x * av[i].x, rv[k][i].x, d);
+                        d = __builtin_fmaf(v.y * av[i].y, rv[k][i].y, d);
+                        d = __builtin_fmaf(v.z * av[i].z, rv[k][i].z, d);
+                        d = __builtin_fmaf(v.w * av[i].w, rv[k][i].w, d);
+                    }
                 }
             }
         }
-        block_sums(dot, tc, s_red);
+        block_sums(dot, EPB * RF_MAX_T, s_red);
         if (rms_alpha) block_sums(ss, tc, s_red);
-        if (tid < tc) {
-            const float lg = rms_alpha ? dot[tid] / sqrtf(ss[tid] / (float)hidden + rms_eps) : dot[tid];
+        const int k = tid / RF_MAX_T, j = tid % RF_MAX_T;
+        if (k < EPB && j < tc) {
+            const float d = dot[k * RF_MAX_T + j];
+            const float lg = rms_alpha ? d / sqrtf(ss[j] / (float)hidden + rms_eps) : d;
             const float p = 1.0f / (expf(-lg) + 1.0f);  // sigmoid (moe.rs:101)
-            const int64_t o = (int64_t)(t0 + tid) * n_expert + e;
-            keys[o] = sel_key(p + be, e);
+            const int64_t o = (int64_t)(t0 + j) * n_expert + e0 + k;
+            keys[o] = sel_key(p + be[k], e0 + k);
             probs[o] = p;
         }
     }
@@ -479,9 +496,14 @@ mx_status launch_route_fused(const float *x, const float *rms_alpha, float rms_e
     const int nq = t * (hidden / 8);
     const int n_stage = (xstage || x_normed) ? (nq + RF_THREADS - 1) / RF_THREADS : 0;
     const int n_tg = (t + RF_MAX_T - 1) / RF_MAX_T;
-    hipLaunchKernelGGL(k_route_fused, dim3((unsigned)(n_expert * n_tg + n_stage)), dim3(RF_THREADS), 0, s, x, rms_alpha,
-                       rms_eps, x_normed, router, bias, t, hidden, n_expert, reinterpret_cast<uint8_t *>(ws),
-                       xstage, xstage_gm);
+    if (t > RF_MAX_T && n_expert % 4 == 0)
+        hipLaunchKernelGGL(k_route_fused<4>, dim3((unsigned)(n_expert / 4 * n_tg + n_stage)), dim3(RF_THREADS), 0, s,
+                           x, rms_alpha, rms_eps, x_normed, router, bias, t, hidden, n_expert,
+                           reinterpret_cast<uint8_t *>(ws), xstage, xstage_gm);
+    else
+        hipLaunchKernelGGL(k_route_fused<1>, dim3((unsigned)(n_expert * n_tg + n_stage)), dim3(RF_THREADS), 0, s, x,
+                           rms_alpha, rms_eps, x_normed, router, bias, t, hidden, n_expert,
+                           reinterpret_cast<uint8_t *>(ws), xstage, xstage_gm);
     MX_LAUNCH("k_route_fused");
     return MX_OK;
 }

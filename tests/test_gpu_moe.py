@@ -340,3 +340,17 @@ def test_decode_down_q6_hidden_off_the_verify_tile(dev, orc):
         x = make_x(spec, 800 + t, t)
         out, ids, w = run_block(layer, x)
         oracle_check(orc, layer, x, out, ids, w, f"hidden 1056 t={t}")
+
+
+def test_router_expert_groups_bit_identical(dev):
+    """Blocks of more than 4 tokens run the fused router with four experts per
+    workgroup (the token rows loaded once for four router rows); every logit is
+    the same sum in the same order, so the routing of the first tokens must be
+    bit-identical to a 4-token block's (one expert per workgroup)."""
+    spec = CONFIGS["C2"]["spec"]
+    layer = build_layer(spec, seed=1003)
+    x = make_x(spec, 21, 16)
+    _, ids16, w16 = run_block(layer, x)
+    _, ids4, w4 = run_block(layer, x[:4])
+    assert np.array_equal(ids16[:4], ids4)
+    assert np.array_equal(w16[:4].view(np.uint32), w4.view(np.uint32))
