@@ -554,12 +554,15 @@ mx_status moe_forward_impl(const mx_moe_layer *L, const float *x, int64_t t, con
     const float *xin = x;
 
     // routing (+ the RMSNorm of the FFN half when requested)
+    // (verify tiles without RMSNorm: the router also writes the f16 x rows)
+    const bool x16_in_router = p.vmm && !L->rms_alpha;
     if (p.fused_router) {
         // logits -> keys/probs; the router also stages the (normalised) rows for the
         // decode expert kernels.  The top-k is its own launch (k_decode_select, below).
         for (int r = 0; r < rep(0); r++)
             MX_TRY(launch_route_fused(x, L->rms_alpha, L->rms_eps, o.x_normed, L->router, L->exp_probs_b, (int)t,
-                                      (int)H, (int)E, o.route_ws, o.xstage, o.xstage_gm, s));
+                                      (int)H, (int)E, o.route_ws, o.xstage, o.xstage_gm, s,
+                                      x16_in_router ? o.x16 : nullptr, x16_in_router ? o.x16s : nullptr));
         if (L->rms_alpha) xin = o.x_normed;
     } else {
         if (L->rms_alpha) {
@@ -668,7 +671,7 @@ mx_status moe_forward_impl(const mx_moe_layer *L, const float *x, int64_t t, con
             g.runs = o.runs;
             g.out = o.act;
             for (int r = 0; r < rep(2); r++) {
-                MX_TRY(launch_to_f16_rows(xin, t, (int)H, nullptr, o.x16, o.x16s, s));
+                if (!x16_in_router) MX_TRY(launch_to_f16_rows(xin, t, (int)H, nullptr, o.x16, o.x16s, s));
                 MX_TRY(launch_vmm(L->gate.dtype, true, g, np, s));
             }
             MX_STAGE();

@@ -40,6 +40,7 @@
 #include "mx_launch.h"
 #include "mx_dma.h"
 #include "mx_wb.h"
+#include "mx_f16row.h"
 
 namespace mx {
 
@@ -432,10 +433,7 @@ __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
     }
 }
 
-// ---- f32 rows -> scaled f16 rows ----------------------------------------------------
-// RPT > 0: k <= 1024 * RPT; the row's float4s stay in registers between the
-// max pass and the conversion (all loads issued up front).  RPT == 0: any k,
-// the row is read twice.
+// ---- f32 rows -> scaled f16 rows (body in mx_f16row.h) -------------------------------
 template <int RPT>
 __global__ void __launch_bounds__(256) k_to_f16_rows(const float *__restrict__ x, int k,
                                                      const int32_t *__restrict__ count,
@@ -443,50 +441,7 @@ __global__ void __launch_bounds__(256) k_to_f16_rows(const float *__restrict__ x
     const int64_t row = blockIdx.x;
     if (count && row >= *count) return;
     __shared__ float s_red[4];
-    const float4 *xr = reinterpret_cast<const float4 *>(x + row * k);
-    const int n4 = k / 4;
-    auto amax4 = [](const float4 &v) { return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))); };
-    float mx = 0.f;
-    float4 cache[RPT > 0 ? RPT : 1];
-    if constexpr (RPT > 0) {
-#pragma unroll
-        for (int j = 0; j < RPT; j++) {
-            const int i = threadIdx.x + 256 * j;
-            cache[j] = i < n4 ? xr[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-#pragma unroll
-        for (int j = 0; j < RPT; j++) mx = fmaxf(mx, amax4(cache[j]));
-    } else {
-        for (int i = threadIdx.x; i < n4; i += 256) mx = fmaxf(mx, amax4(xr[i]));
-    }
-    mx = fmaxf(mx, lane_partner<32>(mx));
-    mx = fmaxf(mx, lane_partner<16>(mx));
-    mx = fmaxf(mx, lane_partner<8>(mx));
-    mx = fmaxf(mx, lane_partner<4>(mx));
-    mx = fmaxf(mx, lane_partner<2>(mx));
-    mx = fmaxf(mx, lane_partner<1>(mx));
-    if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
-    // exponent so that max * 2^-ex lies in [2^14, 2^15)
-    const int ex = mx > 0.f ? ilogbf(mx) - 14 : 0;
-    const float inv = ldexpf(1.0f, -ex);
-    half4_t *yr = reinterpret_cast<half4_t *>(y + row * k);
-    auto put = [&](int i, const float4 &v) {
-        const half2_t lo = __builtin_convertvector((float2_t){v.x * inv, v.y * inv}, half2_t);
-        const half2_t hi = __builtin_convertvector((float2_t){v.z * inv, v.w * inv}, half2_t);
-        yr[i] = (half4_t){lo[0], lo[1], hi[0], hi[1]};
-    };
-    if constexpr (RPT > 0) {
-#pragma unroll
-        for (int j = 0; j < RPT; j++) {
-            const int i = threadIdx.x + 256 * j;
-            if (i < n4) put(i, cache[j]);
-        }
-    } else {
-        for (int i = threadIdx.x; i < n4; i += 256) put(i, xr[i]);
-    }
-    if (threadIdx.x == 0) scale[row] = ldexpf(1.0f, ex);
+    f16_row<RPT>(x + row * k, k, y + row * k, scale + row, s_red);
 }
 
 // out = residual + (sum_s w_s down_s) + shared   (moe.rs:78; combine.metal:16-40 order)

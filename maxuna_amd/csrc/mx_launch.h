@@ -132,14 +132,16 @@ mx_status launch_route_select(const float *logits, const float *bias, int t, int
 // Decode router, first half: RMSNorm (optional) + logits -> sigmoid
 // probabilities and selection sort keys for t tokens (ws: keys u64 [t, E] |
 // probs f32 [t, E]); also stages the (normalised) rows into `xstage`
-// (mx_stage.h layout) and/or writes them to `x_normed` when non-NULL.  The
-// top-k runs in k_decode_select (launch_decode_select).
+// (mx_stage.h layout) and/or writes them to `x_normed` when non-NULL, and (no
+// RMSNorm) as f16 rows times a per-row power of two into x16 / x16s when
+// non-NULL.  The top-k runs in k_decode_select (launch_decode_select).
 size_t route_fused_ws_bytes(int t, int hidden, int n_expert);
 int route_fused_max_t();
 mx_status launch_route_fused(const float *x, const float *rms_alpha, float rms_eps,
                              float *x_normed, const float *router, const float *bias, int t,
                              int hidden, int n_expert, void *ws, uint8_t *xstage, uint8_t *xstage_gm,
-                             hipStream_t s);
+                             hipStream_t s,
+                             _Float16 *x16 = nullptr, float *x16s = nullptr);
 // Stages t rows of k values (mx_stage.h layout, xstage_bytes(k) per row).
 // xstage_gm: optional group-major copy (mx_stage.h; k % 64 == 0)
 mx_status launch_stage_rows(const float *x, int t, int k, uint8_t *xstage, uint8_t *xstage_gm, hipStream_t s);

@@ -14,6 +14,7 @@
 // its matmul (moe.rs:43), which this layout makes unnecessary.
 #include "mx_launch.h"
 #include "mx_stage.h"
+#include "mx_f16row.h"
 #include "mx_select.h"
 #include "mx_dma.h"
 
@@ -326,6 +327,8 @@ mx_status launch_route_logits(const float *x, const float *router, int t, int hi
 // Blocks [n_expert, n_expert + n_stage): stage the (normalised) token rows for
 // the expert kernels (mx_stage.h layout, one row of xstage_bytes(hidden) per
 // token in `xstage`) and, if requested, write them as f32 to `x_normed`.
+// Then, when x16 is given (no RMSNorm), one block per token writes its row as
+// f16 times a power of two (mx_f16row.h) for the MFMA verify tiles.
 constexpr int RF_MAX_T = 4;     // tokens per register pass
 constexpr int RF_TOKENS = 32;   // tokens per launch
 constexpr int RF_THREADS = 256;
@@ -373,7 +376,8 @@ template <int EPB>
 __global__ void __launch_bounds__(RF_THREADS) k_route_fused(
     const float *__restrict__ x, const float *__restrict__ rms_alpha, float rms_eps, float *__restrict__ x_normed,
     const float *__restrict__ router, const float *__restrict__ bias, int t, int hidden, int n_expert,
-    uint8_t *__restrict__ ws, uint8_t *__restrict__ xstage, uint8_t *__restrict__ xstage_gm) {
+    uint8_t *__restrict__ ws, uint8_t *__restrict__ xstage, uint8_t *__restrict__ xstage_gm,
+    _Float16 *__restrict__ x16, float *__restrict__ x16s, int n_stage) {
     __shared__ float s_red[EPB * RF_MAX_T][RF_THREADS / 64];
     uint64_t *keys = reinterpret_cast<uint64_t *>(ws);
     float *probs = reinterpret_cast<float *>(keys + (int64_t)t * n_expert);
@@ -381,6 +385,15 @@ __global__ void __launch_bounds__(RF_THREADS) k_route_fused(
     // expert blocks: one per (EPB experts, group of RF_MAX_T tokens), each one register pass
     const int n_eg = n_expert / EPB;
     const int n_tg = (t + RF_MAX_T - 1) / RF_MAX_T, n_eb = n_eg * n_tg;
+    if ((int)blockIdx.x >= n_eb + n_stage) {
+        // ---- f16 row blocks: token row -> f16 times a power of two (x16 != NULL,
+        // no RMSNorm), the operand of the MFMA verify tiles
+        const int tok = blockIdx.x - n_eb - n_stage;
+        if (hidden <= 4096) f16_row<4>(x + (int64_t)tok * hidden, hidden, x16 + (int64_t)tok * hidden, x16s + tok,
+                                       &s_red[0][0]);
+        else f16_row<0>(x + (int64_t)tok * hidden, hidden, x16 + (int64_t)tok * hidden, x16s + tok, &s_red[0][0]);
+        return;
+    }
     if ((int)blockIdx.x >= n_eb) {
         // ---- staging blocks: quarter qi = 8 values of token qi / nq
         __shared__ float s_m[RF_TOKENS];
@@ -488,22 +501,25 @@ int route_fused_max_t() { return RF_TOKENS; }
 
 mx_status launch_route_fused(const float *x, const float *rms_alpha, float rms_eps, float *x_normed,
                              const float *router, const float *bias, int t, int hidden, int n_expert, void *ws,
-                             uint8_t *xstage, uint8_t *xstage_gm, hipStream_t s) {
+                             uint8_t *xstage, uint8_t *xstage_gm, hipStream_t s, _Float16 *x16, float *x16s) {
     if (t == 0) return MX_OK;
     if (t > RF_TOKENS) return fail(MX_ERR_SHAPE, "fused router handles at most %d tokens", RF_TOKENS);
     if (hidden % 32) return fail(MX_ERR_SHAPE, "fused router needs hidden %% 32 == 0");
     if (xstage_gm && hidden % 64) return fail(MX_ERR_SHAPE, "group-major staging needs hidden %% 64 == 0");
+    if (x16 && (rms_alpha || !x16s || hidden % 4))
+        return fail(MX_ERR_SHAPE, "fused router f16 rows: no RMSNorm, a scale array and hidden %% 4 == 0");
+    const int n_x16 = x16 ? t : 0;
     const int nq = t * (hidden / 8);
     const int n_stage = (xstage || x_normed) ? (nq + RF_THREADS - 1) / RF_THREADS : 0;
     const int n_tg = (t + RF_MAX_T - 1) / RF_MAX_T;
     if (t > RF_MAX_T && n_expert % 4 == 0)
-        hipLaunchKernelGGL(k_route_fused<4>, dim3((unsigned)(n_expert / 4 * n_tg + n_stage)), dim3(RF_THREADS), 0, s,
-                           x, rms_alpha, rms_eps, x_normed, router, bias, t, hidden, n_expert,
-                           reinterpret_cast<uint8_t *>(ws), xstage, xstage_gm);
+        hipLaunchKernelGGL(k_route_fused<4>, dim3((unsigned)(n_expert / 4 * n_tg + n_stage + n_x16)), dim3(RF_THREADS),
+                           0, s, x, rms_alpha, rms_eps, x_normed, router, bias, t, hidden, n_expert,
+                           reinterpret_cast<uint8_t *>(ws), xstage, xstage_gm, x16, x16s, n_stage);
     else
-        hipLaunchKernelGGL(k_route_fused<1>, dim3((unsigned)(n_expert * n_tg + n_stage)), dim3(RF_THREADS), 0, s, x,
-                           rms_alpha, rms_eps, x_normed, router, bias, t, hidden, n_expert,
-                           reinterpret_cast<uint8_t *>(ws), xstage, xstage_gm);
+        hipLaunchKernelGGL(k_route_fused<1>, dim3((unsigned)(n_expert * n_tg + n_stage + n_x16)), dim3(RF_THREADS), 0,
+                           s, x, rms_alpha, rms_eps, x_normed, router, bias, t, hidden, n_expert,
+                           reinterpret_cast<uint8_t *>(ws), xstage, xstage_gm, x16, x16s, n_stage);
     MX_LAUNCH("k_route_fused");
     return MX_OK;
 }

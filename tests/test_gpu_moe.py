@@ -184,6 +184,23 @@ def test_chain_with_rmsnorm_and_residual(dev, orc):
     assert_close(got, x, what="3-layer chain")
 
 
+def test_rmsnorm_verify_tiles(dev, orc):
+    """A 20-token block with the FFN RMSNorm on the MFMA verify tiles: the f16 x
+    rows come from the normalised rows (a separate conversion after the router,
+    which writes them), not from the router's own f16 rows."""
+    spec = CONFIGS["C4"]["spec"]
+    layer = build_layer(spec, seed=2001, rms=True)
+    x = make_x(spec, 24, 20)
+    out, ids, w = layer.block.forward(dev_f32(x), residual=dev_f32(x), return_routing=True)
+    out, ids, w = host(out), host(ids), host(w)
+    xn = orc.rmsnorm(x, np.ones(spec.hidden, np.float32), 1e-6)
+    logits = orc.route_logits(xn, layer.router_t)
+    oid, _ = orc.route_from_logits(logits, layer.bias, spec.top_k, spec.weights_scale, spec.weights_norm)
+    assert check_ids(ids, oid, selection_margin(logits, layer.bias, spec.top_k)) <= 1
+    y, _, _ = orc.moe_layer(spec, layer.keys, layer.router_t, layer.bias, xn, ids=ids, w=w)
+    assert_close(out, (x + y).astype(np.float32), what="rmsnorm verify t=20")
+
+
 def test_wide_rows(dev, orc):
     """hidden = 5120 and ff = 2304: Q4_K rows too wide for the fused decode
     kernels' LDS ring.  Decode (t = 1) and verify (t = 6) take the f32 gather
