@@ -179,12 +179,15 @@ def bench_decode(args):
     # per-kernel time inside the replayed pipeline: the plain rotation minus the
     # rotation with one stage's kernel left out (HIP events on the stream).  Leaving
     # a launch out, unlike launching it twice, keeps every weight byte an HBM read.
-    reps = max(4, replays // 4)
-    base_us = graph_us(lambda: [forward_repeat(layers[i].block, xs[i], outs[i], -1, 1) for i in range(L)], reps)
+    # (base and skip graphs measured alternately three times, the median of the
+    # differences: single pairs moved by 1-2 us from run to run)
+    reps = max(32, replays)
+    base_fn = lambda: [forward_repeat(layers[i].block, xs[i], outs[i], -1, 1) for i in range(L)]  # noqa: E731
     st = []
     for stage in range(4):
-        skip = graph_us(lambda: [forward_repeat(layers[i].block, xs[i], outs[i], stage, 0) for i in range(L)], reps)
-        st.append((base_us - skip) / L * 1e-3)  # ms per launch
+        skip_fn = lambda: [forward_repeat(layers[i].block, xs[i], outs[i], stage, 0) for i in range(L)]  # noqa: E731
+        diffs = [graph_us(base_fn, reps) - graph_us(skip_fn, reps) for _ in range(3)]
+        st.append(float(np.median(diffs)) / L * 1e-3)  # ms per launch
     # eager per-stage HIP events (include the dispatch gap before each kernel)
     eager = np.array([profiled(layers[r % L].block, xs[r % L], outs[r % L], 1)
                       for r in range(max(1, args.profile_iters))]).mean(0)
