@@ -111,6 +111,60 @@ def read_probe():
         log(f"read probe {name}: {us:.2f} us per read, {n / (us * 1e-6) / 1e9:.0f} GB/s")
 
 
+def library_gemm():
+    """The vendor library's f16 GEMMs (torch.mm -> hipBLASLt) on the C3 prefill's own
+    shapes: the per-expert row counts of the C3 layer's routing (routed experts + the
+    shared expert's 2048 rows), gate+up [m x 4096] x [4096 x 3072] and down
+    [m x 1536] x [1536 x 4096] per expert, plus one GEMM over all 22,528 rows.  Plain
+    f16 operands (no dequantisation, no gather): what a library GEMM reaches on this
+    work, next to the quantised grouped GEMM's figures."""
+    import torch
+    from maxuna_amd.synth import CONFIGS, build_layer, make_x
+    spec = CONFIGS["C3"]["spec"]
+    t = 2048
+    layer = build_layer(spec, seed=5151)
+    x = torch.from_numpy(make_x(spec, 88, t)).cuda()
+    _, ids, _ = layer.block.forward(x, return_routing=True)
+    cnt = torch.bincount(ids.view(torch.int32).long().flatten(), minlength=spec.n_expert)
+    rows = [int(c) for c in cnt.tolist() if c > 0] + ([t] if spec.shared else [])
+    del layer
+    h, ff = spec.hidden, spec.ff
+    g = torch.Generator(device="cuda").manual_seed(7)
+    def rnd(*shape):
+        return torch.randn(*shape, device="cuda", dtype=torch.float16, generator=g)
+    wgu = [rnd(2 * ff, h) for _ in rows]
+    wdn = [rnd(h, ff) for _ in rows]
+    agu = [rnd(m, h) for m in rows]
+    adn = [rnd(m, ff) for m in rows]
+    ogu = [torch.empty(m, 2 * ff, device="cuda", dtype=torch.float16) for m in rows]
+    odn = [torch.empty(m, h, device="cuda", dtype=torch.float16) for m in rows]
+    big_a = rnd(sum(rows), h)
+    big_o = torch.empty(sum(rows), 2 * ff, device="cuda", dtype=torch.float16)
+
+    def timed(fn, reps=10):
+        for _ in range(3):
+            fn()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(reps):
+            fn()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) * 1e3 / reps
+
+    n = sum(rows)
+    fl_gu, fl_dn = 2 * n * 2 * ff * h, 2 * n * ff * h
+    us = timed(lambda: [torch.mm(a, w.t(), out=o) for a, w, o in zip(agu, wgu, ogu)])
+    log(f"library f16 GEMM gate+up, {len(rows)} experts (rows {min(rows)}..{max(rows)}, {n} total): "
+        f"{us:.0f} us, {fl_gu / us / 1e6:.0f} TFLOP/s")
+    us = timed(lambda: [torch.mm(a, w.t(), out=o) for a, w, o in zip(adn, wdn, odn)])
+    log(f"library f16 GEMM down, per expert: {us:.0f} us, {fl_dn / us / 1e6:.0f} TFLOP/s")
+    us = timed(lambda: torch.mm(big_a, wgu[0].t(), out=big_o))
+    log(f"library f16 GEMM gate+up as one [{n} x {h}] x [{h} x {2 * ff}]: {us:.0f} us, "
+        f"{fl_gu / us / 1e6:.0f} TFLOP/s")
+
+
 def graph_us(fn, replays):
     """Average time of one replay of the graph captured from fn(), us."""
     import torch
@@ -408,6 +462,8 @@ def main():
     ap.add_argument("--no-chain", action="store_true", help="skip the C4 chain and lm_head figures (keep C2)")
     ap.add_argument("--read-probe", action="store_true",
                     help="only time plain streaming reads of the expert kernels' sizes (achievable HBM read rate)")
+    ap.add_argument("--library-gemm", action="store_true",
+                    help="only time the vendor library's f16 GEMMs on the C3 prefill's per-expert shapes")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="only run N device-to-device copies of this many MB (HBM counter calibration) and exit")
     args = ap.parse_args()
@@ -419,6 +475,9 @@ def main():
     torch.cuda.set_device(0)
     if args.read_probe:
         read_probe()
+        return
+    if args.library_gemm:
+        library_gemm()
         return
     if args.copy_probe_mb:
         # a plain copy of known size: FETCH_SIZE / WRITE_SIZE of its dispatches calibrate
