@@ -712,14 +712,17 @@ static mx_status launch_mv_dt(const MvArgs &a, dim3 grid, hipStream_t s) {
 // MVQ6_RPW rows of one (token, slot) pair in batches through two LDS buffers of
 // its own (batch b + 1 in flight while b is contracted); the workgroup stages the
 // pair's activation row once.  Same per-row arithmetic and 32-lane sum as
-// k_mul_mv_id (Q<kQ6_K>::dot, reduce_tuples).
+// k_mul_mv_id (Q<kQ6_K>::dot, reduce_tuples).  The rows per wave (nb batches) are
+// chosen at launch so that the grid is one round of resident workgroups: with a
+// fixed 16 rows the lm_head's 1568 workgroups ran as 2.04 rounds of 768, the last
+// round almost empty.
 #ifndef MX_MV_Q6
 #define MX_MV_Q6 1
 #endif
 #ifndef MX_MVQ6_RPW
 #define MX_MVQ6_RPW 16
 #endif
-constexpr int MVQ6_RPW = MX_MVQ6_RPW;  // rows per wave
+constexpr int MVQ6_RPW = MX_MVQ6_RPW;  // the fewest rows per wave
 
 template <int NG, int P> struct MvQ6 {
     static constexpr int K = 32 * P * NG, RB = K / 256 * 210, RPI = 64 / P;
@@ -727,10 +730,12 @@ template <int NG, int P> struct MvQ6 {
     static_assert((RPI * RB) % 16 == 0 && RB % 4 == 0, "batches start 16-byte aligned, rows 4-byte aligned");
     static_assert(MVQ6_RPW % RPI == 0 && NB % 2 == 0, "whole batch pairs per wave");
 };
+// nb: batches per wave (even, >= MvQ6::NB)
 template <int NG, int P>
-__global__ void __launch_bounds__(64 * WAVES) k_mv_q6(MvArgs a) {
+__global__ void __launch_bounds__(64 * WAVES) k_mv_q6(MvArgs a, int nb) {
     using G = MvQ6<NG, P>;
-    constexpr int DT = kQ6_K, RB = G::RB, RPI = G::RPI, NI = G::NI, BCH = G::BCH, NB = G::NB;
+    constexpr int DT = kQ6_K, RB = G::RB, RPI = G::RPI, NI = G::NI, BCH = G::BCH;
+    const int rpw = nb * RPI;
     __shared__ __attribute__((aligned(16))) uint8_t ring0[WAVES][NI * 1024];
     __shared__ __attribute__((aligned(16))) uint8_t ring1[WAVES][NI * 1024];
     __shared__ __attribute__((aligned(16))) uint8_t stg[(xstage_bytes(G::K) + 15) & ~15];
@@ -743,9 +748,9 @@ __global__ void __launch_bounds__(64 * WAVES) k_mv_q6(MvArgs a) {
     }
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int sub = lane & (P - 1), rsub = lane / P;
-    const int r0 = (blockIdx.x * WAVES + wave) * MVQ6_RPW;
+    const int r0 = (blockIdx.x * WAVES + wave) * rpw;
     // the last batch that holds a row of this matrix (a wave past the end re-copies it)
-    const int nbv = r0 < a.n_out ? (min(a.n_out - r0, MVQ6_RPW) + RPI - 1) / RPI : 1;
+    const int nbv = r0 < a.n_out ? (min(a.n_out - r0, rpw) + RPI - 1) / RPI : 1;
     const int rlast = r0 < a.n_out ? r0 : ((a.n_out - 1) / RPI) * RPI;
     const float *xrow = a.x + ((int64_t)tok * a.x_per_row + (a.x_per_row == 1 ? 0 : slot)) * a.k;
     const uint8_t *wp = a.w + (int64_t)e * a.expert_bytes + (int64_t)rlast * RB;
@@ -820,7 +825,7 @@ __global__ void __launch_bounds__(64 * WAVES) k_mv_q6(MvArgs a) {
         issue(bi + 2, buf);
     };
 #pragma unroll 1
-    for (int bi = 0; bi < NB; bi += 2) {
+    for (int bi = 0; bi < nb; bi += 2) {
         batch(bi, b0);
         batch(bi + 1, b1);
     }
@@ -841,15 +846,41 @@ static bool mv_q6_pick(const MvArgs &a, int &ng, int &p) {
     // whole batches: a batch's copy never reads past the matrix's last row
     return a.n_out % (64 / p) == 0;
 }
+// resident workgroups of k_mv_q6<NG, P> on the current device (0: unknown)
+template <int NG, int P> static int mv_q6_resident() {
+    static int cache[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    if (!cache[dev]) {
+        int per_cu = 0, cus = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_mv_q6<NG, P>, 64 * WAVES, 0) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            return 0;
+        cache[dev] = per_cu > 0 && cus > 0 ? per_cu * cus : -1;
+    }
+    return cache[dev] > 0 ? cache[dev] : 0;
+}
+template <int NG, int P> static void launch_mv_q6_v(const MvArgs &a, hipStream_t s) {
+    using G = MvQ6<NG, P>;
+    const int64_t pairs = (int64_t)a.t * a.top_k;
+    // batches per wave: at least G::NB, else enough that every workgroup of the grid
+    // is resident at once (the rows of all pairs over the resident waves)
+    const int64_t res = mv_q6_resident<NG, P>();
+    int64_t nb = G::NB;
+    if (res > 0) {
+        const int64_t rows_per_wave = (a.n_out * pairs + res * WAVES - 1) / (res * WAVES);
+        const int64_t want = (rows_per_wave + G::RPI - 1) / G::RPI;
+        nb = want > nb ? (want + 1) & ~int64_t(1) : nb;
+    }
+    const int64_t rpw = nb * G::RPI;
+    const dim3 grid((unsigned)((a.n_out + WAVES * rpw - 1) / (WAVES * rpw)), (unsigned)pairs);
+    hipLaunchKernelGGL((k_mv_q6<NG, P>), grid, dim3(64 * WAVES), 0, s, a, (int)nb);
+}
 static mx_status launch_mv_q6(const MvArgs &a, int ng, int p, hipStream_t s) {
-    const unsigned tiles = (unsigned)((a.n_out + WAVES * MVQ6_RPW - 1) / (WAVES * MVQ6_RPW));
-    const dim3 grid(tiles, (unsigned)(a.t * a.top_k));
-#define MX_Q6(NG, P) hipLaunchKernelGGL((k_mv_q6<NG, P>), grid, dim3(64 * WAVES), 0, s, a)
-    if (ng == 3 && p == 16) MX_Q6(3, 16);
-    else if (ng == 2) MX_Q6(2, 32);
-    else if (ng == 3) MX_Q6(3, 32);
-    else MX_Q6(4, 32);
-#undef MX_Q6
+    if (ng == 3 && p == 16) launch_mv_q6_v<3, 16>(a, s);
+    else if (ng == 2) launch_mv_q6_v<2, 32>(a, s);
+    else if (ng == 3) launch_mv_q6_v<3, 32>(a, s);
+    else launch_mv_q6_v<4, 32>(a, s);
     MX_LAUNCH("k_mv_q6");
     return MX_OK;
 }
