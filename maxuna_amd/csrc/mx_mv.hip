@@ -735,7 +735,7 @@ template <int NG, int P>
 __global__ void __launch_bounds__(64 * WAVES) k_mv_q6(MvArgs a, int nb) {
     using G = MvQ6<NG, P>;
     constexpr int DT = kQ6_K, RB = G::RB, RPI = G::RPI, NI = G::NI, BCH = G::BCH;
-    const int rpw = nb * RPI;
+    const int nbt = a.n_out / RPI;  // batches of the matrix (whole: the launcher checks)
     __shared__ __attribute__((aligned(16))) uint8_t ring0[WAVES][NI * 1024];
     __shared__ __attribute__((aligned(16))) uint8_t ring1[WAVES][NI * 1024];
     __shared__ __attribute__((aligned(16))) uint8_t stg[(xstage_bytes(G::K) + 15) & ~15];
@@ -748,17 +748,18 @@ __global__ void __launch_bounds__(64 * WAVES) k_mv_q6(MvArgs a, int nb) {
     }
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int sub = lane & (P - 1), rsub = lane / P;
-    const int r0 = (blockIdx.x * WAVES + wave) * rpw;
-    // the last batch that holds a row of this matrix (a wave past the end re-copies it)
-    const int nbv = r0 < a.n_out ? (min(a.n_out - r0, rpw) + RPI - 1) / RPI : 1;
-    const int rlast = r0 < a.n_out ? r0 : ((a.n_out - 1) / RPI) * RPI;
+    // grid-strided batches: the wave's batch bi is gw + bi * NW, so the waves of the
+    // grid stream neighbouring batches together (with one contiguous run of rows per
+    // wave the lm_head's copies alone took 51 us, grid-strided 46.5 us); a batch
+    // past the end re-copies the matrix's last batch and stores nothing
+    const int gw = blockIdx.x * WAVES + wave, NW = gridDim.x * WAVES;
     const float *xrow = a.x + ((int64_t)tok * a.x_per_row + (a.x_per_row == 1 ? 0 : slot)) * a.k;
-    const uint8_t *wp = a.w + (int64_t)e * a.expert_bytes + (int64_t)rlast * RB;
+    const uint8_t *wp = a.w + (int64_t)e * a.expert_bytes;
     uint8_t *const b0 = ring0[wave], *const b1 = ring1[wave];
     // every lane issues every copy (spare lanes repeat the batch's last chunk into
     // the buffer's unused tail): no branch around a copy, so the counts stay exact
     auto issue = [&](int bi, uint8_t *dst) {
-        const uint8_t *src = wp + min(bi, nbv - 1) * (RPI * RB);
+        const uint8_t *src = wp + (int64_t)min(gw + bi * NW, nbt - 1) * (RPI * RB);
 #pragma unroll
         for (int q = 0; q < NI; q++) {
             const int ci = min(64 * q + lane, BCH - 1);
@@ -803,26 +804,30 @@ __global__ void __launch_bounds__(64 * WAVES) k_mv_q6(MvArgs a, int nb) {
         wait_vmcnt(NI);  // batch bi has landed (bi + 1 is in flight)
         const uint8_t *rl = buf + rsub * RB;
         float acc[1][1];
-        float v = 0.f;
+        // the batch's fields into registers, then the copy of batch bi + 2 into the
+        // same buffer, then the dots: the copy is in flight while they run (175
+        // VGPRs, 2 waves/SIMD; forced to 3 it spills and takes 64 us instead of 54)
+        typename Q<DT>::Raw r[NG];
 #pragma unroll
         for (int jg = 0; jg < NG; jg++) {
-            typename Q<DT>::Raw r;
-            Q<DT>::ld3(rl + oa[jg], r.a);
-            Q<DT>::ld3(rl + oa[jg] + 32, r.b);
-            Q<DT>::ld3(rl + ohq[jg], r.hq);
-            Q<DT>::ld3(rl + osc[jg], r.sc);
-            r.d = ld_u16(rl + od[jg]);
-            r.sh = sh[jg];
-            v += Q<DT>::dot(r, sub + P * jg, xs[jg]);
+            Q<DT>::ld3(rl + oa[jg], r[jg].a);
+            Q<DT>::ld3(rl + oa[jg] + 32, r[jg].b);
+            Q<DT>::ld3(rl + ohq[jg], r[jg].hq);
+            Q<DT>::ld3(rl + osc[jg], r[jg].sc);
+            r[jg].d = ld_u16(rl + od[jg]);
+            r[jg].sh = sh[jg];
         }
+        wait_lgkmcnt0();  // every read of the buffer returned before it is overwritten
+        issue(bi + 2, buf);
+        float v = 0.f;
+#pragma unroll
+        for (int jg = 0; jg < NG; jg++) v += Q<DT>::dot(r[jg], sub + P * jg, xs[jg]);
         acc[0][0] = v;
         int which;
         bool leader;
         reduce_tuples<1, 1>(acc, P, sub, which, leader);
-        const int row = r0 + bi * RPI + rsub;
-        if (leader && bi < nbv && row < a.n_out && r0 < a.n_out) dst[row] = acc[0][0];
-        wait_lgkmcnt0();  // every read of the buffer returned before it is overwritten
-        issue(bi + 2, buf);
+        const int b = gw + bi * NW;
+        if (leader && b < nbt) dst[b * RPI + rsub] = acc[0][0];
     };
 #pragma unroll 1
     for (int bi = 0; bi < nb; bi += 2) {
