@@ -462,6 +462,8 @@ def main():
     ap.add_argument("--no-chain", action="store_true", help="skip the C4 chain and lm_head figures (keep C2)")
     ap.add_argument("--read-probe", action="store_true",
                     help="only time plain streaming reads of the expert kernels' sizes (achievable HBM read rate)")
+    ap.add_argument("--lm-head", action="store_true",
+                    help="only time the plain Q6_K mat-vec at the lm_head shape (profiling)")
     ap.add_argument("--library-gemm", action="store_true",
                     help="only time the vendor library's f16 GEMMs on the C3 prefill's per-expert shapes")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
@@ -478,6 +480,9 @@ def main():
         return
     if args.library_gemm:
         library_gemm()
+        return
+    if args.lm_head:
+        bench_lm_head(args)
         return
     if args.copy_probe_mb:
         # a plain copy of known size: FETCH_SIZE / WRITE_SIZE of its dispatches calibrate
