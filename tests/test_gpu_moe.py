@@ -71,6 +71,23 @@ def test_verify_block(dev, orc, t):
     oracle_check(orc, layer, x, out, ids, w, f"C2 t={t}", max_flips=1)
 
 
+SWEEP_SPEC = LayerSpec(1024, 512, 64, 4, GgmlDType.Q4_K, GgmlDType.Q6_K, shared=True)
+
+
+@pytest.mark.parametrize("t", [1, 2, 3, 15, 16, 17, 31, 32, 33, 63, 64, 65, 100])
+def test_t_sweep_across_path_boundaries(dev, orc, t):
+    """One shared-expert layer (Q4_K gate/up, Q6_K down; hidden 1024, ff 512,
+    64 experts, top-4) at every t on either side of the path boundaries:
+    t = 1 (top-k in the gate/up blocks), 2..15 (mat-vecs in expert order),
+    16..31 (16-pair MFMA tiles), 32 and up (grouped GEMM), 33 and up (the
+    unfused router), against the oracle."""
+    _log(f"sweep t={t}")
+    layer = build_layer(SWEEP_SPEC, seed=1020)
+    x = make_x(SWEEP_SPEC, 40 + t, t)
+    out, ids, w = run_block(layer, x)
+    oracle_check(orc, layer, x, out, ids, w, f"sweep t={t}", max_flips=max(1, t // 16))
+
+
 def test_verify_block_no_shared(dev, orc):
     """Expert-ordered verify without a shared expert (C0 shape, t = 20)."""
     cfg = CONFIGS["C0"]
