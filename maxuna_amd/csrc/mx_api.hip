@@ -671,7 +671,7 @@ mx_status moe_forward_impl(const mx_moe_layer *L, const float *x, int64_t t, con
             g.runs = o.runs;
             g.out = o.act;
             for (int r = 0; r < rep(2); r++) {
-                if (!x16_in_router) MX_TRY(launch_to_f16_rows(xin, t, (int)H, nullptr, o.x16, o.x16s, s));
+                if (!x16_in_router) MX_TRY(launch_to_f16_rows(xin, t, (int)H, nullptr, o.x16, o.x16s, s, true));
                 MX_TRY(launch_vmm(L->gate.dtype, true, g, np, s));
             }
             MX_STAGE();
@@ -690,7 +690,8 @@ mx_status moe_forward_impl(const mx_moe_layer *L, const float *x, int64_t t, con
             d.a_slots = 1;
             d.out = o.down;
             for (int r = 0; r < rep(3); r++) {
-                MX_TRY(launch_to_f16_rows(o.act, np, (int)FF, nullptr, o.act16, o.act16s, s));
+                MX_TRY(launch_to_f16_rows(o.act, np, (int)FF, nullptr, o.act16, o.act16s, s,
+                                          L->down.dtype == kQ4_K));  // (the Q4_K tiles' K order)
                 MX_TRY(launch_vmm(L->down.dtype, false, d, np, s));
                 MX_TRY(launch_combine_prefill(o.down, w, residual, (int)t, (int)K, shf ? 1 : 0, (int)H, out, s));
             }

@@ -12,7 +12,9 @@ namespace mx {
 // k <= 1024 * RPT, the row's float4s stay in registers between the max pass and
 // the conversion (all loads issued up front); RPT == 0: any k, the row is read
 // twice.  s_red: 4 floats of LDS.  Every thread of the block must call it.
-template <int RPT>
+// PERM: each group of four values is stored in the order 0, 2, 1, 3 (the K order
+// in which the Q4_K verify tiles build their weight operand).
+template <int RPT, bool PERM = false>
 __device__ __forceinline__ void f16_row(const float *__restrict__ x, int k, _Float16 *__restrict__ y,
                                         float *__restrict__ scale, float *s_red) {
     typedef float f2_t __attribute__((ext_vector_type(2)));
@@ -48,7 +50,7 @@ __device__ __forceinline__ void f16_row(const float *__restrict__ x, int k, _Flo
     auto put = [&](int i, const float4 &v) {
         const half2_t lo = __builtin_convertvector((f2_t){v.x * inv, v.y * inv}, half2_t);
         const half2_t hi = __builtin_convertvector((f2_t){v.z * inv, v.w * inv}, half2_t);
-        yr[i] = (half4_t){lo[0], lo[1], hi[0], hi[1]};
+        yr[i] = PERM ? (half4_t){lo[0], hi[0], lo[1], hi[1]} : (half4_t){lo[0], lo[1], hi[0], hi[1]};
     };
     if constexpr (RPT > 0) {
 #pragma unroll

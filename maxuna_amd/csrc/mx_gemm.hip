@@ -434,14 +434,14 @@ __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
 }
 
 // ---- f32 rows -> scaled f16 rows (body in mx_f16row.h) -------------------------------
-template <int RPT>
+template <int RPT, bool PERM>
 __global__ void __launch_bounds__(256) k_to_f16_rows(const float *__restrict__ x, int k,
                                                      const int32_t *__restrict__ count,
                                                      _Float16 *__restrict__ y, float *__restrict__ scale) {
     const int64_t row = blockIdx.x;
     if (count && row >= *count) return;
     __shared__ float s_red[4];
-    f16_row<RPT>(x + row * k, k, y + row * k, scale + row, s_red);
+    f16_row<RPT, PERM>(x + row * k, k, y + row * k, scale + row, s_red);
 }
 
 // out = residual + (sum_s w_s down_s) + shared   (moe.rs:78; combine.metal:16-40 order)
@@ -535,13 +535,20 @@ mx_status launch_gemm(int dtype, bool swiglu, const GemmArgs &a, hipStream_t s) 
     return MX_OK;
 }
 
-mx_status launch_to_f16_rows(const float *x, int64_t rows, int k, const int32_t *count, _Float16 *y, float *scale,
-                             hipStream_t s) {
-    if (rows == 0) return MX_OK;
+template <bool PERM>
+static void to_f16_rows(const float *x, int64_t rows, int k, const int32_t *count, _Float16 *y, float *scale,
+                        hipStream_t s) {
     const dim3 grid((unsigned)rows);
-    if (k <= 1024 * 2) hipLaunchKernelGGL(k_to_f16_rows<2>, grid, dim3(256), 0, s, x, k, count, y, scale);
-    else if (k <= 1024 * 4) hipLaunchKernelGGL(k_to_f16_rows<4>, grid, dim3(256), 0, s, x, k, count, y, scale);
-    else hipLaunchKernelGGL(k_to_f16_rows<0>, grid, dim3(256), 0, s, x, k, count, y, scale);
+    if (k <= 1024 * 2) hipLaunchKernelGGL((k_to_f16_rows<2, PERM>), grid, dim3(256), 0, s, x, k, count, y, scale);
+    else if (k <= 1024 * 4) hipLaunchKernelGGL((k_to_f16_rows<4, PERM>), grid, dim3(256), 0, s, x, k, count, y, scale);
+    else hipLaunchKernelGGL((k_to_f16_rows<0, PERM>), grid, dim3(256), 0, s, x, k, count, y, scale);
+}
+
+mx_status launch_to_f16_rows(const float *x, int64_t rows, int k, const int32_t *count, _Float16 *y, float *scale,
+                             hipStream_t s, bool perm) {
+    if (rows == 0) return MX_OK;
+    if (perm) to_f16_rows<true>(x, rows, k, count, y, scale, s);
+    else to_f16_rows<false>(x, rows, k, count, y, scale, s);
     MX_LAUNCH("k_to_f16_rows");
     return MX_OK;
 }

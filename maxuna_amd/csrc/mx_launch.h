@@ -133,7 +133,8 @@ mx_status launch_route_select(const float *logits, const float *bias, int t, int
 // probabilities and selection sort keys for t tokens (ws: keys u64 [t, E] |
 // probs f32 [t, E]); also stages the (normalised) rows into `xstage`
 // (mx_stage.h layout) and/or writes them to `x_normed` when non-NULL, and (no
-// RMSNorm) as f16 rows times a per-row power of two into x16 / x16s when
+// RMSNorm) as f16 rows times a per-row power of two, in the Q4_K verify tiles'
+// K order (launch_to_f16_rows with perm), into x16 / x16s when
 // non-NULL.  The top-k runs in k_decode_select (launch_decode_select).
 size_t route_fused_ws_bytes(int t, int hidden, int n_expert);
 int route_fused_max_t();
@@ -232,9 +233,10 @@ bool gemm_supported(int dtype, int k);
 bool gemm_fits(int t, int hidden, int ff, int64_t gu_row_bytes, int64_t d_row_bytes);
 mx_status launch_gemm(int dtype, bool swiglu, const GemmArgs &a, hipStream_t s);
 // rows of x (f32, [rows, k], k % 4 == 0) -> f16 times a per-row power of two;
-// rows at or beyond *count (when count != NULL) are skipped
+// rows at or beyond *count (when count != NULL) are skipped.  perm: each group of
+// four values stored in the order 0, 2, 1, 3 (the K order of the Q4_K verify tiles)
 mx_status launch_to_f16_rows(const float *x, int64_t rows, int k, const int32_t *count, _Float16 *y,
-                             float *scale, hipStream_t s);
+                             float *scale, hipStream_t s, bool perm = false);
 // out[t, n] = residual + (sum_s w[t, s] * down[t * kk + s] + shared), kk = top_k + has_shared,
 // shared = down[t * kk + top_k] (has_shared), shared_sep[t] (shared_sep != NULL) or 0; n % 4 == 0
 mx_status launch_combine_prefill(const float *down, const float *w, const float *residual, int t, int top_k,

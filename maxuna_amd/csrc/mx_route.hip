@@ -389,9 +389,10 @@ __global__ void __launch_bounds__(RF_THREADS) k_route_fused(
         // ---- f16 row blocks: token row -> f16 times a power of two (x16 != NULL,
         // no RMSNorm), the operand of the MFMA verify tiles
         const int tok = blockIdx.x - n_eb - n_stage;
-        if (hidden <= 4096) f16_row<4>(x + (int64_t)tok * hidden, hidden, x16 + (int64_t)tok * hidden, x16s + tok,
-                                       &s_red[0][0]);
-        else f16_row<0>(x + (int64_t)tok * hidden, hidden, x16 + (int64_t)tok * hidden, x16s + tok, &s_red[0][0]);
+        // (in the Q4_K verify tiles' K order: the only reader)
+        if (hidden <= 4096)
+            f16_row<4, true>(x + (int64_t)tok * hidden, hidden, x16 + (int64_t)tok * hidden, x16s + tok, &s_red[0][0]);
+        else f16_row<0, true>(x + (int64_t)tok * hidden, hidden, x16 + (int64_t)tok * hidden, x16s + tok, &s_red[0][0]);
         return;
     }
     if ((int)blockIdx.x >= n_eb) {

@@ -27,7 +27,8 @@
 //  * Lane l holds row n = l % 16 of each 16-row block and K quarter q = l / 16.
 //    Q4_K: the lane owns 32-value sub-block q of each half super-block, so it
 //    unpacks one scale / min per half, not four: MFMA step P gives it values
-//    32 q + 8 P + [0, 8) of the half.  Q6_K (16-value scale groups): step P
+//    32 q + 8 P + [0, 8) of the half, each group of four in the order 0, 2, 1, 3
+//    (the A rows are stored so; see VmQ4).  Q6_K (16-value scale groups): step P
 //    gives it 32 P + 8 q + [0, 8) (the prefill GEMM's per-half layout).  The A
 //    fragments follow the same K order.  Results: lane l holds D[4 q + r][n],
 //    r = 0..3.
@@ -89,21 +90,26 @@ __device__ __forceinline__ void vm_load(WB<kQ6_K> &w, const uint8_t *slot, int k
 }
 
 // Q4_K half super-block `PAR` of the lane's row for the sub-block-per-lane
-// order: sub-block j = 4 PAR + q (32 values, one 6-bit scale and min), its 32
-// quant bytes' nibbles unpacked once; step P = values 8 P .. 8 P + 7 of it,
-// dequantised as in WB<kQ4_K> (one f16 rounding of the f32 value).
+// order: sub-block j = 4 PAR + q (32 values, one 6-bit scale and min).  Word i of
+// its 32 quant bytes holds values 4 i .. 4 i + 3 in the lane's nibble (low for
+// even q, high for odd q).  One and-or against the f16 exponent 0x6400 turns a
+// word into the f16 pair 1024 + q of values 4 i and 4 i + 2 (the word shifted by
+// a byte: 4 i + 1 and 4 i + 3), so step P gives values 8 P + {0, 2, 1, 3, 4, 6,
+// 5, 7}: the A rows are stored in that order (launch_to_f16_rows with perm).  A
+// high nibble reads as 1024 + 16 q, so odd sub-blocks take d1 / 16 (exact); each
+// value is the f32 fma (1024 + q) d1 + c rounded to f16 once, as in WB<kQ4_K>.
 struct VmQ4 {
-    uint32_t w[8];  // nibbles of values 4 i .. 4 i + 3 of the sub-block in word i
-    float d1, c1;   // d * sc and -dmin * m - 1024 * d * sc
+    uint32_t w[8];  // the quant bytes of values 4 i .. 4 i + 3 in word i
+    uint32_t m;     // the lane's nibble of bytes 0 and 2: 0x000F000F or 0x00F000F0
+    float d1, c1;   // d * sc (/ 16 for a high nibble) and -dmin * m - 1024 * d1
     template <int PAR> __device__ __forceinline__ void load(const uint8_t *slot, int q) {
         const uint4 h = *reinterpret_cast<const uint4 *>(slot);  // d, dmin | scales[12]
         const uint8_t *qs = slot + 16 + 64 * PAR + 32 * (q >> 1); // the sub-block pair's 32 bytes
         const uint4 a = *reinterpret_cast<const uint4 *>(qs);
         const uint4 b = *reinterpret_cast<const uint4 *>(qs + 16);
-        const uint32_t sh = 4u * (uint32_t)(q & 1);  // odd sub-blocks: the high nibbles
-        const uint32_t raw[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-        for (int i = 0; i < 8; i++) w[i] = (raw[i] >> sh) & 0x0F0F0F0Fu;
+        w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+        w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+        m = (q & 1) ? 0x00F000F0u : 0x000F000Fu;
         // get_scale_min_k4 of sub-block j (q4k_scale_min) with j = 4 PAR + q
         const uint32_t o = 8u * (uint32_t)q;
         uint32_t sc, mn;
@@ -116,10 +122,20 @@ struct VmQ4 {
             mn = (b8 >> 4) | (__builtin_amdgcn_ubfe(h.z, o + 6, 2) << 4);
         }
         const float d = h2f((uint16_t)(h.x & 0xFFFFu)), dmin = h2f((uint16_t)(h.x >> 16));
-        d1 = d * (float)sc;
+        d1 = d * (float)sc * ((q & 1) ? 0.0625f : 1.0f);
         c1 = __builtin_fmaf(-1024.0f, d1, -(dmin * (float)mn));
     }
-    __device__ __forceinline__ half8_t step(int P) const { return dq8_kmin(w[2 * P], w[2 * P + 1], d1, c1); }
+    __device__ __forceinline__ half8_t step(int P) const {
+        const uint32_t r0 = w[2 * P], r1 = w[2 * P + 1];
+        const half2_t x[4] = {__builtin_bit_cast(half2_t, (r0 & m) | 0x64006400u),
+                              __builtin_bit_cast(half2_t, ((r0 >> 8) & m) | 0x64006400u),
+                              __builtin_bit_cast(half2_t, (r1 & m) | 0x64006400u),
+                              __builtin_bit_cast(half2_t, ((r1 >> 8) & m) | 0x64006400u)};
+        half2_t y[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) y[i] = mix2(x[i], d1, c1);
+        return pk_join(y);
+    }
 };
 
 // One work item, as a wave sees it.  Uniform: the matrices and the run; per
