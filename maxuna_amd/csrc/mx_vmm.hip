@@ -299,12 +299,13 @@ k_vmm(VmmArgs a, const int32_t *__restrict__ perm, const int32_t *__restrict__ r
 
     // stage S from (buf, af); issues stage S + 1 (clamped: the last stage re-copies
     // itself into the other buffer) into (nbuf, naf) first
+    // (stage S is stage ks of the wave's item jn; counted along, not divided out)
+    int ks = 0, jn = 0;
     auto body = [&](int S, const uint8_t *__restrict__ buf, half8_t (&af)[8], uint8_t *__restrict__ nbuf,
                     half8_t (&naf)[8]) {
-        const int S1 = min(S + 1, total - 1);
-        const int j1 = S1 / nks, ks1 = S1 - j1 * nks;
-        const int ks = S - (S / nks) * nks;
-        if (ks1 == 0 && S1 != S) vm_item(a, tb, gw + j1 * NW, CB, lane, nxt);  // wave-uniform
+        const bool last = S + 1 >= total;
+        const int ks1 = last ? ks : (ks + 1 == nks ? 0 : ks + 1);
+        if (!last && ks1 == 0) vm_item(a, tb, gw + (jn + 1) * NW, CB, lane, nxt);  // wave-uniform
         wait_lgkmcnt0();  // this wave's reads of nbuf (stage S - 1) have returned
         vm_issue_a<DT>(nxt.arow, nxt.aon, ks1, q, naf);
         vm_issue_b(nxt, ks1, lane, nbuf);
@@ -356,7 +357,9 @@ k_vmm(VmmArgs a, const int32_t *__restrict__ perm, const int32_t *__restrict__ r
 #pragma unroll
             for (int nb = 0; nb < G::NBLK; nb++) acc[nb] = float4_t{0.f, 0.f, 0.f, 0.f};
             cur = nxt;
+            jn++;
         }
+        ks = ks1;
     };
     for (int S = 0; S < total; S += 2) {
         body(S, b0, a0, b1, a1);
