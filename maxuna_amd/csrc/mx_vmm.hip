@@ -327,13 +327,18 @@ k_vmm(VmmArgs a, const int32_t *__restrict__ perm, const int32_t *__restrict__ r
             }
 #pragma unroll
             for (int P = 0; P < 4; P++) {
+                // every column block's weight operand first, then the MFMAs: no MFMA
+                // waits on the instruction just before it (hazard nops 214 -> 85 in the
+                // gate/up loop; C2 278.9 -> 276.6 us)
+                half8_t bf[G::NBLK];
 #pragma unroll
                 for (int nb = 0; nb < G::NBLK; nb++) {
-                    half8_t bf;
-                    if constexpr (DT == kQ4_K) bf = wb[nb].step(P);
-                    else bf = wb[nb].step(P, hh);
-                    acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[4 * PAR + P], bf, acc[nb], 0, 0, 0);
+                    if constexpr (DT == kQ4_K) bf[nb] = wb[nb].step(P);
+                    else bf[nb] = wb[nb].step(P, hh);
                 }
+#pragma unroll
+                for (int nb = 0; nb < G::NBLK; nb++)
+                    acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[4 * PAR + P], bf[nb], acc[nb], 0, 0, 0);
             }
         };
         half(std::integral_constant<int, 0>{});
