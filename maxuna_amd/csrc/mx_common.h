@@ -151,6 +151,21 @@ template <class F> __device__ __forceinline__ void at_offset(int o, F &&f) {
     }
 }
 
+// A lambda that must be inlined: one not inlined gets the arrays it captures by
+// reference (accumulators, register tables) passed by address, which moves them
+// to scratch memory
+#define MX_INLINE_LAMBDA __attribute__((always_inline))
+
+// f(std::integral_constant<int, i>) for i = I .. N - 1: a loop whose index is a
+// compile-time constant in every iteration, whatever the unroller decides (an
+// array indexed by a loop variable that stays a variable is moved to scratch)
+template <int I, int N, class F> __device__ __forceinline__ void static_for(F &&f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<I + 1, N>(f);
+    }
+}
+
 __device__ __forceinline__ float warp_sum_width(float v, int width) {
     for_offsets_down(width >> 1, [&](auto c) { v += lane_partner<decltype(c)::value>(v); });
     return v;

@@ -233,7 +233,7 @@ __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
         const int colr = min(tl.nt * NCOL + rm, a.n_out - 1);
         b_row[q] = (uint32_t)(colr * rb);
     }
-    auto issue_b = [&](int ks, uint8_t *buf) {
+    auto issue_b = [&](int ks, uint8_t *buf) MX_INLINE_LAMBDA {
         const uint32_t so = stage_block_off<DT>(ks);
 #pragma unroll
         for (int q = 0; q < B_PER_WAVE; q++) {
@@ -265,7 +265,7 @@ __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
     const int64_t arow0 = a.a_by_token ? a.map[L0.list + tl.pos0] / a.top_k : tl.pos0;
     const uint8_t *abase = reinterpret_cast<const uint8_t *>(a.a) + arow0 * a.k * 2;  // tile's first A row
     // A stage copy: wave instruction i fills LDS rows 4 (8 wave + i) + lane / 16
-    auto issue_a = [&](int ks, uint8_t *buf) {
+    auto issue_a = [&](int ks, uint8_t *buf) MX_INLINE_LAMBDA {
 #pragma unroll
         for (int i = 0; i < DMA_PER_WAVE; i++) {
             const int inst = DMA_PER_WAVE * wave + i;
@@ -296,21 +296,23 @@ __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
 
     // MB: 32-row blocks of the tile that hold rows (a partly filled last m-tile of
     // an expert skips the MFMAs and A reads of its empty blocks)
-    auto compute = [&](auto mbc, const uint8_t *buf, GW(&wb)[NB]) {
+    auto compute = [&](auto mbc, const uint8_t *buf, GW(&wb)[NB]) MX_INLINE_LAMBDA {
         constexpr int MB = decltype(mbc)::value;
         // the A fragments of step s + 1 are read while step s computes
         half8_t af[2][4];
 #pragma unroll
         for (int mb = 0; mb < MB; mb++) af[0][mb] = *reinterpret_cast<const half8_t *>(buf + mb * 32 * ROWB + aoff[0]);
-#pragma unroll
-        for (int s = 0; s < 8; s++) {
+        // (a compile-time step index: with a runtime one the weight registers, indexed
+        // by step, were moved to scratch in the larger instantiations)
+        static_for<0, 8>([&](auto sc) {
+            constexpr int s = decltype(sc)::value;
             // plain tiles: let the scheduler interleave the step's LDS reads,
             // dequantisation and MFMAs (iglp_opt(0): down GEMM 548 -> 520 us at C3);
             // the SwiGLU tiles measured slower with it (0 or 1: +2-4%)
             if constexpr (!SWIGLU && MX_GEMM_IGLP_PLAIN >= 0) __builtin_amdgcn_iglp_opt(MX_GEMM_IGLP_PLAIN);
             if constexpr (SWIGLU && MX_GEMM_IGLP_SWIGLU >= 0) __builtin_amdgcn_iglp_opt(MX_GEMM_IGLP_SWIGLU);
-            const int p = s >> 1, hh = s & 1, cur = s & 1;
-            if (s + 1 < 8) {
+            constexpr int p = s >> 1, hh = s & 1, cur = s & 1;
+            if constexpr (s + 1 < 8) {
 #pragma unroll
                 for (int mb = 0; mb < MB; mb++)
                     af[cur ^ 1][mb] = *reinterpret_cast<const half8_t *>(buf + mb * 32 * ROWB + aoff[s + 1]);
@@ -326,11 +328,11 @@ __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
 #pragma unroll
                 for (int nb = 0; nb < NB; nb++)
                     acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[cur][mb], bf[nb], acc[mb][nb], 0, 0, 0);
-        }
+        });
     };
     // stage ks's B registers from LDS (the block phase of the lane's row for this stage)
     GW wb[NB];
-    auto load_b = [&](int ks, const uint8_t *buf) {
+    auto load_b = [&](int ks, const uint8_t *buf) MX_INLINE_LAMBDA {
         const uint32_t so = stage_block_off<DT>(ks);
 #pragma unroll
         for (int nb = 0; nb < NB; nb++) {
@@ -348,12 +350,12 @@ __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
     // from LDS, dequantise, compute; stage ends wait for the copies and use a bare
     // s_barrier (the copies are complete (vmcnt) and LDS needs no further fence
     // between the waves of a workgroup).
-    auto stage_end = [&] {
+    auto stage_end = [&]() MX_INLINE_LAMBDA {
         wait_vmcnt(0);
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
     };
-    auto k_loop = [&](auto mbc) {
+    auto k_loop = [&](auto mbc) MX_INLINE_LAMBDA {
         for (int ks = 0; ks < nks; ks += 2) {
             issue_a(ks + 1, sA1);
             issue_b(ks + 1, sB1);

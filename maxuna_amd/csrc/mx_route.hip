@@ -349,22 +349,40 @@ __device__ __forceinline__ void norm8(float (&v)[8], const float *alpha, int h0,
     for (int i = 0; i < 8; i++) v[i] = v[i] / m * a[i];
 }
 
-// Block-wide sum of the first t partials (all threads call).
+// Block-wide sum of the first t partials (all threads call).  The loops run over
+// all N with a block-uniform guard, so v stays in registers (a loop bounded by t
+// indexes it with a variable, which puts it in scratch memory).
 template <int N>
 __device__ __forceinline__ void block_sums(float (&v)[N], int t, float (*s_red)[RF_THREADS / 64]) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    for (int tok = 0; tok < t; tok++) {
-        float a = v[tok];
-        a = warp_sum_width(a, 64);
-        if (lane == 0) s_red[tok][wave] = a;
+#pragma unroll
+    for (int tok = 0; tok < N; tok++) {
+        if (tok < t) {
+            float a = v[tok];
+            a = warp_sum_width(a, 64);
+            if (lane == 0) s_red[tok][wave] = a;
+        }
     }
     __syncthreads();
-    for (int tok = 0; tok < t; tok++) {
-        float a = 0.f;
-        for (int wv = 0; wv < RF_THREADS / 64; wv++) a += s_red[tok][wv];
-        v[tok] = a;
+#pragma unroll
+    for (int tok = 0; tok < N; tok++) {
+        if (tok < t) {
+            float a = 0.f;
+            for (int wv = 0; wv < RF_THREADS / 64; wv++) a += s_red[tok][wv];
+            v[tok] = a;
+        }
     }
     __syncthreads();
+}
+
+// v[i] for a lane-dependent i < N without indexing the array: a register array
+// read at a per-lane index lives in scratch memory, and a chain of selects is
+// folded back into such a read by the compiler, so the bits are masked and OR-ed
+template <int N> __device__ __forceinline__ float pick(const float (&v)[N], int i) {
+    uint32_t r = 0;
+#pragma unroll
+    for (int k = 0; k < N; k++) r |= __float_as_uint(v[k]) & (0u - (uint32_t)(i == k));
+    return __uint_as_float(r);
 }
 
 // EPB: experts per expert block (1, or 4 for t > RF_MAX_T: the block's token
@@ -409,16 +427,19 @@ __global__ void __launch_bounds__(RF_THREADS) k_route_fused(
                 const int tc = min(RF_MAX_T, tb - t0 + 1);
                 float ss[RF_MAX_T] = {};
                 for (int h = 4 * tid; h < hidden; h += 4 * RF_THREADS) {
-                    for (int k = 0; k < tc; k++) {
-                        const float4 v = *reinterpret_cast<const float4 *>(x + (int64_t)(t0 + k) * hidden + h);
-                        ss[k] = __builtin_fmaf(v.x, v.x, ss[k]);
-                        ss[k] = __builtin_fmaf(v.y, v.y, ss[k]);
-                        ss[k] = __builtin_fmaf(v.z, v.z, ss[k]);
-                        ss[k] = __builtin_fmaf(v.w, v.w, ss[k]);
+#pragma unroll
+                    for (int k = 0; k < RF_MAX_T; k++) {
+                        if (k < tc) {  // (block-uniform; a loop bounded by tc put ss in scratch)
+                            const float4 v = *reinterpret_cast<const float4 *>(x + (int64_t)(t0 + k) * hidden + h);
+                            ss[k] = __builtin_fmaf(v.x, v.x, ss[k]);
+                            ss[k] = __builtin_fmaf(v.y, v.y, ss[k]);
+                            ss[k] = __builtin_fmaf(v.z, v.z, ss[k]);
+                            ss[k] = __builtin_fmaf(v.w, v.w, ss[k]);
+                        }
                     }
                 }
                 block_sums(ss, tc, s_red);
-                if (tid < tc) s_m[t0 - ta + tid] = sqrtf(ss[tid] / (float)hidden + rms_eps);
+                if (tid < tc) s_m[t0 - ta + tid] = sqrtf(pick(ss, tid) / (float)hidden + rms_eps);
             }
             __syncthreads();
         }
@@ -453,19 +474,24 @@ __global__ void __launch_bounds__(RF_THREADS) k_route_fused(
             for (int i = 0; i < RF_UNROLL; i++) {
                 const int h = c0 + 4 * RF_THREADS * i;
                 const bool ok = h < hidden;
-                const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+                // (values selected after the loads: a select between a load's address
+                // and a local's put the local in scratch memory)
 #pragma unroll
-                for (int k = 0; k < EPB; k++)
-                    rv[k][i] = ok ? *reinterpret_cast<const float4 *>(router + (int64_t)(e0 + k) * hidden + h) : z;
-                av[i] = (ok && rms_alpha) ? *reinterpret_cast<const float4 *>(rms_alpha + h)
-                                          : make_float4(1.f, 1.f, 1.f, 1.f);
+                for (int k = 0; k < EPB; k++) {
+                    rv[k][i] = make_float4(0.f, 0.f, 0.f, 0.f);
+                    if (ok) rv[k][i] = *reinterpret_cast<const float4 *>(router + (int64_t)(e0 + k) * hidden + h);
+                }
+                av[i] = make_float4(1.f, 1.f, 1.f, 1.f);
+                if (ok && rms_alpha) av[i] = *reinterpret_cast<const float4 *>(rms_alpha + h);
 #pragma unroll
-                for (int j = 0; j < RF_MAX_T; j++)
-                    xv[j][i] = (ok && j < tc) ? *reinterpret_cast<const float4 *>(xt + (int64_t)j * hidden + h) : z;
+                for (int j = 0; j < RF_MAX_T; j++) {
+                    xv[j][i] = make_float4(0.f, 0.f, 0.f, 0.f);
+                    if (ok && j < tc) xv[j][i] = *reinterpret_cast<const float4 *>(xt + (int64_t)j * hidden + h);
+                }
             }
 #pragma unroll
             for (int j = 0; j < RF_MAX_T; j++) {
-                if (j >= tc) break;
+                if (j >= tc) continue;  // (block-uniform)
 #pragma unroll
                 for (int i = 0; i < RF_UNROLL; i++) {
                     const float4 v = xv[j][i];
@@ -488,11 +514,11 @@ __global__ void __launch_bounds__(RF_THREADS) k_route_fused(
         if (rms_alpha) block_sums(ss, tc, s_red);
         const int k = tid / RF_MAX_T, j = tid % RF_MAX_T;
         if (k < EPB && j < tc) {
-            const float d = dot[k * RF_MAX_T + j];
-            const float lg = rms_alpha ? d / sqrtf(ss[j] / (float)hidden + rms_eps) : d;
+            const float d = pick(dot, k * RF_MAX_T + j);
+            const float lg = rms_alpha ? d / sqrtf(pick(ss, j) / (float)hidden + rms_eps) : d;
             const float p = 1.0f / (expf(-lg) + 1.0f);  // sigmoid (moe.rs:101)
             const int64_t o = (int64_t)(t0 + j) * n_expert + e0 + k;
-            keys[o] = sel_key(p + be[k], e0 + k);
+            keys[o] = sel_key(p + pick(be, k), e0 + k);
             probs[o] = p;
         }
     }
