@@ -963,8 +963,19 @@ mx_status launch_mul_mv_id(int dtype, const MvArgs &a, hipStream_t s) {
 #ifndef MX_GU_WPE
 #define MX_GU_WPE 5
 #endif
+// waves per SIMD the generic gate/up kernel's registers must allow: MX_GU_WPE
+// for one activation group per lane; each further group holds its three digit
+// planes in registers (Q4_K / Q5_K: 52 VGPRs a group), so more groups get fewer
+// waves (at 5 waves per SIMD two groups spilled 200 bytes per lane to scratch,
+// eight 1.6 KB)
+template <int DT, int NG> constexpr int gu_wpe() {
+    if (NG <= 1) return MX_GU_WPE;
+    if (DT == kQ8_0) return NG <= 2 ? 5 : NG <= 4 ? 4 : 2;
+    if (DT == kQ6_K) return NG <= 2 ? 4 : NG <= 3 ? 3 : NG <= 4 ? 2 : 1;
+    return NG <= 2 ? 3 : NG <= 4 ? 2 : 1;
+}
 template <int DT, int NG, bool GM>
-__global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(MX_GU_WPE)))
+__global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(gu_wpe<DT, NG>())))
 k_decode_gate_up(DecodeGateUpArgs a, int ni, int slot0, Geo<DT> geo) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int slots = a.top_k + (a.sh_gate ? 1 : 0);
@@ -1246,7 +1257,7 @@ static bool gu64_ok(const DecodeGateUpArgs &a) {
 
 template <int DT>
 static mx_status launch_gu_dt(const DecodeGateUpArgs &a, int slot0, int nslot, hipStream_t s) {
-    if constexpr (DT == kQ4_K || DT == kQ5_K) {
+    if constexpr (DT == kQ4_K) {  // (gu64_ok holds for Q4_K only)
         if (gu64_ok<DT>(a)) {
             const unsigned tiles = (unsigned)((a.ff + WAVES * GU64_R - 1) / (WAVES * GU64_R));
             // verify blocks (t > 1): GU64_TPB tiles per workgroup, the activation
@@ -1712,6 +1723,9 @@ static bool dn_slots_fit(const DecodeDownArgs &a) {
     if (!MX_DN_SLOTS || a.t > MX_DN_SLOTS_MAX_T) return false;
     if (a.top_k + (a.sh_down ? 1 : 0) > DN_SLOTS_MAX) return false;
     const int ng = ng_variant(Geo<DT>(a.ff, DN_FULL).NG);
+    // the slot waves (3 per SIMD: 168 VGPRs) hold this many activation groups without
+    // spilling to scratch; wider rows take k_decode_down and the combine
+    if (ng > (DT == kQ8_0 ? 4 : DT == kQ6_K ? 3 : 2)) return false;
     size_t lds = SIZE_MAX;
     [&] {
 #define MX_L(N) { lds = dn_slots_lds<DT, N>(a); return; }

@@ -291,9 +291,54 @@ __global__ void __launch_bounds__(64 * RL_W) k_route_logits_lds(const float *__r
     }
 }
 
+// Few tokens (t < RLR_T): one block per expert; its 256 threads split the
+// expert's router row (and the same columns of the token rows), then reduce
+// through DPP and LDS.  The tiled kernels give a 256-expert router at t = 1 only
+// four blocks (1.5 ms at hidden 7168).
+constexpr int RLR_T = 8;
+__global__ void __launch_bounds__(256) k_route_logits_rows(const float *__restrict__ x, const float *__restrict__ r,
+                                                           int t, int hidden, int n_expert,
+                                                           float *__restrict__ logits) {
+    __shared__ float s_red[RLR_T][4];
+    const int e = blockIdx.x, tid = threadIdx.x;
+    const float *re = r + (int64_t)e * hidden;
+    float dot[RLR_T] = {};
+    for (int h = 4 * tid; h < hidden; h += 4 * 256) {
+        const float4 rv = *reinterpret_cast<const float4 *>(re + h);
+#pragma unroll
+        for (int j = 0; j < RLR_T; j++) {
+            if (j < t) {  // (block-uniform)
+                const float4 v = *reinterpret_cast<const float4 *>(x + (int64_t)j * hidden + h);
+                dot[j] = __builtin_fmaf(v.x, rv.x, dot[j]);
+                dot[j] = __builtin_fmaf(v.y, rv.y, dot[j]);
+                dot[j] = __builtin_fmaf(v.z, rv.z, dot[j]);
+                dot[j] = __builtin_fmaf(v.w, rv.w, dot[j]);
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < RLR_T; j++) {
+        if (j < t) {
+            const float a = warp_sum_width(dot[j], 64);
+            if ((tid & 63) == 0) s_red[j][tid >> 6] = a;
+        }
+    }
+    __syncthreads();
+    if (tid < t) {
+        const float *sr = s_red[0] + 4 * tid;  // (row tid of s_red)
+        logits[(int64_t)tid * n_expert + e] = ((sr[0] + sr[1]) + sr[2]) + sr[3];
+    }
+}
+
 mx_status launch_route_logits(const float *x, const float *router, int t, int hidden, int n_expert, float *logits,
                               hipStream_t s) {
     if (t == 0) return MX_OK;
+    if (t < RLR_T && hidden % 4 == 0) {
+        hipLaunchKernelGGL(k_route_logits_rows, dim3((unsigned)n_expert), dim3(256), 0, s, x, router, t, hidden,
+                           n_expert, logits);
+        MX_LAUNCH("k_route_logits_rows");
+        return MX_OK;
+    }
     if (MX_RL_LDS && hidden % RLL_KS == 0 && t >= 8) {
         const dim3 grid((unsigned)((n_expert + RL_E - 1) / RL_E), (unsigned)((t + RL_T - 1) / RL_T));
         hipLaunchKernelGGL(k_route_logits_lds, grid, dim3(64 * RL_W), 0, s, x, router, t, hidden, n_expert, logits);

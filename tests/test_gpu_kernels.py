@@ -195,12 +195,14 @@ def test_route_kats_on_device(dev, orc):
 
 
 def test_route_logits(dev, orc):
-    """t = 1: the plain kernel; t >= 8 with hidden % 128 == 0: the LDS-staged MFMA
-    kernel; hidden 1040 (% 16 only): the register-fed MFMA kernel (the two MFMA
-    kernels form the same sums in the same order)."""
+    """t < 8: one block per expert (t = 1 and 7, hidden 7168 as well); t >= 8 with
+    hidden % 128 == 0: the LDS-staged MFMA kernel; hidden 1040 (% 16 only): the
+    register-fed MFMA kernel (the two MFMA kernels form the same sums in the same
+    order); hidden 1036 at t = 9: the tiled f32 kernel."""
     _log("route_logits")
     rng = np.random.default_rng(5)
-    for t, hidden, n_expert in ((1, 1024, 256), (70, 1024, 256), (45, 1040, 100), (45, 1024, 100)):
+    for t, hidden, n_expert in ((1, 1024, 256), (1, 7168, 256), (7, 4096, 64), (70, 1024, 256), (45, 1040, 100),
+                                (45, 1024, 100), (9, 1036, 60)):
         x = rng.standard_normal((t, hidden)).astype(np.float32)
         r = (rng.standard_normal((n_expert, hidden)) * 0.02).astype(np.float32)  # [n_expert, hidden]
         got = host(ops.route_logits(dev_f32(r), dev_f32(x)))
