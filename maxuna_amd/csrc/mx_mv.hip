@@ -317,14 +317,16 @@ constexpr int NG_MAX = MX_NG_MAX;
 // fewer activation registers per lane at the cost of idle lanes.
 // Built on the host and passed to the kernels as an argument (so no wave spends
 // scalar instructions on its divisions); lp = log2 P, lrpi = log2 RPI.
+// wide: every row takes the whole wave (P = 64, the tail groups masked), so one
+// row per iteration: rows whose RPI-row batches would not fit the DMA budget.
 template <int DT> struct Geo {
     int G, P, NG, RPI, lp, lrpi;
-    __host__ __device__ explicit Geo(int k, bool full_wave = false) {
+    __host__ __device__ explicit Geo(int k, bool full_wave = false, bool wide = false) {
         G = (k / block_size(DT)) * Q<DT>::GPB;
         int p = G & (-G);
         if (p > 64) p = 64;
         if (G / p > NG_MAX) p = 64;
-        if (full_wave && G <= 64) p = 64;
+        if ((full_wave && G <= 64) || wide) p = 64;
         P = p;
         NG = (G + p - 1) / p;
         RPI = 64 / p;
@@ -633,8 +635,9 @@ template <int NG> struct BatchDn { static constexpr int NIT = NG == 1 && DN_FULL
 
 // DMA instructions per batch for NM matrices of row_bytes rows at k
 template <int DT, int NG>
-static int ring_insts(int nm, int k, int64_t row_bytes, int nit = Batch<NG>::NIT, bool full_wave = false) {
-    return dma_insts(nm, nit * Geo<DT>(k, full_wave).RPI, row_bytes);
+static int ring_insts(int nm, int k, int64_t row_bytes, int nit = Batch<NG>::NIT, bool full_wave = false,
+                      bool wide = false) {
+    return dma_insts(nm, nit * Geo<DT>(k, full_wave, wide).RPI, row_bytes);
 }
 __host__ __device__ inline size_t align16(size_t v) { return (v + 15) & ~size_t(15); }
 
@@ -904,12 +907,21 @@ template <int DT> static bool mv_fits_dt(int k) {
     const int ni = dma_insts(1, nit * g.RPI, row_bytes_of<DT>(k));
     return ni <= DMA_MAX_INSTS && align16(xstage_bytes(k)) + (size_t)WAVES * RING_MV * ni * 1024 <= 160 * 1024;
 }
-template <int DT> static bool gu_fits_dt(int hidden, int64_t row_bytes) {
-    if (!geo_ok<DT>(hidden) || row_bytes != row_bytes_of<DT>(hidden)) return false;
-    const Geo<DT> g(hidden);
+template <int DT> static bool gu_geo_fits(int hidden, int64_t row_bytes, bool wide) {
+    const Geo<DT> g(hidden, false, wide);
+    if (!(hidden > 0 && hidden % block_size(DT) == 0 && g.NG <= NG_MAX) || row_bytes != row_bytes_of<DT>(hidden))
+        return false;
     const int nit = g.NG == 1 ? Batch<1>::NIT : Batch<2>::NIT;
     const int ni = dma_insts(2, nit * g.RPI, row_bytes);
     return ni <= DMA_MAX_INSTS && (size_t)WAVES * RING_GU * ni * 1024 <= 160 * 1024;
+}
+// the gate/up rows take the wide geometry (hidden 7168: 112 groups, 16 lanes a row
+// and 4 rows an iteration put 32 copy instructions in a gate + up batch)
+template <int DT> static bool gu_wide(int hidden, int64_t row_bytes) {
+    return !gu_geo_fits<DT>(hidden, row_bytes, false) && gu_geo_fits<DT>(hidden, row_bytes, true);
+}
+template <int DT> static bool gu_fits_dt(int hidden, int64_t row_bytes) {
+    return gu_geo_fits<DT>(hidden, row_bytes, false) || gu_geo_fits<DT>(hidden, row_bytes, true);
 }
 template <int DT> static bool dn_fits_dt(int ff, int64_t row_bytes) {
     if (!geo_ok<DT>(ff, DN_FULL) || row_bytes != row_bytes_of<DT>(ff)) return false;
@@ -1226,13 +1238,13 @@ mx_status launch_pair_order(const uint32_t *ids, int t, int top_k, int n_expert,
 }
 
 template <int DT, int NG>
-static mx_status launch_gu_ng(const DecodeGateUpArgs &a, int slot0, int nslot, hipStream_t s) {
+static mx_status launch_gu_ng(const DecodeGateUpArgs &a, int slot0, int nslot, hipStream_t s, bool wide) {
     const unsigned tiles = (unsigned)((a.ff + WAVES * RW_GU - 1) / (WAVES * RW_GU));
     const dim3 grid(tiles, (unsigned)nslot, (unsigned)a.t);
     constexpr bool GM_OK = DT == kQ4_K || DT == kQ5_K;
-    const int ni = ring_insts<DT, NG>(2, a.hidden, a.gu_row_bytes);
+    const int ni = ring_insts<DT, NG>(2, a.hidden, a.gu_row_bytes, Batch<NG>::NIT, false, wide);
     const size_t lds = (size_t)WAVES * RING_GU * ni * 1024;
-    const Geo<DT> geo(a.hidden);
+    const Geo<DT> geo(a.hidden, false, wide);
     if (GM_OK && a.xstage_gm)
         hipLaunchKernelGGL((k_decode_gate_up<DT, NG, GM_OK>), grid, dim3(64 * WAVES), lds, s, a, ni, slot0, geo);
     else
@@ -1278,8 +1290,9 @@ static mx_status launch_gu_dt(const DecodeGateUpArgs &a, int slot0, int nslot, h
             return MX_OK;
         }
     }
-    const int ng = ng_variant(Geo<DT>(a.hidden).NG);
-#define MX_L(N) return launch_gu_ng<DT, N>(a, slot0, nslot, s)
+    const bool wide = gu_wide<DT>(a.hidden, a.gu_row_bytes);
+    const int ng = ng_variant(Geo<DT>(a.hidden, false, wide).NG);
+#define MX_L(N) return launch_gu_ng<DT, N>(a, slot0, nslot, s, wide)
     MX_NG_SWITCH(ng, MX_L)
 #undef MX_L
     return MX_OK;

@@ -88,6 +88,21 @@ def test_t_sweep_across_path_boundaries(dev, orc, t):
     oracle_check(orc, layer, x, out, ids, w, f"sweep t={t}", max_flips=max(1, t // 16))
 
 
+WIDE_SPEC = LayerSpec(7168, 2048, 64, 8, GgmlDType.Q4_K, GgmlDType.Q6_K, shared=True)
+
+
+@pytest.mark.parametrize("t", [1, 4])
+def test_wide_hidden_decode(dev, orc, t):
+    """hidden 7168 (DeepSeek-shaped rows: 112 Q4_K groups): the generic gate/up
+    kernel in its wide geometry (a whole wave per row, tail groups masked), at
+    t = 1 and on the expert-ordered verify path, against the oracle."""
+    _log(f"wide hidden t={t}")
+    layer = build_layer(WIDE_SPEC, seed=1030)
+    x = make_x(WIDE_SPEC, 60 + t, t)
+    out, ids, w = run_block(layer, x)
+    oracle_check(orc, layer, x, out, ids, w, f"wide t={t}", max_flips=1)
+
+
 def test_verify_block_no_shared(dev, orc):
     """Expert-ordered verify without a shared expert (C0 shape, t = 20)."""
     cfg = CONFIGS["C0"]
