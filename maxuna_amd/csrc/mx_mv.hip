@@ -1712,15 +1712,24 @@ static bool dn_q6_ok(const DecodeDownArgs &a) {
            a.d_expert_bytes % 16 == 0 && al(a.down) && (!a.sh_down || (a.sh_row_bytes == DQ6_RB && al(a.sh_down)));
 }
 
+// the slot waves (3 per SIMD: 168 VGPRs) hold this many activation groups without
+// spilling to scratch; wider rows take k_decode_down and the combine
+template <int DT> constexpr int dn_slots_max_ng() { return DT == kQ8_0 ? 4 : DT == kQ6_K ? 3 : 2; }
 template <int DT, int NG>
 static mx_status launch_dn_slots_ng(const DecodeDownArgs &a, hipStream_t s) {
-    const int ni = ring_insts<DT, NG>(1, a.ff, a.d_row_bytes, BatchDnSlots<NG>::NIT, DN_FULL);
-    if (ni > DMA_MAX_INSTS) return fail(MX_ERR_SHAPE, "decode down: rows too long for the LDS ring");
-    const int slots = a.top_k + (a.sh_down ? 1 : 0);
-    const size_t lds = (size_t)slots * dn_slot_area(a.ff, ni);
-    const dim3 grid((unsigned)((a.hidden + RW_DN - 1) / RW_DN), (unsigned)a.t);
-    hipLaunchKernelGGL((k_decode_down_slots<DT, NG>), grid, dim3(64 * slots), lds, s, a, ni, Geo<DT>(a.ff, DN_FULL));
-    return MX_OK;
+    if constexpr (NG > dn_slots_max_ng<DT>()) {  // (not instantiated: dn_slots_fit refuses these)
+        (void)a;
+        (void)s;
+        return fail(MX_ERR_SHAPE, "decode down: %d activation groups per lane exceed the slot kernel", NG);
+    } else {
+        const int ni = ring_insts<DT, NG>(1, a.ff, a.d_row_bytes, BatchDnSlots<NG>::NIT, DN_FULL);
+        if (ni > DMA_MAX_INSTS) return fail(MX_ERR_SHAPE, "decode down: rows too long for the LDS ring");
+        const int slots = a.top_k + (a.sh_down ? 1 : 0);
+        const size_t lds = (size_t)slots * dn_slot_area(a.ff, ni);
+        const dim3 grid((unsigned)((a.hidden + RW_DN - 1) / RW_DN), (unsigned)a.t);
+        hipLaunchKernelGGL((k_decode_down_slots<DT, NG>), grid, dim3(64 * slots), lds, s, a, ni, Geo<DT>(a.ff, DN_FULL));
+        return MX_OK;
+    }
 }
 // LDS bytes of the slot-per-wave kernel (SIZE_MAX: its DMA batch does not fit)
 template <int DT, int NG>
@@ -1736,9 +1745,7 @@ static bool dn_slots_fit(const DecodeDownArgs &a) {
     if (!MX_DN_SLOTS || a.t > MX_DN_SLOTS_MAX_T) return false;
     if (a.top_k + (a.sh_down ? 1 : 0) > DN_SLOTS_MAX) return false;
     const int ng = ng_variant(Geo<DT>(a.ff, DN_FULL).NG);
-    // the slot waves (3 per SIMD: 168 VGPRs) hold this many activation groups without
-    // spilling to scratch; wider rows take k_decode_down and the combine
-    if (ng > (DT == kQ8_0 ? 4 : DT == kQ6_K ? 3 : 2)) return false;
+    if (ng > dn_slots_max_ng<DT>()) return false;
     size_t lds = SIZE_MAX;
     [&] {
 #define MX_L(N) { lds = dn_slots_lds<DT, N>(a); return; }
