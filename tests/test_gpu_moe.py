@@ -103,6 +103,29 @@ def test_wide_hidden_decode(dev, orc, t):
     oracle_check(orc, layer, x, out, ids, w, f"wide t={t}", max_flips=1)
 
 
+SHAPES = {
+    "h2048_ff768_q4q6": LayerSpec(2048, 768, 64, 8, GgmlDType.Q4_K, GgmlDType.Q6_K, shared=True),
+    "h5120_ff1536_q5q6": LayerSpec(5120, 1536, 32, 6, GgmlDType.Q5_K, GgmlDType.Q6_K, shared=True),
+    "h3072_ff2048_q8q8": LayerSpec(3072, 2048, 32, 4, GgmlDType.Q8_0, GgmlDType.Q8_0, shared=False),
+    "h6144_ff2816_q6q4": LayerSpec(6144, 2816, 16, 4, GgmlDType.Q6_K, GgmlDType.Q4_K, shared=True),
+    "h7168_ff2048_q4q5": LayerSpec(7168, 2048, 32, 8, GgmlDType.Q4_K, GgmlDType.Q5_K, shared=False),
+}
+
+
+@pytest.mark.parametrize("name", list(SHAPES))
+@pytest.mark.parametrize("t", [1, 5])
+def test_model_shapes(dev, orc, name, t):
+    """Layer shapes beyond the Laguna one (hidden 2048 to 7168, ff 768 to 2816,
+    mixed quant types, with and without a shared expert): whichever decode
+    kernels, geometry and router each shape selects, against the oracle."""
+    spec = SHAPES[name]
+    _log(f"shape {name} t={t}")
+    layer = build_layer(spec, seed=1040)
+    x = make_x(spec, 70 + t, t)
+    out, ids, w = run_block(layer, x)
+    oracle_check(orc, layer, x, out, ids, w, f"{name} t={t}", max_flips=1)
+
+
 def test_verify_block_no_shared(dev, orc):
     """Expert-ordered verify without a shared expert (C0 shape, t = 20)."""
     cfg = CONFIGS["C0"]
