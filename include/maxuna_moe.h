@@ -122,7 +122,8 @@ mx_status mx_mul_mv(const void *w, int32_t dtype, int64_t n_out, int64_t k, cons
  *   [0, E)                 tpe[e]       pairs routed to expert e
  *   [E, 2E+1)              off[e]       exclusive prefix of tpe (off[E] = t*top_k)
  *   [2E+1]                 n_tiles      number of (expert, m-tile) work items
- *   [2E+2, 2E+2+T_max)     tiles        expert<<16 | m_tile, T_max = t*top_k/64 + E
+ *   [2E+2, 2E+2+T_max)     tiles        expert<<16 | m_tile (m-tiles of 128 pairs),
+ *                                       T_max = ceil(t*top_k/64) + E words reserved
  *   then t*top_k words     list         flattened pair ids token*top_k+slot, grouped by
  *                                       expert (ascending e), tokens ascending within e
  *   then chunk tables (internal).
@@ -147,14 +148,21 @@ mx_status mx_prepare_map0(int64_t n_expert, const uint32_t *ids, int64_t t, int6
 /* Replaces ops::mm_id::mul_mm_id_shared (mm_id.rs:32-39 -> dispatch.rs:789).
  * Shapes as mx_mul_mv_id; `map` must come from mx_prepare_map0 with the same
  * ids, and its geometry must match (n_expert, t, top_k), else MX_ERR_SCRATCH
- * (dispatch.rs:886-896).  Supported: Q4_K, Q5_K, Q6_K, Q8_0. */
+ * (dispatch.rs:886-896).  Supported: Q4_K, Q5_K, Q6_K, Q8_0.
+ * When K is a multiple of 256 the projection runs on the prefill path's MFMA
+ * GEMM over x rounded to f16 (one power-of-two scale per x row); the f16 rows
+ * (t * x_per_row * (2k + 4) bytes) are stream-ordered memory from a library
+ * pool per device, which keeps its peak size reserved.  Other K run the
+ * fallback tiles with no temporary. */
 mx_status mx_mul_mm_id_shared(const mx_expert_stack *stack, const float *x, int64_t t,
                               int64_t x_per_row, int64_t k, const uint32_t *ids,
                               int64_t ids_t, int64_t top_k, const mx_map0 *map,
                               float *dst, mx_stream_t stream);
 
 /* Self-contained form (map0 + mm).  Replaces ops::mm_id::mul_mm_id
- * (mm_id.rs:16-18).  workspace >= mx_mul_mm_id_workspace_bytes(...). */
+ * (mm_id.rs:16-18).  workspace >= mx_mul_mm_id_workspace_bytes(...), 256-byte
+ * aligned: the map0, then (K a multiple of 256) x's f16 rows; results are
+ * bitwise those of mx_mul_mm_id_shared. */
 size_t mx_mul_mm_id_workspace_bytes(int64_t n_expert, int64_t t, int64_t top_k,
                                     int64_t x_per_row, int64_t k);
 mx_status mx_mul_mm_id(const mx_expert_stack *stack, const float *x, int64_t t,

@@ -173,9 +173,93 @@ mx_status mx_prepare_map0(int64_t n_expert, const uint32_t *ids, int64_t t, int6
     if (scratch_bytes < need)
         return fail(MX_ERR_SCRATCH, "map0: scratch of %zu bytes, need %zu", scratch_bytes, need);
     if (t > 0 && !ids) return fail(MX_ERR_NULL, "map0: ids is NULL");
+    // m-tiles of GM_BM pairs: the tiles of the prefill GEMM, which the mm_id
+    // projections run on (the fallback tiles take each as two halves)
     return launch_map0(ids, (int)t, (int)top_k, (int)n_expert, static_cast<int32_t *>(scratch),
-                       (hipStream_t)stream);
+                       (hipStream_t)stream, GM_BM);
 }
+
+}  // extern "C"
+
+namespace {
+// Stream-ordered temporaries come from one memory pool per device that keeps
+// what it has reserved (release threshold: never), so a repeated call of the
+// same size reuses its memory instead of mapping it again.
+std::mutex g_pool_mu;
+hipMemPool_t g_pool[64] = {};
+
+mx_status pool_alloc(size_t bytes, hipStream_t s, void **out) {
+    int dev = -1;
+    MX_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= 64) return fail(MX_ERR_SHAPE, "pool: device %d out of range", dev);
+    hipMemPool_t pool;
+    {
+        std::lock_guard<std::mutex> lock(g_pool_mu);
+        if (!g_pool[dev]) {
+            hipMemPoolProps props{};
+            props.allocType = hipMemAllocationTypePinned;
+            props.location.type = hipMemLocationTypeDevice;
+            props.location.id = dev;
+            hipMemPool_t p = nullptr;
+            MX_HIP(hipMemPoolCreate(&p, &props));
+            uint64_t keep = UINT64_MAX;
+            MX_HIP(hipMemPoolSetAttribute(p, hipMemPoolAttrReleaseThreshold, &keep));
+            g_pool[dev] = p;
+        }
+        pool = g_pool[dev];
+    }
+    MX_HIP(hipMallocFromPoolAsync(out, bytes, pool, s));
+    return MX_OK;
+}
+
+// bytes of x's f16 rows and their scales for the GEMM route
+size_t mm_x16_bytes(int64_t t, int64_t x_per_row, int64_t k) {
+    return (((size_t)(t * x_per_row * k) * 2 + 255) & ~size_t(255)) + (size_t)(t * x_per_row) * 4;
+}
+// the grouped GEMM of the prefill path takes a projection whose K is whole
+// super-blocks and whose operand spans fit its 32-bit offsets; the rest run the
+// fallback tiles
+bool mm_on_gemm(const mx_expert_stack *st, const StackGeom &g, int64_t t, int64_t x_per_row) {
+    // A rows: x's token rows (x_per_row == 1) or a bucket-ordered tile (mm_gemm)
+    return gemm_supported(st->dtype, (int)st->k) &&
+           gemm_plain_fits(x_per_row == 1 ? t : GM_BM, (int)st->k, (int)st->n_out, g.row_bytes);
+}
+mx_status mm_fallback(const mx_expert_stack *st, const StackGeom &g, const float *x, int64_t t, int64_t x_per_row,
+                      int64_t top_k, const int32_t *map, float *dst, hipStream_t s) {
+    MmArgs a{g.w, g.expert_bytes, g.row_bytes, (int)st->n_expert, (int)st->n_out, (int)st->k,
+             x, (int)x_per_row, (int)t, (int)top_k, map, dst};
+    return launch_mul_mm_id(st->dtype, a, s);
+}
+// x -> scaled f16 rows in tmp (mm_x16_bytes, 256-aligned), then the plain GEMM
+// with one output row per pair (row token * top_k + slot of dst)
+mx_status mm_gemm(const mx_expert_stack *st, const StackGeom &g, const float *x, int64_t t, int64_t x_per_row,
+                  int64_t top_k, const int32_t *map, void *tmp, float *dst, hipStream_t s) {
+    const int k = (int)st->k;
+    _Float16 *x16 = static_cast<_Float16 *>(tmp);
+    float *x16s = reinterpret_cast<float *>(static_cast<uint8_t *>(tmp) +
+                                            (((size_t)(t * x_per_row * k) * 2 + 255) & ~size_t(255)));
+    // one x row per pair (x_per_row == top_k): gathered into bucket order, so a
+    // tile's A rows are consecutive (rows past the map's pair count are skipped);
+    // one per token: the token's row, shared by its slots
+    const MapLayout L((int)st->n_expert, (int)t, (int)top_k);
+    const bool by_pair = x_per_row != 1;
+    if (by_pair)
+        MX_TRY(launch_to_f16_rows(x, t * top_k, k, map + L.off + st->n_expert, x16, x16s, s, false, map + L.list));
+    else
+        MX_TRY(launch_to_f16_rows(x, t, k, nullptr, x16, x16s, s));
+    GemmArgs a{};
+    a.w[0] = g.w;
+    a.expert_bytes = g.expert_bytes; a.row_bytes = g.row_bytes; a.sh_row_bytes = g.row_bytes;
+    a.n_expert = (int)st->n_expert; a.n_out = (int)st->n_out; a.k = k;
+    a.a = x16; a.a_scale = x16s;
+    a.a_div = by_pair ? 0 : (int)top_k;  // bucket position / token of the pair
+    a.t = (int)t; a.top_k = (int)top_k; a.n_map_expert = (int)st->n_expert; a.map = map;
+    a.out = dst; a.out_stride = (int)top_k; a.out_add = 0;
+    return launch_gemm(st->dtype, false, a, s);
+}
+}  // namespace
+
+extern "C" {
 
 mx_status mx_mul_mm_id_shared(const mx_expert_stack *stack, const float *x, int64_t t, int64_t x_per_row,
                               int64_t k, const uint32_t *ids, int64_t ids_t, int64_t top_k,
@@ -193,15 +277,22 @@ mx_status mx_mul_mm_id_shared(const mx_expert_stack *stack, const float *x, int6
     if (map->bytes < map0_bytes((int)map->n_expert, (int)t, (int)top_k))
         return fail(MX_ERR_SCRATCH, "shared map0 scratch too small");
     if (t == 0) return MX_OK;
-    MmArgs a{g.w, g.expert_bytes, g.row_bytes, (int)stack->n_expert, (int)stack->n_out, (int)stack->k,
-             x, (int)x_per_row, (int)t, (int)top_k, static_cast<const int32_t *>(map->buffer), dst};
-    return launch_mul_mm_id(stack->dtype, a, (hipStream_t)stream);
+    const hipStream_t s = (hipStream_t)stream;
+    const int32_t *mp = static_cast<const int32_t *>(map->buffer);
+    if (!mm_on_gemm(stack, g, t, x_per_row)) return mm_fallback(stack, g, x, t, x_per_row, top_k, mp, dst, s);
+    // no workspace in this interface (mm_id.rs:32-39): x's f16 rows live in
+    // stream-ordered memory of the library's pool for the length of the call
+    void *tmp = nullptr;
+    MX_TRY(pool_alloc(mm_x16_bytes(t, x_per_row, stack->k), s, &tmp));
+    const mx_status rc = mm_gemm(stack, g, x, t, x_per_row, top_k, mp, tmp, dst, s);
+    MX_HIP(hipFreeAsync(tmp, s));
+    return rc;
 }
 
 size_t mx_mul_mm_id_workspace_bytes(int64_t n_expert, int64_t t, int64_t top_k, int64_t x_per_row, int64_t k) {
-    (void)x_per_row;
-    (void)k;
-    return mx_map0_scratch_bytes(n_expert, t, top_k);
+    // map0, then (GEMM route) x's f16 rows and their scales
+    const size_t map = (mx_map0_scratch_bytes(n_expert, t, top_k) + 255) & ~size_t(255);
+    return k > 0 && k % 256 == 0 ? map + mm_x16_bytes(t, x_per_row, k) : map;
 }
 
 mx_status mx_mul_mm_id(const mx_expert_stack *stack, const float *x, int64_t t, int64_t x_per_row, int64_t k,
@@ -211,9 +302,17 @@ mx_status mx_mul_mm_id(const mx_expert_stack *stack, const float *x, int64_t t, 
     MX_TRY(check_id_call(stack, x, t, x_per_row, k, ids, ids_t, top_k, dst, g));
     MX_TRY(check_map_geom(stack->n_expert, t, top_k));
     if (t == 0) return MX_OK;
-    MX_TRY(mx_prepare_map0(stack->n_expert, ids, t, top_k, workspace, workspace_bytes, stream));
-    mx_map0 m{workspace, workspace_bytes, stack->n_expert, t, top_k};
-    return mx_mul_mm_id_shared(stack, x, t, x_per_row, k, ids, ids_t, top_k, &m, dst, stream);
+    const size_t need = mx_mul_mm_id_workspace_bytes(stack->n_expert, t, top_k, x_per_row, k);
+    if (!workspace) return fail(MX_ERR_NULL, "mul_mm_id: workspace is NULL");
+    if (workspace_bytes < need)
+        return fail(MX_ERR_SCRATCH, "mul_mm_id: workspace of %zu bytes, need %zu", workspace_bytes, need);
+    const size_t map_bytes = (mx_map0_scratch_bytes(stack->n_expert, t, top_k) + 255) & ~size_t(255);
+    MX_TRY(mx_prepare_map0(stack->n_expert, ids, t, top_k, workspace, map_bytes, stream));
+    const hipStream_t s = (hipStream_t)stream;
+    const int32_t *mp = static_cast<const int32_t *>(workspace);
+    if (!mm_on_gemm(stack, g, t, x_per_row)) return mm_fallback(stack, g, x, t, x_per_row, top_k, mp, dst, s);
+    if (!aligned(workspace, 256)) return fail(MX_ERR_ALIGN, "mul_mm_id: workspace must be 256-byte aligned");
+    return mm_gemm(stack, g, x, t, x_per_row, top_k, mp, static_cast<uint8_t *>(workspace) + map_bytes, dst, s);
 }
 
 mx_status mx_check_ids(const uint32_t *ids, int64_t t, int64_t top_k, int64_t n_expert, uint32_t *flags,
@@ -741,7 +840,7 @@ mx_status moe_forward_impl(const mx_moe_layer *L, const float *x, int64_t t, con
         ga.w_sh[0] = shg; ga.w_sh[1] = shu;
         ga.expert_bytes = geo_gu.expert_bytes; ga.row_bytes = geo_gu.row_bytes; ga.sh_row_bytes = geo_sgu.row_bytes;
         ga.n_expert = n_routed; ga.n_out = (int)FF; ga.k = (int)H;
-        ga.a = o.x16; ga.a_scale = o.x16s; ga.a_by_token = 1;
+        ga.a = o.x16; ga.a_scale = o.x16s; ga.a_div = top_k;
         ga.t = (int)t; ga.top_k = top_k; ga.n_map_expert = n_map_expert; ga.map = map;
         ga.out = o.act + act_row0 * FF;
         MX_TRY(launch_gemm(dt_gu, true, ga, s));
@@ -754,7 +853,7 @@ mx_status moe_forward_impl(const mx_moe_layer *L, const float *x, int64_t t, con
         da.w_sh[0] = shd; da.w_sh[1] = nullptr;
         da.expert_bytes = geo_d.expert_bytes; da.row_bytes = geo_d.row_bytes; da.sh_row_bytes = geo_sd.row_bytes;
         da.n_out = (int)H; da.k = (int)FF;
-        da.a = o.act16 + act_row0 * FF; da.a_scale = o.act16s + act_row0; da.a_by_token = 0;
+        da.a = o.act16 + act_row0 * FF; da.a_scale = o.act16s + act_row0; da.a_div = 0;
         da.out = o.down; da.out_stride = KK; da.out_add = out_add;
         MX_TRY(launch_gemm(dt_d, false, da, s));
         MX_STAGE();

@@ -188,10 +188,10 @@ __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
             const int r = min(tid, tl.mrows - 1);  // rows past the tile repeat its last row
             const int pos = tl.pos0 + r;
             const int pair = a.map[L.list + pos];
-            const int64_t arow = a.a_by_token ? pair / a.top_k : pos;
+            const int64_t arow = a.a_div ? pair / a.a_div : pos;
             // rows ascend within a tile (tokens ascend within a bucket), so the
-            // offsets from the first row stay below (t or GM_BM) * k * 2 bytes
-            const int64_t arow0 = a.a_by_token ? a.map[L.list + tl.pos0] / a.top_k : tl.pos0;
+            // offsets from the first row stay below (A rows or GM_BM) * k * 2 bytes
+            const int64_t arow0 = a.a_div ? a.map[L.list + tl.pos0] / a.a_div : tl.pos0;
             s_src[tid] = (uint32_t)((arow - arow0) * a.k * 2);
             s_scale[tid] = a.a_scale[arow];
             s_out[tid] = SWIGLU ? pos : pair / a.top_k * a.out_stride + pair % a.top_k + a.out_add;
@@ -262,7 +262,7 @@ __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
     __syncthreads();
 
     const MapLayout L0(a.n_map_expert, a.t, a.top_k);
-    const int64_t arow0 = a.a_by_token ? a.map[L0.list + tl.pos0] / a.top_k : tl.pos0;
+    const int64_t arow0 = a.a_div ? a.map[L0.list + tl.pos0] / a.a_div : tl.pos0;
     const uint8_t *abase = reinterpret_cast<const uint8_t *>(a.a) + arow0 * a.k * 2;  // tile's first A row
     // A stage copy: wave instruction i fills LDS rows 4 (8 wave + i) + lane / 16
     auto issue_a = [&](int ks, uint8_t *buf) MX_INLINE_LAMBDA {
@@ -439,11 +439,13 @@ __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
 template <int RPT, bool PERM>
 __global__ void __launch_bounds__(256) k_to_f16_rows(const float *__restrict__ x, int k,
                                                      const int32_t *__restrict__ count,
+                                                     const int32_t *__restrict__ src,
                                                      _Float16 *__restrict__ y, float *__restrict__ scale) {
     const int64_t row = blockIdx.x;
     if (count && row >= *count) return;
+    const int64_t xr = src ? src[row] : row;
     __shared__ float s_red[4];
-    f16_row<RPT, PERM>(x + row * k, k, y + row * k, scale + row, s_red);
+    f16_row<RPT, PERM>(x + xr * k, k, y + row * k, scale + row, s_red);
 }
 
 // out = residual + (sum_s w_s down_s) + shared   (moe.rs:78; combine.metal:16-40 order)
@@ -504,6 +506,10 @@ bool gemm_fits(int t, int hidden, int ff, int64_t gu_row_bytes, int64_t d_row_by
     return gemm_spans_fit(t, hidden, ff, gu_row_bytes) && gemm_spans_fit(GM_BM, ff, hidden, d_row_bytes);
 }
 
+bool gemm_plain_fits(int64_t a_rows, int k, int n_out, int64_t row_bytes) {
+    return gemm_spans_fit(a_rows, k, n_out, row_bytes);
+}
+
 mx_status launch_gemm(int dtype, bool swiglu, const GemmArgs &a, hipStream_t s) {
     if (a.t == 0) return MX_OK;
     const MapLayout L(a.n_map_expert, a.t, a.top_k);
@@ -518,7 +524,7 @@ mx_status launch_gemm(int dtype, bool swiglu, const GemmArgs &a, hipStream_t s) 
     const int64_t t_max = ((int64_t)a.t * a.top_k + GM_BM - 1) / GM_BM + a.n_map_expert;  // m-tiles of GM_BM
     // the kernel addresses a tile's A rows from its first row, and one expert's
     // weight rows from the expert, with 32-bit offsets
-    const int64_t a_span = a.a_by_token ? a.t : GM_BM;
+    const int64_t a_span = a.a_div ? ((int64_t)a.t * a.top_k + a.a_div - 1) / a.a_div : GM_BM;
     if (!gemm_spans_fit(a_span, a.k, a.n_out, a.row_bytes > a.sh_row_bytes ? a.row_bytes : a.sh_row_bytes))
         return fail(MX_ERR_OVERFLOW, "gemm: an operand span beyond 4 GiB (t * k * 2 bytes of x); split the batch");
     const int64_t blocks = (t_max * nt + 7) / 8 * 8;
@@ -538,19 +544,21 @@ mx_status launch_gemm(int dtype, bool swiglu, const GemmArgs &a, hipStream_t s) 
 }
 
 template <bool PERM>
-static void to_f16_rows(const float *x, int64_t rows, int k, const int32_t *count, _Float16 *y, float *scale,
-                        hipStream_t s) {
+static void to_f16_rows(const float *x, int64_t rows, int k, const int32_t *count, const int32_t *src, _Float16 *y,
+                        float *scale, hipStream_t s) {
     const dim3 grid((unsigned)rows);
-    if (k <= 1024 * 2) hipLaunchKernelGGL((k_to_f16_rows<2, PERM>), grid, dim3(256), 0, s, x, k, count, y, scale);
-    else if (k <= 1024 * 4) hipLaunchKernelGGL((k_to_f16_rows<4, PERM>), grid, dim3(256), 0, s, x, k, count, y, scale);
-    else hipLaunchKernelGGL((k_to_f16_rows<0, PERM>), grid, dim3(256), 0, s, x, k, count, y, scale);
+    if (k <= 1024 * 2)
+        hipLaunchKernelGGL((k_to_f16_rows<2, PERM>), grid, dim3(256), 0, s, x, k, count, src, y, scale);
+    else if (k <= 1024 * 4)
+        hipLaunchKernelGGL((k_to_f16_rows<4, PERM>), grid, dim3(256), 0, s, x, k, count, src, y, scale);
+    else hipLaunchKernelGGL((k_to_f16_rows<0, PERM>), grid, dim3(256), 0, s, x, k, count, src, y, scale);
 }
 
 mx_status launch_to_f16_rows(const float *x, int64_t rows, int k, const int32_t *count, _Float16 *y, float *scale,
-                             hipStream_t s, bool perm) {
+                             hipStream_t s, bool perm, const int32_t *src) {
     if (rows == 0) return MX_OK;
-    if (perm) to_f16_rows<true>(x, rows, k, count, y, scale, s);
-    else to_f16_rows<false>(x, rows, k, count, y, scale, s);
+    if (perm) to_f16_rows<true>(x, rows, k, count, src, y, scale, s);
+    else to_f16_rows<false>(x, rows, k, count, src, y, scale, s);
     MX_LAUNCH("k_to_f16_rows");
     return MX_OK;
 }

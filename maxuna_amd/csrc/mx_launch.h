@@ -220,7 +220,8 @@ struct GemmArgs {
     int n_expert, n_out, k;     // k % 256 == 0
     const _Float16 *a;          // [rows, k]
     const float *a_scale;       // [rows]
-    int a_by_token;             // 1: A row = pair / top_k, 0: A row = bucket position
+    int a_div;                  // > 0: A row = pair / a_div (top_k: one row per token, 1: one
+                                // per pair), 0: A row = bucket position
     int t, top_k, n_map_expert; // map geometry
     const int32_t *map;         // built with bm = GM_BM
     float *out;                 // SwiGLU: act [position, n_out]; plain: rows
@@ -231,12 +232,15 @@ bool gemm_supported(int dtype, int k);
 // the kernel's 32-bit operand offsets hold for t tokens of x [t, hidden] and
 // weight rows of these byte widths
 bool gemm_fits(int t, int hidden, int ff, int64_t gu_row_bytes, int64_t d_row_bytes);
+// the same for one plain GEMM over a_rows A rows addressed by pair (a_div > 0)
+bool gemm_plain_fits(int64_t a_rows, int k, int n_out, int64_t row_bytes);
 mx_status launch_gemm(int dtype, bool swiglu, const GemmArgs &a, hipStream_t s);
 // rows of x (f32, [rows, k], k % 4 == 0) -> f16 times a per-row power of two;
 // rows at or beyond *count (when count != NULL) are skipped.  perm: each group of
-// four values stored in the order 0, 2, 1, 3 (the K order of the Q4_K verify tiles)
+// four values stored in the order 0, 2, 1, 3 (the K order of the Q4_K verify tiles);
+// src (when not NULL): output row r holds x row src[r] (a gather, e.g. into bucket order)
 mx_status launch_to_f16_rows(const float *x, int64_t rows, int k, const int32_t *count, _Float16 *y,
-                             float *scale, hipStream_t s, bool perm = false);
+                             float *scale, hipStream_t s, bool perm = false, const int32_t *src = nullptr);
 // out[t, n] = residual + (sum_s w[t, s] * down[t * kk + s] + shared), kk = top_k + has_shared,
 // shared = down[t * kk + top_k] (has_shared), shared_sep[t] (shared_sep != NULL) or 0; n % 4 == 0
 mx_status launch_combine_prefill(const float *down, const float *w, const float *residual, int t, int top_k,

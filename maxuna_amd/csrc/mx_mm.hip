@@ -3,11 +3,14 @@
 // 1. Bucket pass (replaces kernel_mul_mm_id_map0, mm_id.metal:207-259): per
 //    expert, the flattened (token*top_k + slot) pairs routed to it, tokens
 //    ascending, compacted into one list with per-expert offsets, plus a list
-//    of (expert, 64-pair m-tile) work items.  Built as chunked histogram ->
-//    scan -> ordered fill, so no thread walks all t*top_k ids.
-// 2. Grouped GEMM (replaces kernel_mul_mm_id_*_t, mm_id.metal:492-647): one
-//    block per (work item, 64-row n-tile).  Each 256-wide K step dequantises
-//    the expert's 64x256 weight tile from raw GGUF blocks into LDS as f16,
+//    of (expert, m-tile) work items (m-tiles of `bm` pairs; the mm_id
+//    projections use GM_BM).  Built as chunked histogram -> scan -> ordered
+//    fill, so no thread walks all t*top_k ids.
+// 2. Fallback grouped GEMM (replaces kernel_mul_mm_id_*_t, mm_id.metal:492-647,
+//    for the projections the MFMA GEMM of the prefill path does not take: K not
+//    a whole number of 256-weight super-blocks, or operand spans past its 32-bit
+//    offsets): one block per (half of a GM_BM work item, 64-row n-tile).
+//    Each 256-wide K step dequantises the expert's 64x256 weight tile from raw GGUF blocks into LDS as f16,
 //    gathers the 64 token rows of x into LDS as f16 with a per-(row, K-step)
 //    power-of-two scale (so any f32 magnitude fits f16 without rounding the
 //    scale), and contracts on v_mfma_f32_16x16x32_f16 with f32 accumulation;
@@ -389,13 +392,15 @@ __global__ void __launch_bounds__(256) k_mul_mm_id(MmArgs a) {
     __shared__ float s_scale[MM_BM];
     __shared__ int s_pair[MM_BM];
     const MapLayout L(a.n_expert, a.t, a.top_k);
-    const int tile = blockIdx.x;
+    // the map's m-tiles hold GM_BM pairs: block pairs 2i, 2i + 1 take the halves of tile i
+    const int tile = blockIdx.x >> 1;
     if (tile >= a.map[L.n_tiles]) return;  // block-uniform
     const int item = a.map[L.tiles + tile];
     const int e = item >> 16, mt = item & 0xFFFF;
     const int cnt = a.map[L.tpe + e];
-    const int m0 = mt * MM_BM;
+    const int m0 = mt * GM_BM + (blockIdx.x & 1) * MM_BM;
     const int mrows = min(MM_BM, cnt - m0);
+    if (mrows <= 0) return;
     const int n0 = blockIdx.y * MM_BN;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     if (tid < MM_BM) s_pair[tid] = tid < mrows ? a.map[L.list + a.map[L.off + e] + m0 + tid] : -1;
@@ -500,9 +505,10 @@ __global__ void __launch_bounds__(256) k_mul_mm_id(MmArgs a) {
 }
 
 mx_status launch_mul_mm_id(int dtype, const MmArgs &a, hipStream_t s) {
-    const MapLayout L(a.n_expert, a.t, a.top_k);
     if (a.t == 0) return MX_OK;
-    const dim3 grid((unsigned)L.t_max, (unsigned)((a.n_out + MM_BN - 1) / MM_BN));
+    static_assert(GM_BM == 2 * MM_BM, "a map tile is two fallback tiles");
+    const int64_t tiles = ((int64_t)a.t * a.top_k + GM_BM - 1) / GM_BM + a.n_expert;  // m-tiles of GM_BM
+    const dim3 grid((unsigned)(2 * tiles), (unsigned)((a.n_out + MM_BN - 1) / MM_BN));
     switch (dtype) {
     case kQ4_K: hipLaunchKernelGGL(k_mul_mm_id<kQ4_K>, grid, dim3(256), 0, s, a); break;
     case kQ5_K: hipLaunchKernelGGL(k_mul_mm_id<kQ5_K>, grid, dim3(256), 0, s, a); break;

@@ -245,7 +245,8 @@ def test_mul_mm_id_matches_oracle(dev, orc, dt):
     key = int(rng.integers(0, 2**62))
     blocks = {e: orc.expert_blocks(int(dt), key, e, n_out, k) for e in range(n_expert)}
     st = upload_stack(dt, blocks, n_expert, n_out, k)
-    for t, top_k in [(16, 2), (64, 10), (130, 4)]:
+    # (600, 8): about 300 pairs per expert, so experts span several 128-pair m-tiles
+    for t, top_k in [(16, 2), (64, 10), (130, 4), (600, 8)]:
         for xpr in (1, top_k):
             _log(f"mm_id {dt.name} t={t} k={top_k} xpr={xpr}")
             ids = _distinct_ids(rng, t, top_k, n_expert)
@@ -253,6 +254,27 @@ def test_mul_mm_id_matches_oracle(dev, orc, dt):
             got = host(ops.mul_mm_id(st, dev_f32(x), dev_u32(ids)))
             want = orc.mul_mv_id(int(dt), blocks, n_expert, n_out, k, x, ids)
             assert_close(got, want, what=f"mm {dt.name} t={t} xpr={xpr}")
+
+
+def test_mul_mm_id_fallback_tiles(dev, orc):
+    """Q8_0 with K = 288 (not whole 256-weight super-blocks) runs the fallback tiles,
+    which take each 128-pair m-tile of the map as two 64-pair halves."""
+    rng = np.random.default_rng(17)
+    dt, n_expert, n_out, k = GgmlDType.Q8_0, 8, 72, 288
+    key = int(rng.integers(0, 2**62))
+    blocks = {e: orc.expert_blocks(int(dt), key, e, n_out, k) for e in range(n_expert)}
+    st = upload_stack(dt, blocks, n_expert, n_out, k)
+    for t, top_k in [(5, 3), (200, 4)]:
+        for xpr in (1, top_k):
+            _log(f"mm_id fallback t={t} k={top_k} xpr={xpr}")
+            ids = _distinct_ids(rng, t, top_k, n_expert)
+            x = (rng.standard_normal((t, xpr, k)) * 10.0 ** rng.integers(-3, 4)).astype(np.float32)
+            xd, idd = dev_f32(x), dev_u32(ids)
+            got = host(ops.mul_mm_id(st, xd, idd))
+            want = orc.mul_mv_id(int(dt), blocks, n_expert, n_out, k, x, ids)
+            assert_close(got, want, what=f"mm fallback t={t} xpr={xpr}")
+            shared = host(ops.mul_mm_id_shared(st, xd, idd, ops.prepare_map0(n_expert, idd)))
+            assert np.array_equal(got.view(np.uint32), shared.view(np.uint32))
 
 
 def test_shared_map0_matches_self_contained(dev, orc):
