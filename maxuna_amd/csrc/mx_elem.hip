@@ -100,35 +100,67 @@ mx_status launch_add3(const float *a, const float *b, const float *c, int64_t n,
 }
 
 // Routing-id validation: flags = (1 if some token repeats an id across its
-// top_k slots) | (2 if some id >= n_expert).  One block walks every token, so
-// the flag word is written once, by a plain store (no memset, no atomics).
+// top_k slots) | (2 if some id >= n_expert).  Up to CHECK_ONE_BLOCK pairs one
+// block walks every token and writes the flag word once by a plain store (no
+// clearing launch, no atomics).  Larger batches: a grid of blocks, one token per
+// thread, each block ORing its flags (when set) into the word that a one-thread
+// launch cleared first.
+constexpr int64_t CHECK_ONE_BLOCK = 1 << 16;
+
+__device__ __forceinline__ uint32_t check_token(const uint32_t *__restrict__ r, int top_k, uint32_t n_expert) {
+    uint32_t f = 0;
+    for (int a = 0; a < top_k; a++) {
+        const uint32_t ia = r[a];
+        if (ia >= n_expert) f |= 2u;
+        for (int b = a + 1; b < top_k; b++)
+            if (r[b] == ia) f |= 1u;
+    }
+    return f;
+}
+
+// OR of f over the block, valid in thread 0
+__device__ __forceinline__ uint32_t block_or(uint32_t f, uint32_t *s_f) {
+    for (int off = 32; off > 0; off >>= 1) f |= (uint32_t)__shfl_xor((int)f, off, 64);
+    if ((threadIdx.x & 63) == 0) s_f[threadIdx.x >> 6] = f;
+    __syncthreads();
+    uint32_t v = 0;
+    if (threadIdx.x == 0)
+        for (int i = 0; i < (int)(blockDim.x >> 6); i++) v |= s_f[i];
+    return v;
+}
+
 __global__ void __launch_bounds__(1024) k_check_ids(const uint32_t *__restrict__ ids, int64_t t, int top_k,
                                                     uint32_t n_expert, uint32_t *__restrict__ flags) {
     __shared__ uint32_t s_f[16];
     uint32_t f = 0;
-    for (int64_t tok = threadIdx.x; tok < t; tok += blockDim.x) {
-        const uint32_t *r = ids + tok * top_k;
-        for (int a = 0; a < top_k; a++) {
-            const uint32_t ia = r[a];
-            if (ia >= n_expert) f |= 2u;
-            for (int b = a + 1; b < top_k; b++)
-                if (r[b] == ia) f |= 1u;
-        }
-    }
-    for (int off = 32; off > 0; off >>= 1) f |= (uint32_t)__shfl_xor((int)f, off, 64);
-    if ((threadIdx.x & 63) == 0) s_f[threadIdx.x >> 6] = f;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        uint32_t v = 0;
-        for (int i = 0; i < (int)(blockDim.x >> 6); i++) v |= s_f[i];
-        *flags = v;
-    }
+    for (int64_t tok = threadIdx.x; tok < t; tok += blockDim.x) f |= check_token(ids + tok * top_k, top_k, n_expert);
+    const uint32_t v = block_or(f, s_f);
+    if (threadIdx.x == 0) *flags = v;
+}
+
+__global__ void k_check_ids_clear(uint32_t *flags) { *flags = 0u; }
+
+__global__ void __launch_bounds__(256) k_check_ids_grid(const uint32_t *__restrict__ ids, int64_t t, int top_k,
+                                                        uint32_t n_expert, uint32_t *__restrict__ flags) {
+    __shared__ uint32_t s_f[4];
+    const int64_t tok = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const uint32_t f = tok < t ? check_token(ids + tok * top_k, top_k, n_expert) : 0u;
+    const uint32_t v = block_or(f, s_f);
+    if (threadIdx.x == 0 && v) atomicOr(flags, v);
 }
 
 mx_status launch_check_ids(const uint32_t *ids, int64_t t, int top_k, int n_expert, uint32_t *flags,
                            hipStream_t s) {
-    hipLaunchKernelGGL(k_check_ids, dim3(1), dim3(1024), 0, s, ids, t, top_k, (uint32_t)n_expert, flags);
-    MX_LAUNCH("k_check_ids");
+    if (t * top_k <= CHECK_ONE_BLOCK) {
+        hipLaunchKernelGGL(k_check_ids, dim3(1), dim3(1024), 0, s, ids, t, top_k, (uint32_t)n_expert, flags);
+        MX_LAUNCH("k_check_ids");
+        return MX_OK;
+    }
+    hipLaunchKernelGGL(k_check_ids_clear, dim3(1), dim3(1), 0, s, flags);
+    MX_LAUNCH("k_check_ids_clear");
+    hipLaunchKernelGGL(k_check_ids_grid, dim3((unsigned)((t + 255) / 256)), dim3(256), 0, s, ids, t, top_k,
+                       (uint32_t)n_expert, flags);
+    MX_LAUNCH("k_check_ids_grid");
     return MX_OK;
 }
 

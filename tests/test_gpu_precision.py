@@ -133,6 +133,17 @@ def test_check_ids(dev):
     assert ops.check_ids(dev_u32(both), 8, raise_on_error=False) == 3
     with pytest.raises(ops.MaxunaError, match="repeats an expert id"):
         ops.check_ids(dev_u32(dup), 8)
+    # beyond 65536 pairs the check runs as a grid of blocks: clean ids, then one bad
+    # token near the end of each kind (the flag word is cleared by the call itself)
+    rng = np.random.default_rng(3)
+    big = np.stack([rng.choice(64, 8, replace=False) for _ in range(20000)]).astype(np.uint32)
+    assert ops.check_ids(dev_u32(big), 64) == 0
+    for row, bad, want in ((19_999, [5, 5, 1, 2, 3, 4, 6, 7], ops.IDS_DUPLICATE),
+                           (17_123, [0, 1, 2, 3, 4, 5, 6, 64], ops.IDS_OUT_OF_RANGE)):
+        b2 = big.copy()
+        b2[row] = bad
+        assert ops.check_ids(dev_u32(b2), 64, raise_on_error=False) == want
+    assert ops.check_ids(dev_u32(big), 64) == 0
 
 
 def test_verify_tiles_outlier_channels(dev, orc):
