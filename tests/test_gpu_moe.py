@@ -109,6 +109,9 @@ SHAPES = {
     "h3072_ff2048_q8q8": LayerSpec(3072, 2048, 32, 4, GgmlDType.Q8_0, GgmlDType.Q8_0, shared=False),
     "h6144_ff2816_q6q4": LayerSpec(6144, 2816, 16, 4, GgmlDType.Q6_K, GgmlDType.Q4_K, shared=True),
     "h7168_ff2048_q4q5": LayerSpec(7168, 2048, 32, 8, GgmlDType.Q4_K, GgmlDType.Q5_K, shared=False),
+    # Q6_K down of ff 1536 with hidden not a multiple of 256 output rows: the
+    # compiled down kernels' row tiles do not divide it, so it takes the generic one
+    "h1056_ff1536_q8q6": LayerSpec(1056, 1536, 16, 4, GgmlDType.Q8_0, GgmlDType.Q6_K, shared=True),
 }
 
 
