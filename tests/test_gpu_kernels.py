@@ -256,6 +256,31 @@ def test_mul_mm_id_matches_oracle(dev, orc, dt):
             assert_close(got, want, what=f"mm {dt.name} t={t} xpr={xpr}")
 
 
+def test_mul_mm_id_prefill_size(dev, orc):
+    """The reference-API projections at prefill size (t = 2048, top-10; gate/up-like
+    Q4_K [1536 x 4096] with one x row per token, down-like Q6_K [4096 x 1536] with
+    one per pair): 64 sampled tokens against the oracle (rows are independent), and
+    the shared-map form bitwise equal to the self-contained one on every row."""
+    rng = np.random.default_rng(23)
+    t, top_k, n_expert = 2048, 10, 64
+    for dt, n_out, k, xpr in ((GgmlDType.Q4_K, 1536, 4096, 1), (GgmlDType.Q6_K, 4096, 1536, top_k)):
+        _log(f"mm_id prefill size {dt.name} [{n_out} x {k}] xpr={xpr}")
+        key = int(rng.integers(0, 2**62))
+        blocks = {e: orc.expert_blocks(int(dt), key, e, n_out, k) for e in range(n_expert)}
+        st = upload_stack(dt, blocks, n_expert, n_out, k)
+        ids = _distinct_ids(rng, t, top_k, n_expert)
+        x = rng.standard_normal((t, xpr, k)).astype(np.float32)
+        xd, idd = dev_f32(x), dev_u32(ids)
+        got = host(ops.mul_mm_id(st, xd, idd))
+        shared = host(ops.mul_mm_id_shared(st, xd, idd, ops.prepare_map0(n_expert, idd)))
+        assert np.array_equal(got.view(np.uint32), shared.view(np.uint32))
+        sub = np.sort(rng.choice(t, 64, replace=False))
+        want = orc.mul_mv_id(int(dt), blocks, n_expert, n_out, k, np.ascontiguousarray(x[sub]),
+                             np.ascontiguousarray(ids[sub]))
+        assert_close(got[sub], want, what=f"mm prefill size {dt.name}")
+        del st, xd
+
+
 def test_mul_mm_id_fallback_tiles(dev, orc):
     """Q8_0 with K = 288 (not whole 256-weight super-blocks) runs the fallback tiles,
     which take each 128-pair m-tile of the map as two 64-pair halves."""
