@@ -149,7 +149,10 @@ template <int DT, bool SWIGLU> struct BSlots {
     static constexpr int positions(int rows) { return rows * CPR + PAD * (rows / 16); }
 };
 
-template <int DT, bool SWIGLU>
+// FEW (plain tiles): compiled for m-tiles that are mostly partly filled, which
+// skip the MFMAs and A reads of their empty 32-row blocks (the SwiGLU tiles
+// always do)
+template <int DT, bool SWIGLU, bool FEW = false>
 __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
     __attribute__((amdgpu_waves_per_eu(GemmWpe<DT, SWIGLU>::v))) k_gemm(GemmArgs a) {
     constexpr int NB = GemmNb<DT, SWIGLU>::nb;
@@ -379,12 +382,18 @@ __global__ void __launch_bounds__((64 * GemmNb<DT, SWIGLU>::waves))
             stage_end();
         }
     };
-    // block-uniform: the tile's filled 32-row blocks (the SwiGLU tiles; the plain
-    // tiles keep the single loop, which the compiler schedules better there)
+    // block-uniform: the tile's filled 32-row blocks.  The plain tiles run full
+    // tiles in a loop of their own: as one more case of k_loop the compiler
+    // schedules it worse (C3 down 524 -> 571 us), and next to the smaller cases
+    // too (-> 541 us), so only the FEW instantiation carries those.
     if constexpr (SWIGLU) {
         if (tl.mrows > 64) k_loop(std::integral_constant<int, 4>{});
         else if (tl.mrows > 32) k_loop(std::integral_constant<int, 2>{});
         else k_loop(std::integral_constant<int, 1>{});
+    } else if (FEW && tl.mrows <= 32) {
+        k_loop(std::integral_constant<int, 1>{});
+    } else if (FEW && tl.mrows <= 64) {
+        k_loop(std::integral_constant<int, 2>{});
     } else {
         for (int ks = 0; ks < nks; ks += 2) {
             issue_a(ks + 1, sA1);
@@ -530,13 +539,18 @@ mx_status launch_gemm(int dtype, bool swiglu, const GemmArgs &a, hipStream_t s) 
     const int64_t blocks = (t_max * nt + 7) / 8 * 8;
     if (blocks > INT32_MAX) return fail(MX_ERR_OVERFLOW, "gemm: too many tiles");
     const dim3 grid((unsigned)blocks);
-#define MX_G(DT, SW) hipLaunchKernelGGL((k_gemm<DT, SW>), grid, dim3((64 * GemmNb<DT, SW>::waves)), 0, s, a)
+    // plain tiles: the FEW form when the average expert holds under 64 pairs
+    // (C3's down, 88 pairs per expert with the shared one, takes the full-tile form)
+    const bool few = !swiglu && (int64_t)a.t * a.top_k < (int64_t)64 * a.n_map_expert;
+#define MX_G(DT, SW, F) hipLaunchKernelGGL((k_gemm<DT, SW, F>), grid, dim3((64 * GemmNb<DT, SW>::waves)), 0, s, a)
+#define MX_P(DT) if (swiglu) MX_G(DT, true, false); else if (few) MX_G(DT, false, true); else MX_G(DT, false, false)
     switch (dtype) {
-    case kQ4_K: if (swiglu) MX_G(kQ4_K, true); else MX_G(kQ4_K, false); break;
-    case kQ5_K: if (swiglu) MX_G(kQ5_K, true); else MX_G(kQ5_K, false); break;
-    case kQ6_K: if (swiglu) MX_G(kQ6_K, true); else MX_G(kQ6_K, false); break;
-    default: if (swiglu) MX_G(kQ8_0, true); else MX_G(kQ8_0, false); break;
+    case kQ4_K: MX_P(kQ4_K); break;
+    case kQ5_K: MX_P(kQ5_K); break;
+    case kQ6_K: MX_P(kQ6_K); break;
+    default: MX_P(kQ8_0); break;
     }
+#undef MX_P
 #undef MX_G
     (void)L;
     MX_LAUNCH("k_gemm");
