@@ -208,12 +208,13 @@ mx_status mx_route_from_logits(const float *logits, const float *bias, int64_t t
  * Replaces MoeBlock::forward (src/moe.rs:73-78) with the FusedExperts runner
  * (moe.rs:221-323) and SharedExpert (moe.rs:327-345):
  *   out = FusedExperts(x, route(x)) + SharedExpert(x)
- * t < mm_min_seq runs the fused decode kernels -- from 16 tokens on as 16-pair
- * MFMA tiles with f16 operands (the grouped GEMM's precision class; fewer
- * tokens keep the f32-class mat-vecs) -- and t >= mm_min_seq the grouped GEMM
- * path (moe.rs:236-240).  mm_min_seq == 0 selects the default 32
- * (ops/mod.rs:31); mm_min_seq < 0 never uses the grouped GEMM nor the tiles
- * (LAGUNA_NO_MM_ID, ops/mod.rs:57-64).  The shared expert is optional (shared_gate.data == NULL).
+ * Fewer than 16 tokens run the f32-class fused decode kernels.  From 16 tokens
+ * on, the expert matmuls take f16 operands (the reference's grouped-matmul
+ * precision class): 16-pair MFMA tiles while t * (top_k + shared) <= 1024, the
+ * grouped GEMM beyond that for t >= mm_min_seq (moe.rs:236-240; mm_min_seq == 0
+ * selects the default 32, ops/mod.rs:31), else the decode kernels.
+ * mm_min_seq < 0 never uses the tiles nor the grouped GEMM (LAGUNA_NO_MM_ID,
+ * ops/mod.rs:57-64).  The shared expert is optional (shared_gate.data == NULL).
  * Optionally (rms_alpha != NULL) the block first applies RMSNorm(rms_eps) to
  * `x`: out = residual + MoE(RMSNorm(x)) -- the FFN half of a decoder layer
  * (model.rs:340-351).  `residual` may equal `out` (in-place update of the

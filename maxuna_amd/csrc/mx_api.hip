@@ -440,22 +440,27 @@ Plan plan_for(const mx_moe_layer *L, int64_t t) {
     if (L->shared_gate.data)
         shapes = shapes && gemm_fits((int)t, (int)L->hidden, (int)L->expert_ff, stack_row_bytes(L->shared_gate),
                                      stack_row_bytes(L->shared_down));
-    p.mm = L->mm_min_seq >= 0 && t >= p.min_seq && shapes;
     p.has_shared = L->shared_gate.data != nullptr;
     p.shared_in_decode = p.has_shared && L->shared_gate.dtype == L->gate.dtype &&
                          L->shared_down.dtype == L->down.dtype;
     const bool decode_fits = decode_gate_up_fits(L->gate.dtype, (int)L->hidden, stack_row_bytes(L->gate)) &&
                              decode_down_fits(L->down.dtype, (int)L->expert_ff, stack_row_bytes(L->down));
-    p.generic = !p.mm && !decode_fits;
-    p.fused_router = !p.mm && !p.generic && t <= route_fused_max_t();
     const int64_t slots = L->top_k + (p.shared_in_decode ? 1 : 0);
     const int64_t gu_rb = stack_row_bytes(L->gate), d_rb = stack_row_bytes(L->down);
-    // (LAGUNA_NO_MM_ID, mm_min_seq < 0, keeps every t on the mat-vec kernels)
-    p.vmm = p.fused_router && L->mm_min_seq >= 0 && t >= kVmmMinT &&
-            (!p.has_shared || p.shared_in_decode) && t * slots <= PAIR_ORDER_MAX && L->gate.n_expert <= 1024 &&
-            vmm_supported(L->gate.dtype, L->down.dtype, (int)L->hidden, (int)L->expert_ff, gu_rb, d_rb) &&
-            L->expert_ff * gu_rb < ((int64_t)1 << 31) && L->hidden * d_rb < ((int64_t)1 << 31) &&
-            (!p.has_shared || (stack_row_bytes(L->shared_gate) == gu_rb && stack_row_bytes(L->shared_down) == d_rb));
+    // 16-pair MFMA tiles: from kVmmMinT tokens up to the pair-order limit, also past
+    // mm_min_seq (the grouped GEMM's tiles are mostly empty there: measured
+    // 25-35% slower per layer from 32 to 93 tokens); LAGUNA_NO_MM_ID
+    // (mm_min_seq < 0) keeps every t on the mat-vec kernels
+    const bool vmm_ok =
+        L->mm_min_seq >= 0 && decode_fits && t >= kVmmMinT && (!p.has_shared || p.shared_in_decode) &&
+        t * slots <= PAIR_ORDER_MAX && L->gate.n_expert <= 1024 &&
+        vmm_supported(L->gate.dtype, L->down.dtype, (int)L->hidden, (int)L->expert_ff, gu_rb, d_rb) &&
+        L->expert_ff * gu_rb < ((int64_t)1 << 31) && L->hidden * d_rb < ((int64_t)1 << 31) &&
+        (!p.has_shared || (stack_row_bytes(L->shared_gate) == gu_rb && stack_row_bytes(L->shared_down) == d_rb));
+    p.mm = L->mm_min_seq >= 0 && t >= p.min_seq && shapes && !vmm_ok;
+    p.generic = !p.mm && !decode_fits;
+    p.fused_router = !p.mm && !p.generic && t <= route_fused_max_t();
+    p.vmm = vmm_ok;
     return p;
 }
 
@@ -654,7 +659,7 @@ mx_status moe_forward_impl(const mx_moe_layer *L, const float *x, int64_t t, con
 
     // routing (+ the RMSNorm of the FFN half when requested)
     // (verify tiles without RMSNorm: the router also writes the f16 x rows)
-    const bool x16_in_router = p.vmm && !L->rms_alpha;
+    const bool x16_in_router = p.vmm && p.fused_router && !L->rms_alpha;
     if (p.fused_router) {
         // logits -> keys/probs; the router also stages the (normalised) rows for the
         // decode expert kernels.  The top-k is its own launch (k_decode_select, below).
@@ -671,7 +676,7 @@ mx_status moe_forward_impl(const mx_moe_layer *L, const float *x, int64_t t, con
         MX_TRY(launch_route_logits(xin, L->router, (int)t, (int)H, (int)E, o.logits, s));
         MX_TRY(launch_route_select(o.logits, L->exp_probs_b, (int)t, (int)E, (int)K, scale, apply,
                                    L->weights_norm, ids, w, s));
-        if (!p.mm && !p.generic) MX_TRY(launch_stage_rows(xin, (int)t, (int)H, o.xstage, o.xstage_gm, s));
+        if (!p.mm && !p.generic && !p.vmm) MX_TRY(launch_stage_rows(xin, (int)t, (int)H, o.xstage, o.xstage_gm, s));
 
     }
     MX_STAGE();

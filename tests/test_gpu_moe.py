@@ -74,13 +74,13 @@ def test_verify_block(dev, orc, t):
 SWEEP_SPEC = LayerSpec(1024, 512, 64, 4, GgmlDType.Q4_K, GgmlDType.Q6_K, shared=True)
 
 
-@pytest.mark.parametrize("t", [1, 2, 3, 15, 16, 17, 31, 32, 33, 63, 64, 65, 100])
+@pytest.mark.parametrize("t", [1, 2, 3, 15, 16, 17, 31, 32, 33, 63, 64, 65, 100, 204, 205, 260])
 def test_t_sweep_across_path_boundaries(dev, orc, t):
     """One shared-expert layer (Q4_K gate/up, Q6_K down; hidden 1024, ff 512,
-    64 experts, top-4) at every t on either side of the path boundaries:
-    t = 1 (top-k in the gate/up blocks), 2..15 (mat-vecs in expert order),
-    16..31 (16-pair MFMA tiles), 32 and up (grouped GEMM), 33 and up (the
-    unfused router), against the oracle."""
+    64 experts, top-4 + shared: 5 slots) at every t on either side of the path
+    boundaries: t = 1 (top-k in the gate/up blocks), 2..15 (mat-vecs in expert
+    order), 16..204 (16-pair MFMA tiles, up to 1024 pairs), 33 and up (the
+    unfused router), 205 and up (grouped GEMM), against the oracle."""
     _log(f"sweep t={t}")
     layer = build_layer(SWEEP_SPEC, seed=1020)
     x = make_x(SWEEP_SPEC, 40 + t, t)
@@ -303,11 +303,12 @@ def test_laguna_geometry(dev, orc):
     moe_intermediate_size 1024, shared_expert_intermediate_size 1024, 256 experts,
     top-10) with the GGUF's expert_weights_scale 2.5 and norm on.  ff = 1024 has 32
     Q4_K groups per gate/up row and 4 Q6_K blocks per down row, so decode takes the
-    generic slot kernels (not the ff = 1536 compile-time forms); t = 6 and 16 are
-    verify blocks and t = 64 the grouped GEMM."""
+    generic slot kernels (not the ff = 1536 compile-time forms); t = 6 is a
+    verify block on them, t = 16 and 64 run the MFMA verify tiles and t = 100
+    the grouped GEMM."""
     spec = LayerSpec(3072, 1024, 256, 10, GgmlDType.Q4_K, GgmlDType.Q6_K, shared=True, weights_scale=2.5)
     layer = build_layer(spec, seed=1051)
-    for t in (1, 6, 16, 64):
+    for t in (1, 6, 16, 64, 100):
         _log(f"laguna geometry t={t}")
         x = make_x(spec, 61 + t, t)
         out, ids, w = run_block(layer, x)
@@ -380,13 +381,13 @@ def test_decode_down_compiled_shape_matches_generic(dev):
 def test_workspace_contents_do_not_matter(dev):
     """The workspace carries no state between calls: a forward whose workspace
     was filled with 0xFF bytes, or with random bytes, is bit-identical to one
-    whose workspace was zeroed -- for a decode token (t = 1), a verify block
-    (t = 16) and a grouped-GEMM block (t = 64 >= mm_min_seq)."""
+    whose workspace was zeroed -- for a decode token (t = 1), MFMA verify tiles
+    (t = 16, and t = 64 past mm_min_seq) and a grouped-GEMM block (t = 100)."""
     spec = CONFIGS["C2"]["spec"]
     layer = build_layer(spec, seed=1305)
     blk = layer.block
     gen = torch.Generator(device="cuda").manual_seed(5)
-    for t in (1, 16, 64):
+    for t in (1, 16, 64, 100):
         _log(f"workspace fill t={t}")
         x = dev_f32(make_x(spec, 700 + t, t))
         ws = blk.workspace(t, x.device)

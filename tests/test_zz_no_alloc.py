@@ -54,26 +54,28 @@ def _largest_fitting_t(blk, cap):
 
 
 def test_noalloc_grouped_path_and_limit(dev):
-    """The grouped-GEMM path (t >= mm_min_seq) from the static scratch: the
-    largest t whose workspace fits the 16 MiB scratch (57 for the C1 shape, as
-    the header states) runs bit-identical to the workspace forward, and t + 1 is
-    rejected with MX_ERR_SCRATCH before any launch."""
-    spec = CONFIGS["C2"]["spec"]
-    layer = build_layer(spec, seed=1307)
-    blk = layer.block
+    """The f16 grouped paths from the static scratch.  C1 shape: t = 32 and the
+    largest t whose workspace fits the 16 MiB scratch (57, as the header states)
+    run the 16-pair MFMA tiles; C0 shape (4 slots): its largest fitting t (540)
+    is past the tiles' 1024 pairs and runs the grouped GEMM (bucket map, GEMMs).
+    Each is bit-identical to the workspace forward, and t + 1 is rejected with
+    MX_ERR_SCRATCH before any launch."""
     cap = lib().mx_moe_forward_noalloc_max_bytes()
-    t_max = _largest_fitting_t(blk, cap)
-    assert t_max == 57, t_max
-    assert t_max >= ops.mm_id_min_seq()  # the grouped path runs from the scratch
-    for t in (ops.mm_id_min_seq(), t_max):
-        print(f"no-alloc grouped t={t}", flush=True)
-        x = dev_f32(make_x(spec, 900 + t, t))
-        want, wid, ww = blk.forward(x, return_routing=True)
-        got, gid, gw = blk.forward_noalloc(x, return_routing=True)
-        assert np.array_equal(host(got).view(np.uint32), host(want).view(np.uint32)), f"t={t}: out"
-        assert np.array_equal(host(gid), host(wid)), f"t={t}: ids"
-        assert np.array_equal(host(gw).view(np.uint32), host(ww).view(np.uint32)), f"t={t}: w"
-    x = dev_f32(make_x(spec, 999, t_max + 1))
-    with pytest.raises(ops.MaxunaError) as ei:
-        blk.forward_noalloc(x)
-    assert ei.value.code == MX_ERR_SCRATCH, ei.value
+    for cfg, seed, want_max, ts in (("C2", 1307, 57, (32,)), ("C0", 1308, 540, ())):
+        spec = CONFIGS[cfg]["spec"]
+        blk = build_layer(spec, seed=seed).block
+        t_max = _largest_fitting_t(blk, cap)
+        assert t_max == want_max, (cfg, t_max)
+        assert t_max >= ops.mm_id_min_seq()
+        for t in ts + (t_max,):
+            print(f"no-alloc grouped {cfg} t={t}", flush=True)
+            x = dev_f32(make_x(spec, 900 + t, t))
+            want, wid, ww = blk.forward(x, return_routing=True)
+            got, gid, gw = blk.forward_noalloc(x, return_routing=True)
+            assert np.array_equal(host(got).view(np.uint32), host(want).view(np.uint32)), f"t={t}: out"
+            assert np.array_equal(host(gid), host(wid)), f"t={t}: ids"
+            assert np.array_equal(host(gw).view(np.uint32), host(ww).view(np.uint32)), f"t={t}: w"
+        x = dev_f32(make_x(spec, 999, t_max + 1))
+        with pytest.raises(ops.MaxunaError) as ei:
+            blk.forward_noalloc(x)
+        assert ei.value.code == MX_ERR_SCRATCH, ei.value
