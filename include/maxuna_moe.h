@@ -210,7 +210,7 @@ mx_status mx_route_from_logits(const float *logits, const float *bias, int64_t t
  *   out = FusedExperts(x, route(x)) + SharedExpert(x)
  * Fewer than 16 tokens run the f32-class fused decode kernels.  From 16 tokens
  * on, the expert matmuls take f16 operands (the reference's grouped-matmul
- * precision class): 16-pair MFMA tiles while t * (top_k + shared) <= 1024, the
+ * precision class): 16-pair MFMA tiles while t * (top_k + shared) <= 2560, the
  * grouped GEMM beyond that for t >= mm_min_seq (moe.rs:236-240; mm_min_seq == 0
  * selects the default 32, ops/mod.rs:31), else the decode kernels.
  * mm_min_seq < 0 never uses the tiles nor the grouped GEMM (LAGUNA_NO_MM_ID,

@@ -398,6 +398,14 @@ constexpr bool kFuseSelect = MX_FUSE_SELECT != 0;
 #define MX_VMM_MIN_T 16
 #endif
 constexpr int64_t kVmmMinT = MX_VMM_MIN_T;
+// the tiles' upper end in (token, slot) pairs: the measured crossover with the
+// grouped GEMM on C1-shaped layers (11 slots; 4 layers replayed, µs, tiles vs
+// GEMM): t = 200: 760 vs 826, 256: 864 vs 862, 300: 945 vs 900
+#ifndef MX_VMM_MAX_PAIRS
+#define MX_VMM_MAX_PAIRS 2560
+#endif
+constexpr int64_t kVmmMaxPairs = MX_VMM_MAX_PAIRS;
+static_assert(kVmmMaxPairs <= PAIR_ORDER_MAX, "the pair order covers the tiles' range");
 
 struct Ws {
     uint8_t *base;
@@ -447,13 +455,13 @@ Plan plan_for(const mx_moe_layer *L, int64_t t) {
                              decode_down_fits(L->down.dtype, (int)L->expert_ff, stack_row_bytes(L->down));
     const int64_t slots = L->top_k + (p.shared_in_decode ? 1 : 0);
     const int64_t gu_rb = stack_row_bytes(L->gate), d_rb = stack_row_bytes(L->down);
-    // 16-pair MFMA tiles: from kVmmMinT tokens up to the pair-order limit, also past
+    // 16-pair MFMA tiles: from kVmmMinT tokens up to kVmmMaxPairs pairs, also past
     // mm_min_seq (the grouped GEMM's tiles are mostly empty there: measured
-    // 25-35% slower per layer from 32 to 93 tokens); LAGUNA_NO_MM_ID
-    // (mm_min_seq < 0) keeps every t on the mat-vec kernels
+    // 25-35% slower per C1-shaped layer from 32 to 93 tokens, 8% at 200);
+    // LAGUNA_NO_MM_ID (mm_min_seq < 0) keeps every t on the mat-vec kernels
     const bool vmm_ok =
         L->mm_min_seq >= 0 && decode_fits && t >= kVmmMinT && (!p.has_shared || p.shared_in_decode) &&
-        t * slots <= PAIR_ORDER_MAX && L->gate.n_expert <= 1024 &&
+        t * slots <= kVmmMaxPairs && L->gate.n_expert <= 1024 &&
         vmm_supported(L->gate.dtype, L->down.dtype, (int)L->hidden, (int)L->expert_ff, gu_rb, d_rb) &&
         L->expert_ff * gu_rb < ((int64_t)1 << 31) && L->hidden * d_rb < ((int64_t)1 << 31) &&
         (!p.has_shared || (stack_row_bytes(L->shared_gate) == gu_rb && stack_row_bytes(L->shared_down) == d_rb));
@@ -466,7 +474,7 @@ Plan plan_for(const mx_moe_layer *L, int64_t t) {
 
 // Verify blocks on the decode kernels launch their gate/up pairs in expert order.
 bool pair_order_used(int64_t t, int64_t slots, int64_t n_expert) {
-    return t > 1 && t * slots <= PAIR_ORDER_MAX && n_expert <= 1024;  // the top-k kernels' limit
+    return t > 1 && t * slots <= PAIR_ORDER_DECODE_MAX && n_expert <= 1024;  // the top-k kernels' limit
 }
 
 // Carves the workspace; with base == nullptr it only measures.

@@ -77,7 +77,15 @@ bool decode_gate_up_selects(int dtype, const DecodeGateUpArgs &a);
 // shared slot as expert n_expert) into perm, so the gate/up blocks of pairs that
 // share an expert run back to back on one XCD and the repeats read its L2.
 // t * slots <= PAIR_ORDER_MAX; the order within an expert is unspecified.
-constexpr int PAIR_ORDER_MAX = 1024;
+#ifndef MX_PAIR_ORDER_MAX
+#define MX_PAIR_ORDER_MAX 4096
+#endif
+constexpr int PAIR_ORDER_MAX = MX_PAIR_ORDER_MAX;
+constexpr int PAIR_ORDER_THREADS = 1024;  // one workgroup; each thread orders up to 4 pairs
+static_assert(PAIR_ORDER_MAX % PAIR_ORDER_THREADS == 0 && PAIR_ORDER_MAX <= 4 * PAIR_ORDER_THREADS,
+              "pairs per thread");
+// the decode kernels take expert-ordered pairs up to this many (verify blocks)
+constexpr int PAIR_ORDER_DECODE_MAX = 1024;
 // runs (optional, 2 * (t * slots + 1) words): runs[0] = the number of runs, run r
 // at runs[2 + 2r] = first perm position | pairs << 16 (1..16 pairs), runs[3 + 2r] =
 // its expert: every expert's pairs cut into consecutive runs of at most 16.

@@ -1175,36 +1175,44 @@ __global__ void __launch_bounds__(SEL_THREADS) k_decode_select(int top_k, Decode
                    sel.ids + (int64_t)blockIdx.x * top_k, sel.w + (int64_t)blockIdx.x * top_k, sh);
 }
 
-__global__ void __launch_bounds__(PAIR_ORDER_MAX) k_pair_order(const uint32_t *__restrict__ ids, int t, int top_k,
-                                                                int n_expert, int slots,
-                                                                int32_t *__restrict__ perm,
-                                                                int32_t *__restrict__ runs) {
+__global__ void __launch_bounds__(PAIR_ORDER_THREADS) k_pair_order(const uint32_t *__restrict__ ids, int t,
+                                                                    int top_k, int n_expert, int slots,
+                                                                    int32_t *__restrict__ perm,
+                                                                    int32_t *__restrict__ runs) {
+    constexpr int NT = PAIR_ORDER_THREADS, PPT = PAIR_ORDER_MAX / NT;  // pairs per thread
     __shared__ int cnt[SEL_MAX_E + 2];
-    __shared__ int s_scan[PAIR_ORDER_MAX];
+    __shared__ int s_scan[NT];
     const int tid = threadIdx.x, n = t * slots, ne = n_expert + 1;  // expert n_expert: the shared slot
-    for (int i = tid; i < ne; i += PAIR_ORDER_MAX) cnt[i] = 0;
+    for (int i = tid; i < ne; i += NT) cnt[i] = 0;
     __syncthreads();
-    int e = 0, rank = 0;
-    if (tid < n) {
-        const int tok = tid / slots, slot = tid % slots;
-        if (slot < top_k) {
-            const uint32_t id = ids[tok * top_k + slot];
-            e = id < (uint32_t)n_expert ? (int)id : n_expert - 1;  // as the expert kernels clamp it
-        } else {
-            e = n_expert;
+    // pair tid + NT j of this thread: its expert and its rank among the expert's pairs
+    int pe[PPT], rank[PPT];
+#pragma unroll
+    for (int j = 0; j < PPT; j++) {
+        const int v = tid + NT * j;
+        pe[j] = 0;
+        rank[j] = 0;
+        if (v < n) {
+            const int tok = v / slots, slot = v % slots;
+            int e = n_expert;
+            if (slot < top_k) {
+                const uint32_t id = ids[tok * top_k + slot];
+                e = id < (uint32_t)n_expert ? (int)id : n_expert - 1;  // as the expert kernels clamp it
+            }
+            pe[j] = e;
+            rank[j] = atomicAdd(&cnt[e], 1);
         }
-        rank = atomicAdd(&cnt[e], 1);
     }
     __syncthreads();
     // exclusive scan of the counts (low 16 bits) and of the 16-pair runs (high
-    // 16 bits; both totals <= PAIR_ORDER_MAX): each thread sums `per` experts
-    const int per = (ne + PAIR_ORDER_MAX - 1) / PAIR_ORDER_MAX;
+    // 16 bits; both totals <= PAIR_ORDER_MAX < 2^16): each thread sums `per` experts
+    const int per = (ne + NT - 1) / NT;
     const int e0 = min(tid * per, ne), e1 = min(e0 + per, ne);
     int sum = 0;
     for (int i = e0; i < e1; i++) sum += cnt[i] + (((cnt[i] + 15) >> 4) << 16);
     s_scan[tid] = sum;
     __syncthreads();
-    for (int d = 1; d < PAIR_ORDER_MAX; d <<= 1) {
+    for (int d = 1; d < NT; d <<= 1) {
         const int v = tid >= d ? s_scan[tid - d] : 0;
         __syncthreads();
         s_scan[tid] += v;
@@ -1222,16 +1230,20 @@ __global__ void __launch_bounds__(PAIR_ORDER_MAX) k_pair_order(const uint32_t *_
             }
         run += c;
     }
-    if (runs && tid == PAIR_ORDER_MAX - 1) runs[0] = s_scan[tid] >> 16;
+    if (runs && tid == NT - 1) runs[0] = s_scan[tid] >> 16;
     __syncthreads();
-    if (tid < n) perm[cnt[e] + rank] = tid | (e << 16);  // the expert rides along: no ids load downstream
+#pragma unroll
+    for (int j = 0; j < PPT; j++) {
+        const int v = tid + NT * j;
+        if (v < n) perm[cnt[pe[j]] + rank[j]] = v | (pe[j] << 16);  // the expert rides along: no ids load downstream
+    }
 }
 
 mx_status launch_pair_order(const uint32_t *ids, int t, int top_k, int n_expert, int slots, int32_t *perm,
                             hipStream_t s, int32_t *runs) {
     if ((int64_t)t * slots > PAIR_ORDER_MAX || n_expert > SEL_MAX_E)
         return fail(MX_ERR_SHAPE, "pair order: t * slots <= %d and n_expert <= %d", PAIR_ORDER_MAX, SEL_MAX_E);
-    hipLaunchKernelGGL(k_pair_order, dim3(1), dim3(PAIR_ORDER_MAX), 0, s, ids, t, top_k, n_expert, slots, perm,
+    hipLaunchKernelGGL(k_pair_order, dim3(1), dim3(PAIR_ORDER_THREADS), 0, s, ids, t, top_k, n_expert, slots, perm,
                        runs);
     MX_LAUNCH("k_pair_order");
     return MX_OK;

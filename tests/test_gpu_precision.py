@@ -108,11 +108,11 @@ def test_mv_id_wide_rows(dev, orc, dt, k):
 
 def test_workspace_reuse_across_t(dev, orc):
     """One block's workspace serves calls of any t in any order: a grouped-GEMM
-    call (t = 100), MFMA verify tiles (t = 64) and then verify blocks on the
+    call (t = 240), MFMA verify tiles (t = 64) and then verify blocks on the
     decode kernels (t = 12, 3) must each match the oracle."""
     spec = CONFIGS["C2"]["spec"]
     layer = build_layer(spec, seed=1102)
-    for t, seed in ((100, 1), (64, 5), (12, 2), (3, 3), (12, 4)):
+    for t, seed in ((240, 1), (64, 5), (12, 2), (3, 3), (12, 4)):
         _log(f"workspace reuse t={t}")
         x = make_x(spec, 300 + seed, t)
         out, ids, w = layer.block.forward(dev_f32(x), return_routing=True)

@@ -11,7 +11,8 @@ import torch
 
 from maxuna_amd import ops
 from maxuna_amd._lib import lib
-from maxuna_amd.synth import CONFIGS, build_layer, make_x
+from maxuna_amd.gguf import GgmlDType
+from maxuna_amd.synth import CONFIGS, LayerSpec, build_layer, make_x
 from tests.gpu_util import dev_f32, host
 
 pytestmark = pytest.mark.gpu
@@ -56,13 +57,16 @@ def _largest_fitting_t(blk, cap):
 def test_noalloc_grouped_path_and_limit(dev):
     """The f16 grouped paths from the static scratch.  C1 shape: t = 32 and the
     largest t whose workspace fits the 16 MiB scratch (57, as the header states)
-    run the 16-pair MFMA tiles; C0 shape (4 slots): its largest fitting t (540)
-    is past the tiles' 1024 pairs and runs the grouped GEMM (bucket map, GEMMs).
-    Each is bit-identical to the workspace forward, and t + 1 is rejected with
-    MX_ERR_SCRATCH before any launch."""
+    run the 16-pair MFMA tiles; a Q8_0 layer (hidden 1024, ff 512, 64 experts,
+    top-4; a type the tiles do not take) runs the grouped GEMM (bucket map,
+    GEMMs) at t = 32 and at its largest fitting t (540).  Each is bit-identical
+    to the workspace forward, and t + 1 is rejected with MX_ERR_SCRATCH before
+    any launch."""
     cap = lib().mx_moe_forward_noalloc_max_bytes()
-    for cfg, seed, want_max, ts in (("C2", 1307, 57, (32,)), ("C0", 1308, 540, ())):
-        spec = CONFIGS[cfg]["spec"]
+    q8 = LayerSpec(1024, 512, 64, 4, GgmlDType.Q8_0, GgmlDType.Q8_0, shared=False)
+    for spec, seed, want_max in ((CONFIGS["C2"]["spec"], 1307, 57), (q8, 1308, 540)):
+        cfg = f"{spec.gate_dt.name}/{spec.hidden}"
+        ts = (32,)
         blk = build_layer(spec, seed=seed).block
         t_max = _largest_fitting_t(blk, cap)
         assert t_max == want_max, (cfg, t_max)
