@@ -375,7 +375,14 @@ mx_status launch_route_logits(const float *x, const float *router, int t, int hi
 // Then, when x16 is given (no RMSNorm), one block per token writes its row as
 // f16 times a power of two (mx_f16row.h) for the MFMA verify tiles.
 constexpr int RF_MAX_T = 4;     // tokens per register pass
-constexpr int RF_TOKENS = 32;   // tokens per launch
+#ifndef MX_RF_TOKENS
+#define MX_RF_TOKENS 128
+#endif
+// tokens per launch: up to 128 the per-expert blocks beat the MFMA logits
+// kernel, whose few 32-token x 64-expert tiles leave most CUs idle at these t
+// (C1-shaped layer on the verify tiles, µs: t = 40: 451 -> 428, 64: 505 -> 485,
+// 96: 568 -> 550, 128: 627 -> 614; from 160 on equal)
+constexpr int RF_TOKENS = MX_RF_TOKENS;
 constexpr int RF_THREADS = 256;
 constexpr int RF_UNROLL = 4;  // float4 loads per thread per pass
 
@@ -460,7 +467,7 @@ __global__ void __launch_bounds__(RF_THREADS) k_route_fused(
     }
     if ((int)blockIdx.x >= n_eb) {
         // ---- staging blocks: quarter qi = 8 values of token qi / nq
-        __shared__ float s_m[RF_TOKENS];
+        __shared__ float s_m[RF_THREADS * 8 / 32 + 2];  // the RMS of the block's tokens (hidden >= 32)
         const int nq = hidden / 8;
         const int qi0 = (blockIdx.x - n_eb) * RF_THREADS;
         const int qi = qi0 + tid;

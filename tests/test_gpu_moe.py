@@ -74,12 +74,12 @@ def test_verify_block(dev, orc, t):
 SWEEP_SPEC = LayerSpec(1024, 512, 64, 4, GgmlDType.Q4_K, GgmlDType.Q6_K, shared=True)
 
 
-@pytest.mark.parametrize("t", [1, 2, 3, 15, 16, 17, 31, 32, 33, 63, 64, 65, 100, 300, 512, 513])
+@pytest.mark.parametrize("t", [1, 2, 3, 15, 16, 17, 31, 32, 33, 63, 64, 65, 100, 128, 129, 300, 512, 513])
 def test_t_sweep_across_path_boundaries(dev, orc, t):
     """One shared-expert layer (Q4_K gate/up, Q6_K down; hidden 1024, ff 512,
     64 experts, top-4 + shared: 5 slots) at every t on either side of the path
     boundaries: t = 1 (top-k in the gate/up blocks), 2..15 (mat-vecs in expert
-    order), 16..512 (16-pair MFMA tiles, up to 2560 pairs), 33 and up (the
+    order), 16..512 (16-pair MFMA tiles, up to 2560 pairs), 129 and up (the
     unfused router), 513 and up (grouped GEMM), against the oracle."""
     _log(f"sweep t={t}")
     layer = build_layer(SWEEP_SPEC, seed=1020)
