@@ -503,7 +503,7 @@ Layout carve(const mx_moe_layer *L, int64_t t, const Plan &p, void *base) {
     if (p.fused_router) {
         o.route_ws = ws.take<uint8_t>(route_fused_ws_bytes((int)t, (int)H, (int)E));
     } else {
-        o.logits = ws.take<float>(t * E);
+        o.logits = ws.take<float>(t * E * route_logits_splits((int)t, (int)L->hidden, (int)E));
     }
     if (p.generic) {
         const int64_t KK = K + (p.has_shared ? 1 : 0);
@@ -681,9 +681,10 @@ mx_status moe_forward_impl(const mx_moe_layer *L, const float *x, int64_t t, con
             MX_TRY(launch_rms_norm(x, L->rms_alpha, (int)t, (int)H, L->rms_eps, o.x_normed, s));
             xin = o.x_normed;
         }
-        MX_TRY(launch_route_logits(xin, L->router, (int)t, (int)H, (int)E, o.logits, s));
+        const int splits = route_logits_splits((int)t, (int)H, (int)E);
+        MX_TRY(launch_route_logits_split(xin, L->router, (int)t, (int)H, (int)E, o.logits, splits, s));
         MX_TRY(launch_route_select(o.logits, L->exp_probs_b, (int)t, (int)E, (int)K, scale, apply,
-                                   L->weights_norm, ids, w, s));
+                                   L->weights_norm, ids, w, s, splits));
         if (!p.mm && !p.generic && !p.vmm) MX_TRY(launch_stage_rows(xin, (int)t, (int)H, o.xstage, o.xstage_gm, s));
 
     }

@@ -134,9 +134,17 @@ mx_status launch_decode_down(int dtype, const DecodeDownArgs &a, hipStream_t s);
 // router: [n_expert, hidden] (GGUF ffn_gate_inp layout)
 mx_status launch_route_logits(const float *x, const float *router, int t, int hidden,
                               int n_expert, float *logits, hipStream_t s);
+// parts > 1: logits are launch_route_logits_split's partial sums, added first
 mx_status launch_route_select(const float *logits, const float *bias, int t, int n_expert,
                               int top_k, float scale, int apply_scale, int norm, uint32_t *ids,
-                              float *w, hipStream_t s);
+                              float *w, hipStream_t s, int parts = 1);
+// K splits of the logits GEMM for this shape (1: none): grids under 256
+// workgroups split K into 2, 4 or 8 parts
+int route_logits_splits(int t, int hidden, int n_expert);
+// the logits as `splits` partial sums parts[splits][t][n_expert] (splits ==
+// route_logits_splits(...); 1: the logits themselves)
+mx_status launch_route_logits_split(const float *x, const float *router, int t, int hidden, int n_expert,
+                                    float *parts, int splits, hipStream_t s);
 // Decode router, first half: RMSNorm (optional) + logits -> sigmoid
 // probabilities and selection sort keys for t tokens (ws: keys u64 [t, E] |
 // probs f32 [t, E]); also stages the (normalised) rows into `xstage`

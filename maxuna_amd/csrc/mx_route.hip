@@ -45,20 +45,33 @@ __device__ void select_token(const float *logits, const float *__restrict__ bias
     topk_select(key, prob, n_expert, top_k, scale, apply_scale, norm, ids_out, w_out, sh);
 }
 
-__global__ void __launch_bounds__(RT_THREADS) k_route_select(const float *__restrict__ logits,
+// parts > 1: logits holds `parts` partial sums [parts][t][n_expert] over K
+// (launch_route_logits_split), added in part order into the token's row first
+__global__ void __launch_bounds__(RT_THREADS) k_route_select(const float *__restrict__ logits, int parts, int t,
                                                              const float *__restrict__ bias, int n_expert,
                                                              int top_k, float scale, int apply_scale, int norm,
                                                              uint32_t *__restrict__ ids, float *__restrict__ w) {
+    __shared__ float s_row[SEL_MAX_E];
     const int tok = blockIdx.x;
-    select_token(logits + (int64_t)tok * n_expert, bias, n_expert, top_k, scale, apply_scale, norm,
-                 ids + (int64_t)tok * top_k, w + (int64_t)tok * top_k);
+    const float *row = logits + (int64_t)tok * n_expert;
+    if (parts > 1) {
+        for (int e = threadIdx.x; e < n_expert; e += RT_THREADS) {
+            float v = row[e];
+            for (int z = 1; z < parts; z++) v += row[(int64_t)z * t * n_expert + e];
+            s_row[e] = v;
+        }
+        __syncthreads();
+        row = s_row;
+    }
+    select_token(row, bias, n_expert, top_k, scale, apply_scale, norm, ids + (int64_t)tok * top_k,
+                 w + (int64_t)tok * top_k);
 }
 
 mx_status launch_route_select(const float *logits, const float *bias, int t, int n_expert, int top_k, float scale,
-                              int apply_scale, int norm, uint32_t *ids, float *w, hipStream_t s) {
+                              int apply_scale, int norm, uint32_t *ids, float *w, hipStream_t s, int parts) {
     if (t == 0) return MX_OK;
-    hipLaunchKernelGGL(k_route_select, dim3(t), dim3(RT_THREADS), 0, s, logits, bias, n_expert, top_k, scale,
-                       apply_scale, norm, ids, w);
+    hipLaunchKernelGGL(k_route_select, dim3(t), dim3(RT_THREADS), 0, s, logits, parts, t, bias, n_expert, top_k,
+                       scale, apply_scale, norm, ids, w);
     MX_LAUNCH("k_route_select");
     return MX_OK;
 }
@@ -207,6 +220,8 @@ static_assert(2 * RLL_STAGE >= RL_W * RL_T * RL_E * 4, "the reduction fits the s
 __global__ void __launch_bounds__(64 * RL_W) k_route_logits_lds(const float *__restrict__ x,
                                                                  const float *__restrict__ r, int t, int hidden,
                                                                  int n_expert, float *__restrict__ logits) {
+    // split K (gridDim.z > 1, small grids): block z sums stages [z nst / Z, (z + 1) nst / Z)
+    // into partial tile z of logits ([Z][t][n_expert]); the selection adds the parts
     // two separate objects: a copy into one buffer is not ordered against reads of the other
     __shared__ __attribute__((aligned(1024))) uint8_t sb0[RLL_STAGE];
     __shared__ __attribute__((aligned(1024))) uint8_t sb1[RLL_STAGE];
@@ -241,7 +256,13 @@ __global__ void __launch_bounds__(64 * RL_W) k_route_logits_lds(const float *__r
     float16_t acc0, acc1;
 #pragma unroll
     for (int q = 0; q < 16; q++) acc0[q] = acc1[q] = 0.f;
-    const int nst = hidden / RLL_KS;
+    const int nst = hidden / RLL_KS / (int)gridDim.z;  // stages of this block (the launcher checks divisibility)
+    {
+        const int64_t k0 = (int64_t)blockIdx.z * nst * RLL_KS;
+#pragma unroll
+        for (int u = 0; u < RLL_NI / RL_W; u++) src[u] += k0;
+        logits += (int64_t)blockIdx.z * t * n_expert;
+    }
     // stage st from cur while stage st + 1 is copied into nxt; the loop is unrolled
     // by two so each buffer is a compile-time object (a runtime choice between
     // them makes the compiler wait for every copy before any LDS read)
@@ -340,7 +361,7 @@ mx_status launch_route_logits(const float *x, const float *router, int t, int hi
         return MX_OK;
     }
     if (MX_RL_LDS && hidden % RLL_KS == 0 && t >= 8) {
-        const dim3 grid((unsigned)((n_expert + RL_E - 1) / RL_E), (unsigned)((t + RL_T - 1) / RL_T));
+        const dim3 grid((unsigned)((n_expert + RL_E - 1) / RL_E), (unsigned)((t + RL_T - 1) / RL_T), 1u);
         hipLaunchKernelGGL(k_route_logits_lds, grid, dim3(64 * RL_W), 0, s, x, router, t, hidden, n_expert, logits);
         MX_LAUNCH("k_route_logits_lds");
         return MX_OK;
@@ -354,6 +375,29 @@ mx_status launch_route_logits(const float *x, const float *router, int t, int hi
     const dim3 grid((unsigned)((n_expert + LG_E - 1) / LG_E), (unsigned)((t + LG_T - 1) / LG_T));
     hipLaunchKernelGGL(k_route_logits, grid, dim3(256), 0, s, x, router, t, hidden, n_expert, logits);
     MX_LAUNCH("k_route_logits");
+    return MX_OK;
+}
+
+#ifndef MX_RL_SPLIT
+#define MX_RL_SPLIT 1
+#endif
+int route_logits_splits(int t, int hidden, int n_expert) {
+    if (!MX_RL_SPLIT || !MX_RL_LDS || hidden % RLL_KS || t < RLR_T) return 1;
+    const int64_t blocks = (int64_t)((n_expert + RL_E - 1) / RL_E) * ((t + RL_T - 1) / RL_T);
+    int z = 1;
+    while (z < 8 && blocks * z * 2 <= 256 && (hidden / RLL_KS) % (z * 2) == 0) z *= 2;
+    return z;
+}
+
+mx_status launch_route_logits_split(const float *x, const float *router, int t, int hidden, int n_expert,
+                                    float *parts, int splits, hipStream_t s) {
+    if (t == 0) return MX_OK;
+    if (splits == 1) return launch_route_logits(x, router, t, hidden, n_expert, parts, s);
+    if (splits != route_logits_splits(t, hidden, n_expert))
+        return fail(MX_ERR_SHAPE, "route logits: %d K splits do not fit this shape", splits);
+    const dim3 grid((unsigned)((n_expert + RL_E - 1) / RL_E), (unsigned)((t + RL_T - 1) / RL_T), (unsigned)splits);
+    hipLaunchKernelGGL(k_route_logits_lds, grid, dim3(64 * RL_W), 0, s, x, router, t, hidden, n_expert, parts);
+    MX_LAUNCH("k_route_logits_lds");
     return MX_OK;
 }
 

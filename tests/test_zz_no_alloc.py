@@ -59,12 +59,12 @@ def test_noalloc_grouped_path_and_limit(dev):
     largest t whose workspace fits the 16 MiB scratch (57, as the header states)
     run the 16-pair MFMA tiles; a Q8_0 layer (hidden 1024, ff 512, 64 experts,
     top-4; a type the tiles do not take) runs the grouped GEMM (bucket map,
-    GEMMs) at t = 32 and at its largest fitting t (540).  Each is bit-identical
+    GEMMs) at t = 32 and at its largest fitting t (510).  Each is bit-identical
     to the workspace forward, and t + 1 is rejected with MX_ERR_SCRATCH before
     any launch."""
     cap = lib().mx_moe_forward_noalloc_max_bytes()
     q8 = LayerSpec(1024, 512, 64, 4, GgmlDType.Q8_0, GgmlDType.Q8_0, shared=False)
-    for spec, seed, want_max in ((CONFIGS["C2"]["spec"], 1307, 57), (q8, 1308, 540)):
+    for spec, seed, want_max in ((CONFIGS["C2"]["spec"], 1307, 57), (q8, 1308, 510)):
         cfg = f"{spec.gate_dt.name}/{spec.hidden}"
         ts = (32,)
         blk = build_layer(spec, seed=seed).block
