@@ -389,6 +389,28 @@ def bench_lm_head(args):
             "hbm_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": int(nbytes)}
 
 
+def t_sweep(ts, replays=20):
+    """C1-shaped layers (C2's routing spread) at other block sizes: 4 distinct
+    layers replayed as one graph per t, µs per layer forward.  Which kernels run
+    depends on t: the 16-pair MFMA tiles up to 2560 (token, slot) pairs, the
+    grouped GEMM beyond."""
+    import torch
+    from maxuna_amd.synth import CONFIGS, build_layer, make_x
+
+    spec = CONFIGS["C2"]["spec"]
+    layers = [build_layer(spec, seed=1002, layer=i) for i in range(4)]
+    out = {}
+    for t in ts:
+        xs = [torch.from_numpy(make_x(spec, 99, t, layer=i)).cuda() for i in range(4)]
+        ys = [torch.empty_like(x) for x in xs]
+        us = graph_us(lambda: [layers[i].block.forward(xs[i], out=ys[i]) for i in range(4)], replays) / 4
+        slots = spec.top_k + 1
+        path = "tiles" if t >= 16 and t * slots <= 2560 else ("grouped GEMM" if t >= 32 else "decode")
+        log(f"t-sweep t={t}: {us:.1f} us/layer ({path})")
+        out[t] = round(us, 1)
+    return out
+
+
 def cpu_model() -> str:
     try:
         for ln in open("/proc/cpuinfo"):
@@ -466,6 +488,8 @@ def main():
                     help="only time the plain Q6_K mat-vec at the lm_head shape (profiling)")
     ap.add_argument("--library-gemm", action="store_true",
                     help="only time the vendor library's f16 GEMMs on the C3 prefill's per-expert shapes")
+    ap.add_argument("--t-sweep", type=str, default="",
+                    help="only time C1-shaped layers at these comma-separated block sizes (tokens)")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="only run N device-to-device copies of this many MB (HBM counter calibration) and exit")
     args = ap.parse_args()
@@ -483,6 +507,9 @@ def main():
         return
     if args.lm_head:
         bench_lm_head(args)
+        return
+    if args.t_sweep:
+        t_sweep([int(v) for v in args.t_sweep.split(",")])
         return
     if args.copy_probe_mb:
         # a plain copy of known size: FETCH_SIZE / WRITE_SIZE of its dispatches calibrate
