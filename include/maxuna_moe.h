@@ -149,11 +149,14 @@ mx_status mx_prepare_map0(int64_t n_expert, const uint32_t *ids, int64_t t, int6
  * Shapes as mx_mul_mv_id; `map` must come from mx_prepare_map0 with the same
  * ids, and its geometry must match (n_expert, t, top_k), else MX_ERR_SCRATCH
  * (dispatch.rs:886-896).  Supported: Q4_K, Q5_K, Q6_K, Q8_0.
- * When K is a multiple of 256 the projection runs on the prefill path's MFMA
- * GEMM over x rounded to f16 (one power-of-two scale per x row); the f16 rows
- * (t * x_per_row * (2k + 4) bytes) are stream-ordered memory from a library
- * pool per device, which keeps its peak size reserved.  Other K run the
- * fallback tiles with no temporary. */
+ * Up to 2560 (token, slot) pairs (Q4_K / Q6_K, K a multiple of 512, n_out of
+ * 32) the projection runs the 16-pair MFMA tiles of the MoE forward's verify
+ * blocks; beyond that, when K is a multiple of 256, the prefill path's MFMA
+ * GEMM; both over x rounded to f16 (one power-of-two scale per x row).  Their
+ * temporaries (the f16 rows, t * x_per_row * (2k + 4) bytes, and the tiles'
+ * pair order) are stream-ordered memory from a library pool per device, which
+ * keeps its peak size reserved.  Other K run the fallback tiles with no
+ * temporary. */
 mx_status mx_mul_mm_id_shared(const mx_expert_stack *stack, const float *x, int64_t t,
                               int64_t x_per_row, int64_t k, const uint32_t *ids,
                               int64_t ids_t, int64_t top_k, const mx_map0 *map,

@@ -1,6 +1,7 @@
 // C-ABI entry points: host-side validation (every check happens before any
 // launch, as dispatch.rs:812-847 does), then the launchers.  No exception or
 // HIP error escapes as anything but a status code + thread-local text.
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -31,6 +32,15 @@ mx_status hip_check(hipError_t e, const char *what) {
     if (e == hipSuccess) return MX_OK;
     return fail(MX_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
 }
+
+// the 16-pair MFMA tiles' upper end (MoE forward and the mm_id projections) in (token, slot) pairs: the measured crossover with the
+// grouped GEMM on C1-shaped layers (11 slots; 4 layers replayed, µs, tiles vs
+// GEMM): t = 200: 760 vs 826, 256: 864 vs 862, 300: 945 vs 900
+#ifndef MX_VMM_MAX_PAIRS
+#define MX_VMM_MAX_PAIRS 2560
+#endif
+constexpr int64_t kVmmMaxPairs = MX_VMM_MAX_PAIRS;
+static_assert(kVmmMaxPairs <= PAIR_ORDER_MAX, "the pair order covers the tiles' range");
 
 static bool supported(int dt) { return dt == kQ4_K || dt == kQ5_K || dt == kQ6_K || dt == kQ8_0; }
 static bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
@@ -216,6 +226,42 @@ mx_status pool_alloc(size_t bytes, hipStream_t s, void **out) {
 size_t mm_x16_bytes(int64_t t, int64_t x_per_row, int64_t k) {
     return (((size_t)(t * x_per_row * k) * 2 + 255) & ~size_t(255)) + (size_t)(t * x_per_row) * 4;
 }
+// the tiles route: the pair order (perm, then its runs: the tiles read 16 words
+// from a run's start, which stay inside the runs table), then x's f16 rows
+size_t mm_tiles_order_bytes(int64_t pairs) { return (((size_t)pairs + 2 * ((size_t)pairs + 1)) * 4 + 255) & ~size_t(255); }
+size_t mm_tiles_bytes(int64_t t, int64_t top_k, int64_t x_per_row, int64_t k) {
+    return mm_tiles_order_bytes(t * top_k) + mm_x16_bytes(t, x_per_row, k);
+}
+// A few pairs per expert: the 16-pair MFMA tiles of the verify blocks (each
+// touched expert's weights streamed once) instead of 128-pair GEMM m-tiles
+bool mm_on_tiles(const mx_expert_stack *st, const StackGeom &g, int64_t t, int64_t top_k) {
+    return (st->dtype == kQ4_K || st->dtype == kQ6_K) && st->k % 512 == 0 && st->n_out % 32 == 0 &&
+           t * top_k <= kVmmMaxPairs && st->n_expert <= 1024 && (st->dtype != kQ4_K || g.row_bytes % 16 == 0) &&
+           st->n_out * g.row_bytes < ((int64_t)1 << 31) && st->k * 2 < ((int64_t)1 << 31);
+}
+// pair order, x -> scaled f16 rows (the Q4_K tiles' K order), the plain tiles;
+// output row of pair v = token * top_k + slot is dst row v
+mx_status mm_tiles(const mx_expert_stack *st, const StackGeom &g, const float *x, int64_t t, int64_t x_per_row,
+                   const uint32_t *ids, int64_t top_k, void *tmp, float *dst, hipStream_t s) {
+    const int64_t np = t * top_k;
+    const int k = (int)st->k;
+    int32_t *perm = static_cast<int32_t *>(tmp);
+    int32_t *runs = perm + np;
+    uint8_t *xb = static_cast<uint8_t *>(tmp) + mm_tiles_order_bytes(np);
+    _Float16 *x16 = reinterpret_cast<_Float16 *>(xb);
+    float *x16s = reinterpret_cast<float *>(xb + (((size_t)(t * x_per_row * k) * 2 + 255) & ~size_t(255)));
+    MX_TRY(launch_pair_order(ids, (int)t, (int)top_k, (int)st->n_expert, (int)top_k, perm, s, runs));
+    MX_TRY(launch_to_f16_rows(x, t * x_per_row, k, nullptr, x16, x16s, s, st->dtype == kQ4_K));
+    VmmArgs a{};
+    a.w[0] = g.w;
+    a.expert_bytes = g.expert_bytes; a.row_bytes = g.row_bytes; a.sh_row_bytes = g.row_bytes;
+    a.n_expert = (int)st->n_expert; a.n_out = (int)st->n_out; a.k = k;
+    a.a = x16; a.a_scale = x16s;
+    a.a_slots = x_per_row == 1 ? (int)top_k : 1;  // A row of pair v: v / a_slots
+    a.perm = perm; a.runs = runs;
+    a.out = dst;
+    return launch_vmm(st->dtype, false, a, (int)np, s);
+}
 // the grouped GEMM of the prefill path takes a projection whose K is whole
 // super-blocks and whose operand spans fit its 32-bit offsets; the rest run the
 // fallback tiles
@@ -279,20 +325,27 @@ mx_status mx_mul_mm_id_shared(const mx_expert_stack *stack, const float *x, int6
     if (t == 0) return MX_OK;
     const hipStream_t s = (hipStream_t)stream;
     const int32_t *mp = static_cast<const int32_t *>(map->buffer);
-    if (!mm_on_gemm(stack, g, t, x_per_row)) return mm_fallback(stack, g, x, t, x_per_row, top_k, mp, dst, s);
-    // no workspace in this interface (mm_id.rs:32-39): x's f16 rows live in
-    // stream-ordered memory of the library's pool for the length of the call
+    const bool tiles = mm_on_tiles(stack, g, t, top_k);
+    if (!tiles && !mm_on_gemm(stack, g, t, x_per_row)) return mm_fallback(stack, g, x, t, x_per_row, top_k, mp, dst, s);
+    // no workspace in this interface (mm_id.rs:32-39): x's f16 rows (and the tiles'
+    // pair order) live in stream-ordered memory of the library's pool for the call
     void *tmp = nullptr;
-    MX_TRY(pool_alloc(mm_x16_bytes(t, x_per_row, stack->k), s, &tmp));
-    const mx_status rc = mm_gemm(stack, g, x, t, x_per_row, top_k, mp, tmp, dst, s);
+    MX_TRY(pool_alloc(tiles ? mm_tiles_bytes(t, top_k, x_per_row, stack->k) : mm_x16_bytes(t, x_per_row, stack->k),
+                      s, &tmp));
+    const mx_status rc = tiles ? mm_tiles(stack, g, x, t, x_per_row, ids, top_k, tmp, dst, s)
+                               : mm_gemm(stack, g, x, t, x_per_row, top_k, mp, tmp, dst, s);
     MX_HIP(hipFreeAsync(tmp, s));
     return rc;
 }
 
 size_t mx_mul_mm_id_workspace_bytes(int64_t n_expert, int64_t t, int64_t top_k, int64_t x_per_row, int64_t k) {
-    // map0, then (GEMM route) x's f16 rows and their scales
+    // map0, then x's f16 rows and their scales (GEMM route) or the pair order and
+    // the f16 rows (tiles route)
     const size_t map = (mx_map0_scratch_bytes(n_expert, t, top_k) + 255) & ~size_t(255);
-    return k > 0 && k % 256 == 0 ? map + mm_x16_bytes(t, x_per_row, k) : map;
+    size_t extra = 0;
+    if (k > 0 && k % 256 == 0) extra = mm_x16_bytes(t, x_per_row, k);
+    if (k > 0 && k % 512 == 0 && t * top_k <= kVmmMaxPairs) extra = std::max(extra, mm_tiles_bytes(t, top_k, x_per_row, k));
+    return map + extra;
 }
 
 mx_status mx_mul_mm_id(const mx_expert_stack *stack, const float *x, int64_t t, int64_t x_per_row, int64_t k,
@@ -307,12 +360,16 @@ mx_status mx_mul_mm_id(const mx_expert_stack *stack, const float *x, int64_t t, 
     if (workspace_bytes < need)
         return fail(MX_ERR_SCRATCH, "mul_mm_id: workspace of %zu bytes, need %zu", workspace_bytes, need);
     const size_t map_bytes = (mx_map0_scratch_bytes(stack->n_expert, t, top_k) + 255) & ~size_t(255);
-    MX_TRY(mx_prepare_map0(stack->n_expert, ids, t, top_k, workspace, map_bytes, stream));
     const hipStream_t s = (hipStream_t)stream;
+    const bool tiles = mm_on_tiles(stack, g, t, top_k);
+    if ((tiles || mm_on_gemm(stack, g, t, x_per_row)) && !aligned(workspace, 256))
+        return fail(MX_ERR_ALIGN, "mul_mm_id: workspace must be 256-byte aligned");
+    uint8_t *tmp = static_cast<uint8_t *>(workspace) + map_bytes;
+    if (tiles) return mm_tiles(stack, g, x, t, x_per_row, ids, top_k, tmp, dst, s);  // (no bucket map)
+    MX_TRY(mx_prepare_map0(stack->n_expert, ids, t, top_k, workspace, map_bytes, stream));
     const int32_t *mp = static_cast<const int32_t *>(workspace);
     if (!mm_on_gemm(stack, g, t, x_per_row)) return mm_fallback(stack, g, x, t, x_per_row, top_k, mp, dst, s);
-    if (!aligned(workspace, 256)) return fail(MX_ERR_ALIGN, "mul_mm_id: workspace must be 256-byte aligned");
-    return mm_gemm(stack, g, x, t, x_per_row, top_k, mp, static_cast<uint8_t *>(workspace) + map_bytes, dst, s);
+    return mm_gemm(stack, g, x, t, x_per_row, top_k, mp, tmp, dst, s);
 }
 
 mx_status mx_check_ids(const uint32_t *ids, int64_t t, int64_t top_k, int64_t n_expert, uint32_t *flags,
@@ -398,14 +455,6 @@ constexpr bool kFuseSelect = MX_FUSE_SELECT != 0;
 #define MX_VMM_MIN_T 16
 #endif
 constexpr int64_t kVmmMinT = MX_VMM_MIN_T;
-// the tiles' upper end in (token, slot) pairs: the measured crossover with the
-// grouped GEMM on C1-shaped layers (11 slots; 4 layers replayed, µs, tiles vs
-// GEMM): t = 200: 760 vs 826, 256: 864 vs 862, 300: 945 vs 900
-#ifndef MX_VMM_MAX_PAIRS
-#define MX_VMM_MAX_PAIRS 2560
-#endif
-constexpr int64_t kVmmMaxPairs = MX_VMM_MAX_PAIRS;
-static_assert(kVmmMaxPairs <= PAIR_ORDER_MAX, "the pair order covers the tiles' range");
 
 struct Ws {
     uint8_t *base;
